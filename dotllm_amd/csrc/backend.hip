@@ -1,0 +1,1050 @@
+// backend.hip -- host side of libllmdot_hip.so: the C ABI declared in
+// include/llmdot_hip.h.
+//
+//   * llmdot_hip_ctx   : one device + one HIP stream + the persistent weight
+//                        table keyed like the reference's weightKey cache
+//                        (src/Llmdot.Metal/MetalBackend.cs:92-100).
+//   * op-level calls   : IComputeBackend members (src/Llmdot.Core/Inference/
+//                        Backends/IComputeBackend.cs:7-29) over host spans.
+//   * llmdot_hip_model : the decode step of InferenceEngine (IE:134-196) with
+//                        weights, KV cache and activations resident in HBM.
+//                        One step = embed + per layer [QKV GEMV(+RmsNorm),
+//                        attention (2 kernels), O GEMV(+residual), gate/up
+//                        GEMV(+RmsNorm, SwiGLU), down GEMV(+residual)] + LM
+//                        head GEMV(+final RmsNorm, argmax).  The step reads the
+//                        token and position from device memory and the head
+//                        writes the next token and position back, so a single
+//                        captured HIP graph is replayed for every token and
+//                        the greedy loop never returns to the host.
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/llmdot_hip.h"
+#include "common.h"
+#include "kernels.h"
+
+using namespace llmdot;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIPCHK(expr)                                                                              \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return fail(LLMDOT_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));       \
+    } while (0)
+
+struct Weight {
+    uint32_t type = 0;
+    int64_t rows = 0, cols = 0;
+    size_t nbytes = 0;
+    uint8_t* dev = nullptr;
+};
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t n) {
+        if (n <= cap) return hipSuccess;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        hipError_t e = hipMalloc(&p, n + WEIGHT_PAD);
+        if (e == hipSuccess) cap = n;
+        return e;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+bool env_flag(const char* name) {
+    const char* v = getenv(name);
+    return v && *v && strcmp(v, "0") != 0;
+}
+
+}  // namespace
+
+struct llmdot_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::unordered_map<std::string, Weight> weights;
+    DevBuf scratch[6];
+    int32_t* am_ints = nullptr;  // [0] token_out, [1..2] counter + pad
+    float* am_val = nullptr;
+    int32_t* am_idx = nullptr;
+    int am_cap = 0;
+};
+
+namespace {
+
+int ensure_device(llmdot_hip_ctx* ctx) {
+    HIPCHK(hipSetDevice(ctx->device));
+    return 0;
+}
+
+int ensure_argmax(llmdot_hip_ctx* ctx, int n) {
+    if (!ctx->am_ints) {
+        HIPCHK(hipMalloc(&ctx->am_ints, 64));
+        HIPCHK(hipMemset(ctx->am_ints, 0, 64));
+    }
+    if (n > ctx->am_cap) {
+        if (ctx->am_val) (void)hipFree(ctx->am_val);
+        if (ctx->am_idx) (void)hipFree(ctx->am_idx);
+        ctx->am_val = nullptr; ctx->am_idx = nullptr; ctx->am_cap = 0;
+        HIPCHK(hipMalloc(&ctx->am_val, sizeof(float) * (size_t)n));
+        HIPCHK(hipMalloc(&ctx->am_idx, sizeof(int32_t) * (size_t)n));
+        ctx->am_cap = n;
+    }
+    return 0;
+}
+
+int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const void* bytes, size_t nbytes,
+           int64_t rows, int64_t cols, const Weight** out) {
+    if (block_elems(type) == 0) return fail(LLMDOT_E_UNSUPPORTED, "unsupported ggml type " + std::to_string(type));
+    if (rows <= 0 || cols <= 0 || cols % block_elems(type) != 0)
+        return fail(LLMDOT_E_INVALID, "bad shape for weight '" + key + "'");
+    const int64_t need = rows * byte_count(type, cols);
+    if ((int64_t)nbytes < need)
+        return fail(LLMDOT_E_INVALID, "weight '" + key + "' has " + std::to_string(nbytes) + " bytes, needs " +
+                                          std::to_string(need));
+    auto it = ctx->weights.find(key);
+    if (it != ctx->weights.end()) {
+        (void)hipFree(it->second.dev);
+        ctx->weights.erase(it);
+    }
+    Weight w;
+    w.type = type; w.rows = rows; w.cols = cols; w.nbytes = (size_t)need;
+    HIPCHK(hipMalloc(&w.dev, (size_t)need + WEIGHT_PAD));
+    HIPCHK(hipMemcpy(w.dev, bytes, (size_t)need, hipMemcpyHostToDevice));
+    HIPCHK(hipMemset(w.dev + need, 0, WEIGHT_PAD));
+    auto& slot = ctx->weights[key];
+    slot = w;
+    if (out) *out = &slot;
+    return 0;
+}
+
+}  // namespace
+
+// =============================================================== context ==
+
+extern "C" const char* llmdot_hip_last_error(void) { return g_err.c_str(); }
+
+extern "C" int32_t llmdot_hip_device_count(int32_t* count) {
+    if (!count) return fail(LLMDOT_E_INVALID, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) { *count = 0; return fail(LLMDOT_E_DEVICE, std::string("hipGetDeviceCount: ") + hipGetErrorString(e)); }
+    *count = n;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_create(int32_t device, llmdot_hip_ctx** out) {
+    if (!out) return fail(LLMDOT_E_INVALID, "null out");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(LLMDOT_E_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n) return fail(LLMDOT_E_INVALID, "device index out of range");
+    auto* ctx = new llmdot_hip_ctx();
+    ctx->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(LLMDOT_E_DEVICE, std::string("stream creation failed: ") + hipGetErrorString(e));
+    }
+    *out = ctx;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
+    if (!ctx) return 0;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->weights) (void)hipFree(kv.second.dev);
+    for (auto& b : ctx->scratch) b.release();
+    if (ctx->am_ints) (void)hipFree(ctx->am_ints);
+    if (ctx->am_val) (void)hipFree(ctx->am_val);
+    if (ctx->am_idx) (void)hipFree(ctx->am_idx);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_get_device_info(llmdot_hip_ctx* ctx, llmdot_hip_device_info* out) {
+    if (!ctx || !out) return fail(LLMDOT_E_INVALID, "null argument");
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, ctx->device));
+    memset(out, 0, sizeof *out);
+    snprintf(out->name, sizeof out->name, "%s", p.name);
+    snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+    out->compute_units = p.multiProcessorCount;
+    out->clock_mhz = p.clockRate / 1000;
+    out->hbm_bytes = (uint64_t)p.totalGlobalMem;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_upload_weight(llmdot_hip_ctx* ctx, const char* key, uint32_t type, const void* bytes,
+                                            size_t nbytes, int64_t rows, int64_t cols) {
+    if (!ctx || !key || !bytes) return fail(LLMDOT_E_INVALID, "null argument");
+    if (int rc = ensure_device(ctx)) return rc;
+    return upload(ctx, key, type, bytes, nbytes, rows, cols, nullptr);
+}
+
+extern "C" int32_t llmdot_hip_release_weight(llmdot_hip_ctx* ctx, const char* key) {
+    if (!ctx || !key) return fail(LLMDOT_E_INVALID, "null argument");
+    auto it = ctx->weights.find(key);
+    if (it == ctx->weights.end()) return fail(LLMDOT_E_NOT_FOUND, std::string("Tensor '") + key + "' not found.");
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(it->second.dev);
+    ctx->weights.erase(it);
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_has_weight(llmdot_hip_ctx* ctx, const char* key, int32_t* present) {
+    if (!ctx || !key || !present) return fail(LLMDOT_E_INVALID, "null argument");
+    *present = ctx->weights.count(key) ? 1 : 0;
+    return 0;
+}
+
+// ============================================================== op level ==
+
+namespace {
+
+template <typename T>
+int stage_in(llmdot_hip_ctx* ctx, int slot, const T* host, size_t n, T** dev) {
+    HIPCHK(ctx->scratch[slot].ensure(sizeof(T) * (n ? n : 1)));
+    *dev = reinterpret_cast<T*>(ctx->scratch[slot].p);
+    if (n && host) HIPCHK(hipMemcpyAsync(*dev, host, sizeof(T) * n, hipMemcpyHostToDevice, ctx->stream));
+    return 0;
+}
+
+int copy_out(llmdot_hip_ctx* ctx, void* host, const void* dev, size_t nbytes) {
+    HIPCHK(hipMemcpyAsync(host, dev, nbytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int matmul_common(llmdot_hip_ctx* ctx, const float* a, const void* b, float* result, int64_t result_len,
+                  uint32_t type, int a_cols, int b_cols, const char* weight_key) {
+    if (!ctx || !a || !result) return fail(LLMDOT_E_INVALID, "null argument");
+    if (a_cols <= 0 || b_cols <= 0 || result_len < b_cols || result_len % b_cols != 0)
+        return fail(LLMDOT_E_INVALID, "bad MatMul shape");
+    if (!gemv_supported(type)) return fail(LLMDOT_E_UNSUPPORTED, "MatMul: unsupported weight type " + std::to_string(type));
+    if (a_cols % block_elems(type) != 0 || (type != GGML_F32 && type != GGML_F16 && a_cols % (type == GGML_Q6_K ? 64 : 32) != 0))
+        return fail(LLMDOT_E_UNSUPPORTED, "MatMul: width not a multiple of the block size");
+    if (int rc = ensure_device(ctx)) return rc;
+    const Weight* w = nullptr;
+    Weight tmp;
+    if (weight_key) {
+        auto it = ctx->weights.find(weight_key);
+        if (it != ctx->weights.end()) {
+            w = &it->second;
+            if (w->type != type || w->cols != a_cols || w->rows != b_cols)
+                return fail(LLMDOT_E_INVALID, std::string("weight '") + weight_key + "' shape/type mismatch");
+        }
+    }
+    if (!w) {
+        if (!b) return fail(LLMDOT_E_NOT_FOUND, std::string("Tensor '") + (weight_key ? weight_key : "") + "' not found.");
+        if (weight_key) {
+            if (int rc = upload(ctx, weight_key, type, b, (size_t)(b_cols * byte_count(type, a_cols)), b_cols, a_cols, &w)) return rc;
+        } else {
+            const size_t nb = (size_t)(b_cols * byte_count(type, a_cols));
+            HIPCHK(ctx->scratch[5].ensure(nb));
+            HIPCHK(hipMemcpyAsync(ctx->scratch[5].p, b, nb, hipMemcpyHostToDevice, ctx->stream));
+            HIPCHK(hipMemsetAsync((uint8_t*)ctx->scratch[5].p + nb, 0, WEIGHT_PAD, ctx->stream));
+            tmp.type = type; tmp.rows = b_cols; tmp.cols = a_cols; tmp.nbytes = nb;
+            tmp.dev = (uint8_t*)ctx->scratch[5].p;
+            w = &tmp;
+        }
+    }
+    const int64_t a_rows = result_len / b_cols;
+    float *da, *dy;
+    if (int rc = stage_in(ctx, 0, a, (size_t)(a_rows * a_cols), &da)) return rc;
+    if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)result_len, &dy)) return rc;
+    for (int64_t r = 0; r < a_rows; r++) {
+        GemvArgs ga{};
+        ga.nseg = 1;
+        ga.seg[0] = {w->dev, dy + r * b_cols, b_cols};
+        ga.cols = a_cols;
+        ga.x = da + r * a_cols;
+        HIPCHK(launch_gemv(type, PRO_NONE, EPI_STORE, ga, ctx->stream));
+    }
+    return copy_out(ctx, result, dy, sizeof(float) * (size_t)result_len);
+}
+
+}  // namespace
+
+extern "C" int32_t llmdot_hip_matmul(llmdot_hip_ctx* ctx, const float* a, const void* b, float* result,
+                                     int64_t result_len, uint32_t b_type, int32_t a_cols, int32_t b_cols,
+                                     const char* weight_key) {
+    return matmul_common(ctx, a, b, result, result_len, b_type, a_cols, b_cols, weight_key);
+}
+
+extern "C" int32_t llmdot_hip_matmul_f32(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result,
+                                         int64_t result_len, int32_t a_cols, int32_t b_cols, const char* weight_key) {
+    return matmul_common(ctx, a, b, result, result_len, GGML_F32, a_cols, b_cols, weight_key);
+}
+
+extern "C" int32_t llmdot_hip_rms_norm(llmdot_hip_ctx* ctx, const float* input, const float* weights, float* output,
+                                       int32_t n, float eps) {
+    if (!ctx || !input || !weights || !output || n <= 0) return fail(LLMDOT_E_INVALID, "bad RmsNorm arguments");
+    if (int rc = ensure_device(ctx)) return rc;
+    float *di, *dw, *dy;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &di)) return rc;
+    if (int rc = stage_in(ctx, 1, weights, (size_t)n, &dw)) return rc;
+    if (int rc = stage_in<float>(ctx, 2, nullptr, (size_t)n, &dy)) return rc;
+    HIPCHK(launch_rmsnorm(di, dw, dy, n, eps, ctx->stream));
+    return copy_out(ctx, output, dy, sizeof(float) * (size_t)n);
+}
+
+namespace {
+int rope_common(llmdot_hip_ctx* ctx, float* q, float* k, int head_dim, const std::vector<float>& cs,
+                const std::vector<float>& sn, int same) {
+    const int half = (int)cs.size();
+    if (2 * half > head_dim) return fail(LLMDOT_E_INVALID, "rotary dims exceed head_dim");
+    float *dq, *dk = nullptr, *dc, *ds;
+    if (int rc = ensure_device(ctx)) return rc;
+    if (int rc = stage_in(ctx, 0, q, (size_t)head_dim, &dq)) return rc;
+    if (!same) { if (int rc = stage_in(ctx, 1, k, (size_t)head_dim, &dk)) return rc; }
+    if (int rc = stage_in(ctx, 2, cs.data(), cs.size(), &dc)) return rc;
+    if (int rc = stage_in(ctx, 3, sn.data(), sn.size(), &ds)) return rc;
+    HIPCHK(launch_rope(dq, same ? dq : dk, dc, ds, half, same, ctx->stream));
+    HIPCHK(hipMemcpyAsync(q, dq, sizeof(float) * (size_t)head_dim, hipMemcpyDeviceToHost, ctx->stream));
+    if (!same) HIPCHK(hipMemcpyAsync(k, dk, sizeof(float) * (size_t)head_dim, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+}  // namespace
+
+extern "C" int32_t llmdot_hip_apply_rope(llmdot_hip_ctx* ctx, float* query, float* key, int32_t head_dim, int32_t position,
+                                         const float* freq_table, int32_t half_dim, int32_t same_span) {
+    if (!ctx || !query || !freq_table || half_dim < 0 || head_dim <= 0) return fail(LLMDOT_E_INVALID, "bad ApplyRoPE arguments");
+    const int same = same_span || key == nullptr || key == query;
+    std::vector<float> cs((size_t)half_dim), sn((size_t)half_dim);
+    for (int i = 0; i < half_dim; i++) {   // TO:688-693: angles and libm cos/sin on the host, as the reference
+        float angle = (float)position * freq_table[i];
+        cs[i] = cosf(angle);
+        sn[i] = sinf(angle);
+    }
+    return rope_common(ctx, query, key, head_dim, cs, sn, same);
+}
+
+extern "C" int32_t llmdot_hip_apply_rope_base(llmdot_hip_ctx* ctx, float* query, float* key, int32_t head_dim,
+                                              int32_t position, float freq_base, int32_t rotary_dim, int32_t same_span) {
+    if (!ctx || !query || head_dim <= 0) return fail(LLMDOT_E_INVALID, "bad ApplyRoPE arguments");
+    const int same = same_span || key == nullptr || key == query;
+    const int actual = rotary_dim > 0 ? rotary_dim : head_dim;
+    const int half = actual / 2;
+    std::vector<float> cs((size_t)half), sn((size_t)half);
+    for (int i = 0; i < half; i++) {       // TO:668-674
+        float freq = 1.0f / powf(freq_base, 2.0f * (float)i / (float)actual);
+        float angle = (float)position * freq;
+        cs[i] = cosf(angle);
+        sn[i] = sinf(angle);
+    }
+    return rope_common(ctx, query, key, head_dim, cs, sn, same);
+}
+
+extern "C" int32_t llmdot_hip_softmax(llmdot_hip_ctx* ctx, float* input, int32_t n, int32_t has_softcap, float softcap) {
+    if (!ctx || (!input && n > 0) || n < 0) return fail(LLMDOT_E_INVALID, "bad Softmax arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float* dx;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    HIPCHK(launch_softmax(dx, n, has_softcap, softcap, ctx->stream));
+    return copy_out(ctx, input, dx, sizeof(float) * (size_t)n);
+}
+
+extern "C" int32_t llmdot_hip_silu(llmdot_hip_ctx* ctx, const float* input, float* result, int32_t n) {
+    if (!ctx || !input || !result || n < 0) return fail(LLMDOT_E_INVALID, "bad Silu arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float *dx, *dy;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)n, &dy)) return rc;
+    HIPCHK(launch_silu(dx, dy, n, ctx->stream));
+    return copy_out(ctx, result, dy, sizeof(float) * (size_t)n);
+}
+
+namespace {
+int binary_common(llmdot_hip_ctx* ctx, int op, const float* a, const float* b, float* result, int n) {
+    if (!ctx || !a || !b || !result || n < 0) return fail(LLMDOT_E_INVALID, "bad elementwise arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float *da, *db, *dy;
+    if (int rc = stage_in(ctx, 0, a, (size_t)n, &da)) return rc;
+    if (int rc = stage_in(ctx, 1, b, (size_t)n, &db)) return rc;
+    if (int rc = stage_in<float>(ctx, 2, nullptr, (size_t)n, &dy)) return rc;
+    HIPCHK(launch_binary(op, da, db, dy, n, ctx->stream));
+    return copy_out(ctx, result, dy, sizeof(float) * (size_t)n);
+}
+}  // namespace
+
+extern "C" int32_t llmdot_hip_add(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result, int32_t n) {
+    return binary_common(ctx, 0, a, b, result, n);
+}
+extern "C" int32_t llmdot_hip_mul(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result, int32_t n) {
+    return binary_common(ctx, 1, a, b, result, n);
+}
+extern "C" int32_t llmdot_hip_scale(llmdot_hip_ctx* ctx, const float* input, float scale, float* result, int32_t n) {
+    if (!ctx || !input || !result || n < 0) return fail(LLMDOT_E_INVALID, "bad Scale arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float *dx, *dy;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)n, &dy)) return rc;
+    HIPCHK(launch_scale(dx, scale, dy, n, ctx->stream));
+    return copy_out(ctx, result, dy, sizeof(float) * (size_t)n);
+}
+
+extern "C" int32_t llmdot_hip_dequantize(llmdot_hip_ctx* ctx, const void* src, float* dst, uint32_t type, int32_t num_rows,
+                                         int32_t row_elements) {
+    if (!ctx || !src || !dst || num_rows < 0 || row_elements <= 0) return fail(LLMDOT_E_INVALID, "bad DequantizeToFloat arguments");
+    if (block_elems(type) == 0 || type == GGML_Q4_1 || type == GGML_Q5_0 || type == GGML_Q5_1)
+        return fail(LLMDOT_E_UNSUPPORTED, "Dequantization for type " + std::to_string(type) + " not implemented.");
+    if (row_elements % block_elems(type) != 0) return fail(LLMDOT_E_INVALID, "row not a whole number of blocks");
+    if (num_rows == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    const size_t nb = (size_t)((int64_t)num_rows * byte_count(type, row_elements));
+    uint8_t* ds;
+    float* dy;
+    if (int rc = stage_in(ctx, 0, reinterpret_cast<const uint8_t*>(src), nb, &ds)) return rc;
+    if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)num_rows * row_elements, &dy)) return rc;
+    HIPCHK(launch_dequant(ds, dy, type, num_rows, row_elements, ctx->stream));
+    return copy_out(ctx, dst, dy, sizeof(float) * (size_t)num_rows * row_elements);
+}
+
+extern "C" int32_t llmdot_hip_argmax(llmdot_hip_ctx* ctx, const float* input, int32_t n, int32_t* index) {
+    if (!ctx || !input || !index || n <= 0) return fail(LLMDOT_E_INVALID, "bad ArgMax arguments");
+    if (int rc = ensure_device(ctx)) return rc;
+    if (int rc = ensure_argmax(ctx, argmax_grid(n))) return rc;
+    float* dx;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    ArgmaxState st{};
+    st.cand_val = ctx->am_val; st.cand_idx = ctx->am_idx;
+    st.token_out = ctx->am_ints; st.counter = reinterpret_cast<uint32_t*>(ctx->am_ints + 1);
+    HIPCHK(launch_argmax(dx, n, st, ctx->stream));
+    return copy_out(ctx, index, ctx->am_ints, sizeof(int32_t));
+}
+
+// ========================================================= device pointers ==
+
+extern "C" int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, void** dptr) {
+    if (!ctx || !dptr) return fail(LLMDOT_E_INVALID, "null argument");
+    if (int rc = ensure_device(ctx)) return rc;
+    hipError_t e = hipMalloc(dptr, nbytes + WEIGHT_PAD);
+    if (e != hipSuccess) return fail(LLMDOT_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    HIPCHK(hipMemset(*dptr, 0, nbytes + WEIGHT_PAD));
+    return 0;
+}
+extern "C" int32_t llmdot_hip_device_free(llmdot_hip_ctx* ctx, void* dptr) {
+    if (!ctx) return fail(LLMDOT_E_INVALID, "null ctx");
+    if (dptr) { (void)hipStreamSynchronize(ctx->stream); HIPCHK(hipFree(dptr)); }
+    return 0;
+}
+extern "C" int32_t llmdot_hip_memcpy_h2d(llmdot_hip_ctx* ctx, void* dst, const void* src, size_t nbytes) {
+    if (!ctx || !dst || !src) return fail(LLMDOT_E_INVALID, "null argument");
+    HIPCHK(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+extern "C" int32_t llmdot_hip_memcpy_d2h(llmdot_hip_ctx* ctx, void* dst, const void* src, size_t nbytes) {
+    if (!ctx || !dst || !src) return fail(LLMDOT_E_INVALID, "null argument");
+    return copy_out(ctx, dst, src, nbytes);
+}
+extern "C" int32_t llmdot_hip_synchronize(llmdot_hip_ctx* ctx) {
+    if (!ctx) return fail(LLMDOT_E_INVALID, "null ctx");
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_gemv_device(llmdot_hip_ctx* ctx, uint32_t type, const void* w_dev, const float* x_dev,
+                                          float* y_dev, int32_t rows, int32_t cols) {
+    if (!ctx || !w_dev || !x_dev || !y_dev || rows <= 0 || cols <= 0) return fail(LLMDOT_E_INVALID, "bad gemv arguments");
+    if (!gemv_supported(type)) return fail(LLMDOT_E_UNSUPPORTED, "unsupported gemv type");
+    GemvArgs ga{};
+    ga.nseg = 1;
+    ga.seg[0] = {reinterpret_cast<const uint8_t*>(w_dev), y_dev, rows};
+    ga.cols = cols;
+    ga.x = x_dev;
+    HIPCHK(launch_gemv(type, PRO_NONE, EPI_STORE, ga, ctx->stream));
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_time_gemv(llmdot_hip_ctx* ctx, uint32_t type, const void* const* w_devs, int32_t n_weights,
+                                        const float* x_dev, float* y_dev, int32_t rows, int32_t cols, int32_t iters,
+                                        float* ms) {
+    if (!ctx || !w_devs || n_weights <= 0 || iters <= 0 || !ms) return fail(LLMDOT_E_INVALID, "bad timing arguments");
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    HIPCHK(hipEventRecord(e0, ctx->stream));
+    for (int i = 0; i < iters; i++)
+        if (int rc = llmdot_hip_gemv_device(ctx, type, w_devs[i % n_weights], x_dev, y_dev, rows, cols)) return rc;
+    HIPCHK(hipEventRecord(e1, ctx->stream));
+    HIPCHK(hipEventSynchronize(e1));
+    HIPCHK(hipEventElapsedTime(ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return 0;
+}
+
+// ================================================================== model ==
+
+namespace {
+
+struct LayerW {
+    const Weight *attn_norm, *ffn_norm, *q, *k, *v, *o, *gate, *up, *down;
+    float *attn_norm_f, *ffn_norm_f;   // fp32 norm weights on the device
+};
+
+}  // namespace
+
+struct llmdot_hip_model {
+    llmdot_hip_ctx* ctx = nullptr;
+    llmdot_hip_model_desc d{};
+    std::string prefix;
+    std::vector<LayerW> L;
+    const Weight *embd = nullptr, *out = nullptr, *out_norm = nullptr;
+    float* out_norm_f = nullptr;
+    std::vector<void*> owned;          // device allocations owned by the model
+    // activations
+    float *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    // KV cache [layer][kv_head][context][head_dim]
+    uint8_t *kcache = nullptr, *vcache = nullptr;
+    size_t kv_layer_bytes = 0;
+    float *cos_tab = nullptr, *sin_tab = nullptr;
+    int rope_half = 0;
+    // attention scratch
+    float *scores = nullptr, *chunk_max = nullptr, *part_out = nullptr, *part_sum = nullptr;
+    uint32_t* attn_counters = nullptr;
+    // argmax + device-side loop state: ints[0] token, [1] pos, [2] step, [3] counter
+    int32_t* ints = nullptr;
+    int32_t* token_log = nullptr;
+    float* am_val = nullptr;
+    int32_t* am_idx = nullptr;
+    hipGraphExec_t graph = nullptr;
+    bool use_graph = true;
+    // per-kernel timing (eager mode only)
+    std::vector<hipEvent_t> ev;
+    int ev_used = 0;
+    bool timing = false;
+    double gemv_bytes_per_launch = 0;
+};
+
+namespace {
+
+int32_t* m_token(llmdot_hip_model* m) { return m->ints; }
+int32_t* m_pos(llmdot_hip_model* m) { return m->ints + 1; }
+int32_t* m_step(llmdot_hip_model* m) { return m->ints + 2; }
+
+int dalloc(llmdot_hip_model* m, size_t n, void** p) {
+    hipError_t e = hipMalloc(p, n + WEIGHT_PAD);
+    if (e != hipSuccess) return fail(LLMDOT_E_NOMEM, "device allocation of " + std::to_string(n) + " bytes failed: " + hipGetErrorString(e));
+    m->owned.push_back(*p);
+    HIPCHK(hipMemset(*p, 0, n + WEIGHT_PAD));
+    return 0;
+}
+
+const Weight* find_w(llmdot_hip_model* m, const std::string& name) {
+    auto it = m->ctx->weights.find(m->prefix + name);
+    return it == m->ctx->weights.end() ? nullptr : &it->second;
+}
+
+int need_w(llmdot_hip_model* m, const std::string& name, int64_t rows, int64_t cols, const Weight** out) {
+    const Weight* w = find_w(m, name);
+    if (!w) return fail(LLMDOT_E_NOT_FOUND, "Tensor '" + m->prefix + name + "' not found.");
+    if ((rows >= 0 && w->rows != rows) || (cols >= 0 && w->cols != cols))
+        return fail(LLMDOT_E_INVALID, "Tensor '" + name + "' has shape [" + std::to_string(w->rows) + " x " +
+                                          std::to_string(w->cols) + "], expected [" + std::to_string(rows) + " x " +
+                                          std::to_string(cols) + "]");
+    *out = w;
+    return 0;
+}
+
+// Norm weights as fp32 on the device (LoadedModel.GetDequantizedWeights, LM:63-75).
+int norm_f32(llmdot_hip_model* m, const Weight* w, int n, float** out) {
+    if (w->rows * w->cols != n) return fail(LLMDOT_E_INVALID, "norm weight has wrong size");
+    if (w->type == GGML_F32) { *out = reinterpret_cast<float*>(w->dev); return 0; }
+    void* p;
+    if (int rc = dalloc(m, sizeof(float) * (size_t)n, &p)) return rc;
+    HIPCHK(launch_dequant(w->dev, (float*)p, w->type, 1, n, m->ctx->stream));
+    *out = (float*)p;
+    return 0;
+}
+
+int check_gemv_type(const Weight* w, const std::string& name) {
+    if (!gemv_supported(w->type)) return fail(LLMDOT_E_UNSUPPORTED, "tensor " + name + ": unsupported type " + std::to_string(w->type));
+    const int ue = w->type == GGML_Q6_K ? 64 : 32;
+    if (w->cols % ue != 0) return fail(LLMDOT_E_UNSUPPORTED, "tensor " + name + ": width not a multiple of " + std::to_string(ue));
+    return 0;
+}
+
+hipError_t timed_gemv(llmdot_hip_model* m, uint32_t type, int pro, int epi, const GemvArgs& a, bool dominant) {
+    hipStream_t s = m->ctx->stream;
+    if (m->timing && dominant && m->ev_used + 2 <= (int)m->ev.size()) {
+        hipError_t e = hipEventRecord(m->ev[m->ev_used], s);
+        if (e != hipSuccess) return e;
+        e = launch_gemv(type, pro, epi, a, s);
+        if (e != hipSuccess) return e;
+        e = hipEventRecord(m->ev[m->ev_used + 1], s);
+        m->ev_used += 2;
+        return e;
+    }
+    return launch_gemv(type, pro, epi, a, s);
+}
+
+// Enqueues one decode step on the model stream (token and position on the device).
+int enqueue_step(llmdot_hip_model* m) {
+    const auto& d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int qdim = d.heads * d.head_dim, kvdim = d.kv_heads * d.head_dim;
+    HIPCHK(launch_embed(m->embd->dev, m->embd->type, d.hidden, m_token(m), m->h, s));
+    for (int l = 0; l < d.layers; l++) {
+        const LayerW& w = m->L[l];
+        // Q, K, V projections over RmsNorm(h) (IE:185-186, IE:333-353); same-type tensors share a launch.
+        const Weight* mats[3] = {w.q, w.k, w.v};
+        float* outs[3] = {m->q, m->k, m->v};
+        int rows[3] = {qdim, kvdim, kvdim};
+        bool done[3] = {false, false, false};
+        for (int i = 0; i < 3; i++) {
+            if (done[i]) continue;
+            GemvArgs ga{};
+            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.attn_norm_f; ga.eps = d.eps;
+            for (int j = i; j < 3; j++)
+                if (!done[j] && mats[j]->type == mats[i]->type) {
+                    ga.seg[ga.nseg++] = {mats[j]->dev, outs[j], rows[j]};
+                    done[j] = true;
+                }
+            HIPCHK(timed_gemv(m, mats[i]->type, PRO_RMSNORM, EPI_STORE, ga, false));
+        }
+        AttnArgs aa{};
+        aa.q = m->q; aa.k = m->k; aa.v = m->v;
+        aa.kcache = m->kcache + (size_t)l * m->kv_layer_bytes;
+        aa.vcache = m->vcache + (size_t)l * m->kv_layer_bytes;
+        aa.cos_tab = m->cos_tab; aa.sin_tab = m->sin_tab; aa.pos = m_pos(m);
+        aa.scores = m->scores; aa.chunk_max = m->chunk_max; aa.part_out = m->part_out; aa.part_sum = m->part_sum;
+        aa.counters = m->attn_counters; aa.out = m->attn;
+        aa.heads = d.heads; aa.kv_heads = d.kv_heads; aa.head_dim = d.head_dim; aa.rope_half = m->rope_half;
+        aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
+        HIPCHK(launch_attention(aa, s));
+        {   // O projection + residual (IE:444-449, IE:189)
+            GemvArgs ga{};
+            ga.nseg = 1; ga.seg[0] = {w.o->dev, m->h, d.hidden}; ga.cols = qdim; ga.x = m->attn;
+            HIPCHK(timed_gemv(m, w.o->type, PRO_NONE, EPI_ADD, ga, false));
+        }
+        {   // gate/up over RmsNorm(h), SiLU(gate) * up (IE:190, IE:463-474)
+            GemvArgs ga{};
+            ga.nseg = 2; ga.seg[0] = {w.gate->dev, m->act, d.ffn}; ga.seg[1] = {w.up->dev, m->act, d.ffn};
+            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.ffn_norm_f; ga.eps = d.eps;
+            HIPCHK(timed_gemv(m, w.gate->type, PRO_RMSNORM, EPI_SWIGLU, ga, true));
+        }
+        {   // down projection + residual (IE:475, IE:195)
+            GemvArgs ga{};
+            ga.nseg = 1; ga.seg[0] = {w.down->dev, m->h, d.hidden}; ga.cols = d.ffn; ga.x = m->act;
+            HIPCHK(timed_gemv(m, w.down->type, PRO_NONE, EPI_ADD, ga, false));
+        }
+    }
+    {   // final RmsNorm + LM head + greedy ArgMax (IE:575-602, Sampler.cs:26-27)
+        GemvArgs ga{};
+        ga.nseg = 1; ga.seg[0] = {m->out->dev, m->logits, d.vocab}; ga.cols = d.hidden; ga.x = m->h;
+        ga.norm_w = m->out_norm_f; ga.eps = d.eps;
+        ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx;
+        ga.am.counter = reinterpret_cast<uint32_t*>(m->ints + 3);
+        ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
+        ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
+        HIPCHK(timed_gemv(m, m->out->type, PRO_RMSNORM, EPI_ARGMAX, ga, false));
+    }
+    return 0;
+}
+
+int build_graph(llmdot_hip_model* m) {
+    if (!m->use_graph) return 0;
+    hipStream_t s = m->ctx->stream;
+    HIPCHK(hipStreamSynchronize(s));
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m);
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return fail(LLMDOT_E_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) { m->graph = nullptr; return fail(LLMDOT_E_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e)); }
+    return 0;
+}
+
+int run_step(llmdot_hip_model* m) {
+    if (m->graph && !m->timing) {
+        HIPCHK(hipGraphLaunch(m->graph, m->ctx->stream));
+        return 0;
+    }
+    return enqueue_step(m);
+}
+
+int set_int(llmdot_hip_model* m, int32_t* dst, int32_t v) {
+    HIPCHK(launch_set_scalar(dst, v, m->ctx->stream));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int32_t llmdot_hip_model_destroy(llmdot_hip_model* m) {
+    if (!m) return 0;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    for (auto e : m->ev) (void)hipEventDestroy(e);
+    for (void* p : m->owned) (void)hipFree(p);
+    delete m;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip_model_desc* desc, llmdot_hip_model** out) {
+    if (!ctx || !desc || !out) return fail(LLMDOT_E_INVALID, "null argument");
+    *out = nullptr;
+    const auto& d = *desc;
+    if (d.hidden <= 0 || d.layers <= 0 || d.heads <= 0 || d.kv_heads <= 0 || d.head_dim <= 0 || d.ffn <= 0 ||
+        d.vocab <= 0 || d.context <= 0 || d.heads % d.kv_heads != 0 || d.hidden % 8 != 0)
+        return fail(LLMDOT_E_INVALID, "invalid model description");
+    if (int rc = ensure_device(ctx)) return rc;
+    auto* m = new llmdot_hip_model();
+    m->ctx = ctx;
+    m->d = d;
+    m->prefix = d.key_prefix ? d.key_prefix : "";
+    m->d.key_prefix = nullptr;
+    m->use_graph = !env_flag("LLMDOT_HIP_NO_GRAPH");
+    const int qdim = d.heads * d.head_dim, kvdim = d.kv_heads * d.head_dim;
+    int rc = 0;
+    auto bail = [&](int code) { llmdot_hip_model_destroy(m); return code; };
+    if ((rc = need_w(m, "token_embd.weight", -1, d.hidden, &m->embd))) return bail(rc);
+    if (m->embd->rows < d.vocab && !find_w(m, "output.weight"))
+        return bail(fail(LLMDOT_E_INVALID, "token_embd has fewer rows than the vocabulary"));
+    const Weight* onorm = find_w(m, "output_norm.weight");
+    if (!onorm) onorm = find_w(m, "token_embd_norm.weight");
+    if (!onorm) return bail(fail(LLMDOT_E_NOT_FOUND, "Tensor 'output_norm.weight' not found."));
+    m->out_norm = onorm;
+    m->out = find_w(m, "output.weight");
+    if (!m->out) m->out = m->embd;   // tied embeddings (IE:585-589)
+    if (m->out->cols != d.hidden || m->out->rows != d.vocab)
+        return bail(fail(LLMDOT_E_INVALID, "output projection shape does not match hidden x vocab"));
+    if ((rc = check_gemv_type(m->out, "output"))) return bail(rc);
+    if (!(m->embd->type == GGML_F32 || m->embd->type == GGML_F16 || m->embd->type == GGML_BF16 ||
+          m->embd->type == GGML_Q4_0 || m->embd->type == GGML_Q8_0 || m->embd->type == GGML_Q4_K ||
+          m->embd->type == GGML_Q5_K || m->embd->type == GGML_Q6_K))
+        return bail(fail(LLMDOT_E_UNSUPPORTED, "token_embd type not supported"));
+    if ((rc = norm_f32(m, onorm, d.hidden, &m->out_norm_f))) return bail(rc);
+    m->L.resize((size_t)d.layers);
+    for (int l = 0; l < d.layers; l++) {
+        LayerW& w = m->L[l];
+        const std::string p = "blk." + std::to_string(l) + ".";
+        if ((rc = need_w(m, p + "attn_norm.weight", -1, -1, &w.attn_norm))) return bail(rc);
+        w.ffn_norm = find_w(m, p + "ffn_norm.weight");
+        if (!w.ffn_norm) w.ffn_norm = w.attn_norm;   // IE:547
+        if ((rc = need_w(m, p + "attn_q.weight", qdim, d.hidden, &w.q))) return bail(rc);
+        if ((rc = need_w(m, p + "attn_k.weight", kvdim, d.hidden, &w.k))) return bail(rc);
+        if ((rc = need_w(m, p + "attn_v.weight", kvdim, d.hidden, &w.v))) return bail(rc);
+        if ((rc = need_w(m, p + "attn_output.weight", d.hidden, qdim, &w.o))) return bail(rc);
+        if ((rc = need_w(m, p + "ffn_gate.weight", d.ffn, d.hidden, &w.gate))) return bail(rc);
+        if ((rc = need_w(m, p + "ffn_up.weight", d.ffn, d.hidden, &w.up))) return bail(rc);
+        if ((rc = need_w(m, p + "ffn_down.weight", d.hidden, d.ffn, &w.down))) return bail(rc);
+        const Weight* all[7] = {w.q, w.k, w.v, w.o, w.gate, w.up, w.down};
+        const char* nm[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+        for (int i = 0; i < 7; i++)
+            if ((rc = check_gemv_type(all[i], p + nm[i]))) return bail(rc);
+        if (w.gate->type != w.up->type) return bail(fail(LLMDOT_E_UNSUPPORTED, "ffn_gate and ffn_up must share a type"));
+        if ((rc = norm_f32(m, w.attn_norm, d.hidden, &w.attn_norm_f))) return bail(rc);
+        if ((rc = norm_f32(m, w.ffn_norm, d.hidden, &w.ffn_norm_f))) return bail(rc);
+    }
+    // RoPE tables: PrecomputeRopeFrequencies (IE:57-72) then, per position, the
+    // reference's per-call cosf/sinf of position * freq (TO:688-693).
+    const int rot = d.rope_dim > 0 ? d.rope_dim : d.head_dim;
+    m->rope_half = rot / 2;
+    if (2 * m->rope_half > d.head_dim) return bail(fail(LLMDOT_E_INVALID, "rope_dim exceeds head_dim"));
+    {
+        std::vector<float> freq((size_t)m->rope_half);
+        for (int i = 0; i < m->rope_half; i++) {
+            float f = 1.0f / powf(d.rope_base, 2.0f * (float)i / (float)rot);
+            if (d.rope_linear_factor > 1.0f) f /= d.rope_linear_factor;
+            freq[i] = f;
+        }
+        const size_t n = (size_t)d.context * (size_t)(m->rope_half > 0 ? m->rope_half : 1);
+        std::vector<float> cs(n, 1.0f), sn(n, 0.0f);
+        for (int t = 0; t < d.context; t++)
+            for (int i = 0; i < m->rope_half; i++) {
+                float angle = (float)t * freq[i];
+                cs[(size_t)t * m->rope_half + i] = cosf(angle);
+                sn[(size_t)t * m->rope_half + i] = sinf(angle);
+            }
+        void *pc, *ps;
+        if ((rc = dalloc(m, n * sizeof(float), &pc)) || (rc = dalloc(m, n * sizeof(float), &ps))) return bail(rc);
+        m->cos_tab = (float*)pc; m->sin_tab = (float*)ps;
+        if (hipMemcpy(pc, cs.data(), n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(ps, sn.data(), n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(LLMDOT_E_DEVICE, "RoPE table upload failed"));
+    }
+    void* p;
+    auto A = [&](size_t n, void** dst) { return dalloc(m, n, dst); };
+    if ((rc = A(sizeof(float) * d.hidden, &p))) return bail(rc); m->h = (float*)p;
+    if ((rc = A(sizeof(float) * qdim, &p))) return bail(rc); m->q = (float*)p;
+    if ((rc = A(sizeof(float) * kvdim, &p))) return bail(rc); m->k = (float*)p;
+    if ((rc = A(sizeof(float) * kvdim, &p))) return bail(rc); m->v = (float*)p;
+    if ((rc = A(sizeof(float) * qdim, &p))) return bail(rc); m->attn = (float*)p;
+    if ((rc = A(sizeof(float) * d.ffn, &p))) return bail(rc); m->act = (float*)p;
+    if ((rc = A(sizeof(float) * d.vocab, &p))) return bail(rc); m->logits = (float*)p;
+    const size_t elt = d.kv_fp16 ? 2 : 4;
+    m->kv_layer_bytes = (size_t)d.kv_heads * d.context * d.head_dim * elt;
+    if ((rc = A(m->kv_layer_bytes * d.layers, &p))) return bail(rc); m->kcache = (uint8_t*)p;
+    if ((rc = A(m->kv_layer_bytes * d.layers, &p))) return bail(rc); m->vcache = (uint8_t*)p;
+    const int nch = attn_max_chunks(d.heads, d.kv_heads, d.context);
+    if ((rc = A(sizeof(float) * (size_t)d.heads * d.context, &p))) return bail(rc); m->scores = (float*)p;
+    if ((rc = A(sizeof(float) * (size_t)d.heads * nch, &p))) return bail(rc); m->chunk_max = (float*)p;
+    if ((rc = A(sizeof(float) * (size_t)nch * qdim, &p))) return bail(rc); m->part_out = (float*)p;
+    if ((rc = A(sizeof(float) * (size_t)nch * d.heads, &p))) return bail(rc); m->part_sum = (float*)p;
+    if ((rc = A(sizeof(uint32_t) * (size_t)d.kv_heads, &p))) return bail(rc); m->attn_counters = (uint32_t*)p;
+    if ((rc = A(64, &p))) return bail(rc); m->ints = (int32_t*)p;
+    if ((rc = A(sizeof(int32_t) * (size_t)(d.context + 1), &p))) return bail(rc); m->token_log = (int32_t*)p;
+    {
+        GemvArgs ga{};
+        ga.nseg = 1; ga.seg[0] = {m->out->dev, m->logits, d.vocab}; ga.cols = d.hidden;
+        const int g = gemv_grid(m->out->type, EPI_ARGMAX, ga);
+        if ((rc = A(sizeof(float) * (size_t)g, &p))) return bail(rc); m->am_val = (float*)p;
+        if ((rc = A(sizeof(int32_t) * (size_t)g, &p))) return bail(rc); m->am_idx = (int32_t*)p;
+    }
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return bail(fail(LLMDOT_E_DEVICE, "synchronize failed"));
+    if ((rc = build_graph(m))) {
+        // fall back to eager launches
+        m->use_graph = false;
+        if (m->graph) { (void)hipGraphExecDestroy(m->graph); m->graph = nullptr; }
+        (void)hipGetLastError();
+    }
+    *out = m;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_model_reset(llmdot_hip_model* m) {
+    if (!m) return fail(LLMDOT_E_INVALID, "null model");
+    if (int rc = set_int(m, m_pos(m), 0)) return rc;
+    if (int rc = set_int(m, m_step(m), 0)) return rc;
+    HIPCHK(hipStreamSynchronize(m->ctx->stream));
+    return 0;
+}
+
+namespace {
+int check_token(llmdot_hip_model* m, int32_t token) {
+    if (token < 0 || token >= m->embd->rows) return fail(LLMDOT_E_RANGE, "token id out of range");
+    return 0;
+}
+int check_pos(llmdot_hip_model* m, int32_t pos) {
+    if (pos < 0 || pos >= m->d.context) return fail(LLMDOT_E_RANGE, "position outside the KV cache");
+    return 0;
+}
+int fetch_outputs(llmdot_hip_model* m, float* logits, int32_t* am) {
+    hipStream_t s = m->ctx->stream;
+    if (logits) HIPCHK(hipMemcpyAsync(logits, m->logits, sizeof(float) * (size_t)m->d.vocab, hipMemcpyDeviceToHost, s));
+    if (am) HIPCHK(hipMemcpyAsync(am, m_token(m), sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    HIPCHK(hipStreamSynchronize(s));
+    return 0;
+}
+}  // namespace
+
+extern "C" int32_t llmdot_hip_decode_step(llmdot_hip_model* m, int32_t token, int32_t position, float* logits, int32_t* am) {
+    if (!m) return fail(LLMDOT_E_INVALID, "null model");
+    if (int rc = check_token(m, token)) return rc;
+    if (int rc = check_pos(m, position)) return rc;
+    if (int rc = set_int(m, m_token(m), token)) return rc;
+    if (int rc = set_int(m, m_pos(m), position)) return rc;
+    if (int rc = run_step(m)) return rc;
+    return fetch_outputs(m, logits, am);
+}
+
+extern "C" int32_t llmdot_hip_prefill(llmdot_hip_model* m, const int32_t* tokens, int32_t n, int32_t pos0, float* logits,
+                                      int32_t* am) {
+    if (!m || (!tokens && n > 0) || n < 0) return fail(LLMDOT_E_INVALID, "bad prefill arguments");
+    if (n == 0) return 0;
+    if (int rc = check_pos(m, pos0)) return rc;
+    if (int rc = check_pos(m, pos0 + n - 1)) return rc;
+    for (int i = 0; i < n; i++)
+        if (int rc = check_token(m, tokens[i])) return rc;
+    if (int rc = set_int(m, m_pos(m), pos0)) return rc;
+    for (int i = 0; i < n; i++) {
+        if (int rc = set_int(m, m_token(m), tokens[i])) return rc;
+        if (int rc = run_step(m)) return rc;
+    }
+    return fetch_outputs(m, logits, am);
+}
+
+extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
+                                       int32_t eos, int32_t* tokens_out, int32_t* n_out, float* logits_out) {
+    if (!m || (!prompt && n_prompt > 0) || n_prompt < 0 || max_tokens < 0 || (!tokens_out && max_tokens > 0) || !n_out)
+        return fail(LLMDOT_E_INVALID, "bad Generate arguments");
+    *n_out = 0;
+    const auto& d = m->d;
+    std::vector<int32_t> pr(prompt, prompt + n_prompt);
+    if (pr.empty()) pr.push_back(d.bos > 0 ? d.bos : 0);   // IE:90-95
+    const int np = (int)pr.size();
+    for (int t : pr)
+        if (int rc = check_token(m, t)) return rc;
+    if (np > d.context) return fail(LLMDOT_E_RANGE, "prompt longer than the KV cache");
+    if (max_tokens == 0) return 0;
+    // Token g (0-based) is sampled after position np-1+g; producing it needs
+    // np + g steps, and positions stop at context - 1.
+    const int fit = d.context - np + 1;
+    const int produce = max_tokens < fit ? max_tokens : fit;
+    hipStream_t s = m->ctx->stream;
+    if (int rc = set_int(m, m_pos(m), 0)) return rc;   // KvCache.Reset (IE:79)
+    for (int i = 0; i < np; i++) {
+        if (i == np - 1)
+            if (int rc = set_int(m, m_step(m), 0)) return rc;
+        if (int rc = set_int(m, m_token(m), pr[i])) return rc;
+        if (int rc = run_step(m)) return rc;
+    }
+    if (logits_out) HIPCHK(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
+    for (int g = 1; g < produce; g++) {
+        if (int rc = run_step(m)) return rc;   // consumes the token the previous head wrote
+        if (logits_out)
+            HIPCHK(hipMemcpyAsync(logits_out + (size_t)g * d.vocab, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
+    }
+    HIPCHK(hipMemcpyAsync(tokens_out, m->token_log, sizeof(int32_t) * (size_t)produce, hipMemcpyDeviceToHost, s));
+    HIPCHK(hipStreamSynchronize(s));
+    int n = produce;
+    if (eos >= 0)
+        for (int i = 0; i < produce; i++)
+            if (tokens_out[i] == eos) { n = i + 1; break; }   // IE:112-115
+    *n_out = n;
+    if (produce < max_tokens && n == produce)
+        return fail(LLMDOT_E_RANGE, "generation reached the end of the KV cache");
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_kv_read(llmdot_hip_model* m, int32_t layer, int32_t position, float* k, float* v) {
+    if (!m || !k || !v) return fail(LLMDOT_E_INVALID, "null argument");
+    if (layer < 0 || layer >= m->d.layers) return fail(LLMDOT_E_RANGE, "layer out of range");
+    if (int rc = check_pos(m, position)) return rc;
+    const auto& d = m->d;
+    const size_t elt = d.kv_fp16 ? 2 : 4;
+    std::vector<uint8_t> kb((size_t)d.head_dim * elt), vb((size_t)d.head_dim * elt);
+    HIPCHK(hipStreamSynchronize(m->ctx->stream));
+    for (int h = 0; h < d.kv_heads; h++) {
+        const size_t off = (size_t)layer * m->kv_layer_bytes + (((size_t)h * d.context + position) * d.head_dim) * elt;
+        HIPCHK(hipMemcpy(kb.data(), m->kcache + off, kb.size(), hipMemcpyDeviceToHost));
+        HIPCHK(hipMemcpy(vb.data(), m->vcache + off, vb.size(), hipMemcpyDeviceToHost));
+        for (int i = 0; i < d.head_dim; i++) {
+            if (d.kv_fp16) {
+                _Float16 hk, hv;
+                memcpy(&hk, kb.data() + 2 * i, 2);
+                memcpy(&hv, vb.data() + 2 * i, 2);
+                k[h * d.head_dim + i] = (float)hk;
+                v[h * d.head_dim + i] = (float)hv;
+            } else {
+                memcpy(&k[h * d.head_dim + i], kb.data() + 4 * i, 4);
+                memcpy(&v[h * d.head_dim + i], vb.data() + 4 * i, 4);
+            }
+        }
+    }
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_model_step_bytes(llmdot_hip_model* m, int32_t position, double* bytes) {
+    if (!m || !bytes) return fail(LLMDOT_E_INVALID, "null argument");
+    const auto& d = m->d;
+    double b = 0;
+    for (const auto& w : m->L) {
+        const Weight* all[7] = {w.q, w.k, w.v, w.o, w.gate, w.up, w.down};
+        for (auto* x : all) b += (double)x->nbytes;
+        b += (double)w.attn_norm->nbytes + (w.ffn_norm != w.attn_norm ? (double)w.ffn_norm->nbytes : 0.0);
+    }
+    b += (double)m->out->nbytes + (double)m->out_norm->nbytes;
+    b += (double)byte_count(m->embd->type, d.hidden);
+    const double elt = d.kv_fp16 ? 2.0 : 4.0;
+    b += (double)d.layers * 2.0 * (double)(position + 1) * (double)(d.kv_heads * d.head_dim) * elt;
+    *bytes = b;
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* m, int32_t n, uint64_t seed) {
+    if (!m) return fail(LLMDOT_E_INVALID, "null model");
+    if (n < 0 || n > m->d.context) return fail(LLMDOT_E_RANGE, "fill length outside the KV cache");
+    const size_t elt = m->d.kv_fp16 ? 2 : 4;
+    const size_t count = m->kv_layer_bytes * m->d.layers / elt;
+    HIPCHK(launch_fill_random_half(m->kcache, count, seed, m->d.kv_fp16, m->ctx->stream));
+    HIPCHK(launch_fill_random_half(m->vcache, count, seed ^ 0x5DEECE66Dull, m->d.kv_fp16, m->ctx->stream));
+    HIPCHK(hipStreamSynchronize(m->ctx->stream));
+    return 0;
+}
+
+extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t first_token, int32_t position, int32_t steps,
+                                                int32_t per_kernel, llmdot_hip_step_timing* out) {
+    if (!m || !out || steps <= 0) return fail(LLMDOT_E_INVALID, "bad timing arguments");
+    if (int rc = check_token(m, first_token)) return rc;
+    if (int rc = check_pos(m, position)) return rc;
+    if (position + steps > m->d.context) return fail(LLMDOT_E_RANGE, "timed steps run past the KV cache");
+    memset(out, 0, sizeof *out);
+    hipStream_t s = m->ctx->stream;
+    if (int rc = set_int(m, m_token(m), first_token)) return rc;
+    if (int rc = set_int(m, m_pos(m), position)) return rc;
+    if (int rc = set_int(m, m_step(m), 0)) return rc;
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    if (per_kernel) {
+        const int need = 2 * m->d.layers;
+        while ((int)m->ev.size() < need) {
+            hipEvent_t e;
+            HIPCHK(hipEventCreate(&e));
+            m->ev.push_back(e);
+        }
+        m->timing = true;
+    }
+    double gemv_ms = 0;
+    int launches = 0;
+    HIPCHK(hipStreamSynchronize(s));
+    HIPCHK(hipEventRecord(e0, s));
+    for (int i = 0; i < steps; i++) {
+        m->ev_used = 0;
+        int rc = run_step(m);
+        if (rc) { m->timing = false; return rc; }
+        if (per_kernel) {
+            HIPCHK(hipStreamSynchronize(s));
+            for (int j = 0; j + 1 < m->ev_used; j += 2) {
+                float ms = 0;
+                HIPCHK(hipEventElapsedTime(&ms, m->ev[j], m->ev[j + 1]));
+                gemv_ms += ms;
+                launches++;
+            }
+        }
+    }
+    HIPCHK(hipEventRecord(e1, s));
+    HIPCHK(hipEventSynchronize(e1));
+    m->timing = false;
+    float total = 0;
+    HIPCHK(hipEventElapsedTime(&total, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    out->total_ms = total;
+    out->gemv_ms = (float)gemv_ms;
+    out->gemv_launches = launches;
+    if (per_kernel && !m->L.empty()) {
+        const LayerW& w = m->L[0];
+        out->gemv_bytes = (double)launches * ((double)w.gate->nbytes + (double)w.up->nbytes +
+                                              4.0 * (2.0 * m->d.hidden + (double)m->d.ffn));
+    }
+    return 0;
+}

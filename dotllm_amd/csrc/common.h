@@ -1,0 +1,122 @@
+// common.h -- shared definitions for the llmdot HIP backend (gfx950 / MI355X).
+//
+// Weight tensors stay in HBM in their native GGUF block layout, row-major by
+// output row: row r of a [rows x cols] tensor is ByteCount(type, cols) bytes
+// starting at r * ByteCount(type, cols) (src/Llmdot.Core/Tensors/TensorSize.cs:7-24).
+// Every device allocation that holds weights is padded by WEIGHT_PAD bytes so
+// that the realigning dword loads below may read up to 8 bytes past a tensor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmdot {
+
+// GgmlType (src/Llmdot.Core/Loading/GgmlType.cs:3-28).
+enum GgmlType : uint32_t {
+    GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2, GGML_Q4_1 = 3, GGML_Q5_0 = 6, GGML_Q5_1 = 7,
+    GGML_Q8_0 = 8, GGML_Q8_1 = 9, GGML_Q2_K = 10, GGML_Q3_K = 11, GGML_Q4_K = 12,
+    GGML_Q5_K = 13, GGML_Q6_K = 14, GGML_BF16 = 25
+};
+
+constexpr size_t WEIGHT_PAD = 256;
+
+// Block geometry (elements per block, bytes per block); 0 = not supported.
+__host__ __device__ inline constexpr int block_elems(uint32_t t) {
+    return t == GGML_F32 || t == GGML_F16 || t == GGML_BF16 ? 1
+         : t == GGML_Q4_0 || t == GGML_Q4_1 || t == GGML_Q5_0 || t == GGML_Q5_1 || t == GGML_Q8_0 ? 32
+         : t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K ? 256 : 0;
+}
+__host__ __device__ inline constexpr int block_bytes(uint32_t t) {
+    return t == GGML_F32 ? 4 : t == GGML_F16 || t == GGML_BF16 ? 2
+         : t == GGML_Q4_0 ? 18 : t == GGML_Q4_1 ? 20 : t == GGML_Q5_0 ? 22 : t == GGML_Q5_1 ? 24
+         : t == GGML_Q8_0 ? 34 : t == GGML_Q4_K ? 144 : t == GGML_Q5_K ? 176 : t == GGML_Q6_K ? 210 : 0;
+}
+// TensorSize.ByteCount (TensorSize.cs:7-24); -1 when unsupported.
+inline int64_t byte_count(uint32_t t, int64_t n) {
+    int be = block_elems(t), bb = block_bytes(t);
+    if (!be) return -1;
+    return n / be * bb;
+}
+
+// ---- device helpers -------------------------------------------------------
+
+// Bit pattern -> float for fp16 exactly as HalfHelper.HalfToFloat (HH:7-34),
+// including the canonical NaN it returns for any NaN payload.
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    uint32_t sign = (h >> 15) & 1u, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign << 31;
+        } else {
+            // subnormal: normalise; value = m * 2^-24
+            int sh = __builtin_clz(m) - 21;        // shifts until bit 10 is set
+            uint32_t nm = (m << sh) & 0x3FFu;
+            bits = (sign << 31) | ((uint32_t)(127 - 14 - sh) << 23) | (nm << 13);
+        }
+    } else if (e == 31) {
+        bits = m == 0 ? ((sign << 31) | 0x7F800000u) : 0xFFC00000u;
+    } else {
+        bits = (sign << 31) | ((e - 15 + 127) << 23) | (m << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// 16 bytes from a 4-byte-aligned address (one global_load_dwordx4).
+struct __attribute__((aligned(4))) u32x4 { uint32_t x, y, z, w; };
+__device__ __forceinline__ u32x4 ld16_a4(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ uint32_t ld4_a4(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// n*4 bytes starting at a 2-byte-aligned address p, realigned with v_alignbyte:
+// loads n+1 dwords from p & ~3 (may read up to 2 bytes past p + 4n).
+template <int N>
+__device__ __forceinline__ void ld_realign(const uint8_t* p, uint32_t* out) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = (uint32_t)(a & 3u);
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i + 4 <= N + 1; i += 4) {
+        u32x4 v = ld16_a4(base + 4 * i);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = ((N + 1) / 4) * 4; i < N + 1; i++) w[i] = ld4_a4(base + 4 * i);
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// One lane of ExpApproxVector (src/Llmdot.Core/Tensors/Numeric/VectorMath.cs:137-166),
+// bit-exact: every operation is a separately rounded fp32 op (no contraction).
+__device__ __forceinline__ float exp_approx(float x) {
+    float c = x > -87.3f ? x : -87.3f;
+    c = c < 88.4f ? c : 88.4f;
+    int k = (int)__fadd_rn(__fmul_rn(c, 1.4426950408889634f), 0.5f);   // truncates
+    float kf = (float)k;
+    float y = __fsub_rn(__fsub_rn(c, __fmul_rn(kf, 0.693145751953125f)), __fmul_rn(kf, 1.42860677e-6f));
+    float cc = __fmul_rn(__fmul_rn(y, y), 0.5f);
+    float cy = __fmul_rn(cc, y);
+    float pade = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(1.0f, y), cc), __fmul_rn(cy, 0.3333333f)),
+                           __fmul_rn(__fmul_rn(cy, y), 0.2f));
+    float r = __fmul_rn(pade, __uint_as_float((uint32_t)(k + 127) << 23));
+    if (x < -87.3f) r = 0.0f;
+    if (x > 88.4f) r = __uint_as_float(0x7F800000u);
+    return r;
+}
+
+// Vector lanes of VectorMath.SiluInPlace (VM:118-135): x / (1 + ExpApprox(-x)).
+__device__ __forceinline__ float silu_ref(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, exp_approx(-x))); }
+
+}  // namespace llmdot

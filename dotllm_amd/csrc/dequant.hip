@@ -1,0 +1,109 @@
+// dequant.hip -- bit-exact dequantisation of the reference's block formats.
+//
+// Every element is produced with the same separately rounded fp32 operations,
+// in the same order, as src/Llmdot.Core/Tensors/Dequantize/{DequantizeK,
+// DequantizeBlock}.cs (no FMA contraction: __fmul_rn/__fsub_rn/__fadd_rn).
+#include "common.h"
+#include "kernels.h"
+
+namespace llmdot {
+
+__device__ __forceinline__ float h2f_at(const uint8_t* p) { return half_bits_to_float(p[0] | (p[1] << 8)); }
+
+// DequantizeK.Extract6Bit (DK:189-199).
+__device__ __forceinline__ int extract6(const uint8_t* src, int bit) {
+    int byteIdx = bit >> 3, sh = bit & 7;
+    if (sh <= 2) return (src[byteIdx] >> sh) & 0x3F;
+    return ((src[byteIdx] >> sh) | (src[byteIdx + 1] << (8 - sh))) & 0x3F;
+}
+
+// Element i (0-based within the row) of one row of `type` blocks.
+__device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
+    switch (type) {
+    case GGML_F32: return reinterpret_cast<const float*>(row)[i];
+    case GGML_F16: return h2f_at(row + 2 * i);
+    case GGML_BF16: return __uint_as_float(((uint32_t)row[2 * i + 1] << 24) | ((uint32_t)row[2 * i] << 16));
+    case GGML_Q4_0: {  // DB:7-34
+        const uint8_t* b = row + (i >> 5) * 18;
+        int j = i & 31;
+        float d = h2f_at(b);
+        int qs = b[2 + (j & 15)];
+        int q = j < 16 ? (qs & 0x0F) : ((qs >> 4) & 0x0F);
+        return __fmul_rn((float)(q - 8), d);
+    }
+    case GGML_Q8_0: {  // DB:36-59
+        const uint8_t* b = row + (i >> 5) * 34;
+        return __fmul_rn((float)(int8_t)b[2 + (i & 31)], h2f_at(b));
+    }
+    case GGML_Q4_K: {  // DK:76-106
+        const uint8_t* b = row + (i >> 8) * 144;
+        int j = i & 255, g = j >> 5;
+        float d = h2f_at(b), dmin = h2f_at(b + 2);
+        int sc = extract6(b + 4, g * 12), mi = extract6(b + 4, g * 12 + 6);
+        int q = (b[16 + (j >> 1)] >> ((j & 1) * 4)) & 0xF;
+        return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)(q - 8)), __fmul_rn(dmin, (float)mi));
+    }
+    case GGML_Q5_K: {  // DK:108-140
+        const uint8_t* b = row + (i >> 8) * 176;
+        int j = i & 255, g = j >> 5;
+        float d = h2f_at(b), dmin = h2f_at(b + 2);
+        int sc = extract6(b + 4, g * 12), mi = extract6(b + 4, g * 12 + 6);
+        int ql = (b[48 + (j >> 1)] >> ((j & 1) * 4)) & 0xF;
+        int qh = (b[16 + (j >> 3)] >> (j & 7)) & 0x1;
+        int q5 = ql + (qh << 4);
+        return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)(q5 - 16)), __fmul_rn(dmin, (float)mi));
+    }
+    case GGML_Q6_K: {  // DK:142-187
+        const uint8_t* b = row + (i >> 8) * 210;
+        int j = i & 255, n = j & 128, r = j & 127, t = r >> 5, l = r & 31;
+        float d = h2f_at(b + 208);
+        const uint8_t* ql = b + n / 2;
+        const uint8_t* qh = b + 128 + n / 4;
+        int lo = (t & 1) ? ql[l + 32] : ql[l];
+        int nib = (t & 2) ? (lo >> 4) : (lo & 0xF);
+        int q = (nib | (((qh[l] >> (2 * t)) & 3) << 4)) - 32;
+        int sc = (int8_t)b[192 + n / 16 + (l >> 4) + 2 * t];
+        return __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+    }
+    default: return 0.0f;
+    }
+}
+
+__global__ void dequant_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst, uint32_t type,
+                               int num_rows, int row_elems, int64_t row_bytes) {
+    int64_t n = (int64_t)num_rows * row_elems;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = e / row_elems;
+        int i = (int)(e - r * row_elems);
+        dst[e] = deq_elem(type, src + r * row_bytes, i);
+    }
+}
+
+__global__ void embed_kernel(const uint8_t* __restrict__ table, uint32_t type, int hidden, int64_t row_bytes,
+                             const int32_t* __restrict__ token, float* __restrict__ out) {
+    int tok = *token;
+    const uint8_t* row = table + (int64_t)tok * row_bytes;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
+        out[i] = deq_elem(type, row, i);
+}
+
+hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num_rows, int row_elems,
+                          hipStream_t s) {
+    int64_t rb = byte_count(type, row_elems);
+    int64_t n = (int64_t)num_rows * row_elems;
+    if (n <= 0) return hipSuccess;
+    int grid = (int)((n + 255) / 256);
+    if (grid > 65536) grid = 65536;
+    dequant_kernel<<<grid, 256, 0, s>>>(src, dst, type, num_rows, row_elems, rb);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const int32_t* token_dev,
+                        float* out, hipStream_t s) {
+    int64_t rb = byte_count(type, hidden);
+    int grid = (hidden + 255) / 256;
+    embed_kernel<<<grid, 256, 0, s>>>(table, type, hidden, rb, token_dev, out);
+    return hipGetLastError();
+}
+
+}  // namespace llmdot

@@ -1,0 +1,93 @@
+// kernels.h -- host-side launchers for the HIP kernels (all asynchronous on `s`).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmdot {
+
+// ---- dequant.hip ----
+// Bit-exact TensorOps.DequantizeToFloat (TO:18-56) of num_rows rows.
+hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num_rows, int row_elems,
+                          hipStream_t s);
+// Embedding row (InferenceEngine.GetEmbedding, IE:148-156): row *token_dev of
+// the [vocab][hidden] table, bit-exact, into out.  The token id is read on the
+// device so that a captured step can take it from the previous argmax.
+hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const int32_t* token_dev,
+                        float* out, hipStream_t s);
+
+// ---- gemv.hip ----
+enum GemvPro : int { PRO_NONE = 0, PRO_RMSNORM = 1 };
+enum GemvEpi : int { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+
+struct GemvSeg {
+    const uint8_t* w;   // [rows][row_bytes] blocks
+    float* out;         // rows outputs
+    int rows;
+};
+
+struct ArgmaxState {
+    float* cand_val;      // per workgroup
+    int32_t* cand_idx;
+    uint32_t* counter;    // zero before launch; the last workgroup resets it
+    int32_t* token_out;   // argmax result (next token)
+    int32_t* pos;         // optional: incremented by the last workgroup
+    int32_t* token_log;   // optional: token_log[*step] = argmax while *step < log_cap
+    int32_t log_cap;
+    int32_t* step;        // optional: incremented by the last workgroup
+};
+
+struct GemvArgs {
+    GemvSeg seg[3];
+    int nseg;
+    int cols;
+    const float* x;       // input vector (PRO_NONE) or hidden state (PRO_RMSNORM)
+    const float* norm_w;  // PRO_RMSNORM weights
+    float eps;
+    // EPI_SWIGLU: seg[0] = gate, seg[1] = up (equal rows), output to seg[0].out.
+    ArgmaxState am;       // EPI_ARGMAX
+};
+
+// Number of workgroups launch_gemv will use (for sizing ArgmaxState arrays).
+int gemv_grid(uint32_t type, int epi, const GemvArgs& a);
+hipError_t launch_gemv(uint32_t type, int pro, int epi, const GemvArgs& a, hipStream_t s);
+bool gemv_supported(uint32_t type);
+
+// ---- ops.hip (op-level IComputeBackend members) ----
+hipError_t launch_rmsnorm(const float* in, const float* w, float* out, int n, float eps, hipStream_t s);
+hipError_t launch_rope(float* q, float* k, const float* cosv, const float* sinv, int half, int same,
+                       hipStream_t s);
+hipError_t launch_softmax(float* x, int n, int has_softcap, float cap, hipStream_t s);
+hipError_t launch_silu(const float* in, float* out, int n, hipStream_t s);
+hipError_t launch_binary(int op, const float* a, const float* b, float* out, int n, hipStream_t s);  // 0 add, 1 mul
+hipError_t launch_scale(const float* in, float sc, float* out, int n, hipStream_t s);
+// ArgMax over n floats; st.cand_* sized for argmax_grid(n) workgroups.
+int argmax_grid(int n);
+hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream_t s);
+// Position bookkeeping for a captured decode step.
+hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s);
+hipError_t launch_fill_random_half(void* dst, size_t n, uint64_t seed, int fp16, hipStream_t s);
+
+// ---- attention.hip ----
+struct AttnArgs {
+    const float* q;         // [heads][head_dim] (pre-RoPE)
+    const float* k;         // [kv_heads][head_dim] (pre-RoPE), current token
+    const float* v;         // [kv_heads][head_dim], current token
+    void* kcache;           // this layer: [kv_heads][context][head_dim], fp16 or fp32
+    void* vcache;
+    const float* cos_tab;   // [context][rope_half]
+    const float* sin_tab;
+    const int32_t* pos;     // device position T
+    float* scores;          // [heads][context]
+    float* chunk_max;       // [heads][max_chunks]
+    float* part_out;        // [max_chunks][heads][head_dim]
+    float* part_sum;        // [max_chunks][heads]
+    uint32_t* counters;     // [kv_heads], zero; the last workgroup of each kv head resets its own
+    float* out;             // [heads][head_dim]
+    int heads, kv_heads, head_dim, rope_half, context, kv_fp16;
+};
+int attn_chunk(int heads, int kv_heads);
+int attn_max_chunks(int heads, int kv_heads, int context);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+}  // namespace llmdot

@@ -1,0 +1,230 @@
+// ops.hip -- op-level IComputeBackend members (src/Llmdot.Core/Inference/Backends/
+// IComputeBackend.cs:7-29) that are not GEMVs: RmsNorm, ApplyRoPE, Softmax,
+// Silu, Add, Mul, Scale, ArgMax.  Each reproduces the arithmetic of the
+// reference's VectorMath (src/Llmdot.Core/Tensors/Numeric/VectorMath.cs) per
+// element: the 8-lane Vector<float> part and the scalar tail use their own
+// formulas where the reference's differ.
+#include "common.h"
+#include "kernels.h"
+
+namespace llmdot {
+
+namespace {
+
+constexpr int WG = 256;
+constexpr int WG_BIG = 1024;
+
+template <int NT>
+__device__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < NT / 64; i++) s += red[i];
+    __syncthreads();
+    return s;
+}
+template <int NT>
+__device__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = -INFINITY;
+    for (int i = 0; i < NT / 64; i++) s = fmaxf(s, red[i]);
+    __syncthreads();
+    return s;
+}
+
+// VectorMath.RmsNorm, VM:308-340.
+__global__ __launch_bounds__(WG_BIG) void rmsnorm_kernel(const float* in, const float* w, float* out, int n, float eps) {
+    __shared__ float red[16];
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += WG_BIG) ss += in[i] * in[i];
+    ss = block_sum<WG_BIG>(ss, red);
+    const float inv = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+    const int n8 = n & ~7;
+    for (int i = threadIdx.x; i < n; i += WG_BIG)
+        out[i] = i < n8 ? __fmul_rn(__fmul_rn(w[i], in[i]), inv) : __fmul_rn(w[i], __fmul_rn(in[i], inv));
+}
+
+// TensorOps.ApplyRoPECore, TO:699-743 (cos/sin supplied by the host).
+__global__ void rope_kernel(float* q, float* k, const float* cosv, const float* sinv, int half, int same) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= half) return;
+    const float c = cosv[i], s = sinv[i];
+    float q0 = q[i], q1 = q[i + half];
+    q[i] = __fsub_rn(__fmul_rn(q0, c), __fmul_rn(q1, s));
+    q[i + half] = __fadd_rn(__fmul_rn(q0, s), __fmul_rn(q1, c));
+    if (same) return;
+    float k0 = k[i], k1 = k[i + half];
+    k[i] = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
+    k[i + half] = __fadd_rn(__fmul_rn(k0, s), __fmul_rn(k1, c));
+}
+
+// TanhApproxVector, VM:196-209.
+__device__ __forceinline__ float tanh_approx(float x) {
+    const float x2 = __fmul_rn(x, x);
+    const float ap = __fdiv_rn(__fmul_rn(x, __fadd_rn(27.0f, x2)), __fadd_rn(27.0f, __fmul_rn(9.0f, x2)));
+    return fabsf(x) > 4.0f ? (x > 0.0f ? 1.0f : -1.0f) : ap;
+}
+
+// VectorMath.Softmax, VM:215-258 (one workgroup).
+__global__ __launch_bounds__(WG_BIG) void softmax_kernel(float* x, int n, int has_cap, float cap) {
+    __shared__ float red[16];
+    const int n8 = n & ~7;
+    if (has_cap) {
+        const float inv_cap = __frcp_rn(cap);
+        for (int i = threadIdx.x; i < n; i += WG_BIG)
+            x[i] = i < n8 ? __fmul_rn(cap, tanh_approx(__fmul_rn(x[i], inv_cap))) : __fmul_rn(cap, tanhf(__fdiv_rn(x[i], cap)));
+        __syncthreads();
+    }
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += WG_BIG) m = fmaxf(m, x[i]);
+    m = block_max<WG_BIG>(m, red);
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n; i += WG_BIG) {
+        const float d = __fsub_rn(x[i], m);
+        const float e = i < n8 ? exp_approx(d) : expf(d);
+        x[i] = e;
+        s += e;
+    }
+    s = block_sum<WG_BIG>(s, red);
+    const float inv = __frcp_rn(s);
+    for (int i = threadIdx.x; i < n; i += WG_BIG) x[i] = __fmul_rn(x[i], inv);
+}
+
+// VectorMath.Silu / SiluInPlace, VM:99-135.
+__global__ void silu_kernel(const float* in, float* out, int n) {
+    const int n8 = n & ~7;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float v = in[i];
+        out[i] = i < n8 ? silu_ref(v) : __fdiv_rn(v, __fadd_rn(1.0f, expf(-v)));
+    }
+}
+
+__global__ void binary_kernel(int op, const float* a, const float* b, float* out, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = op == 0 ? __fadd_rn(a[i], b[i]) : __fmul_rn(a[i], b[i]);
+}
+
+__global__ void scale_kernel(const float* in, float sc, float* out, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = __fmul_rn(in[i], sc);
+}
+
+constexpr int AM_PER_WG = 4096;
+
+// VectorMath.ArgMax, VM:412-425: first index of the strict maximum.  Each
+// workgroup reduces AM_PER_WG elements; the last one reduces the candidates.
+__global__ __launch_bounds__(WG) void argmax_kernel(const float* x, int n, ArgmaxState st) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    __shared__ int last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float v = -INFINITY;
+    int idx = 0x7FFFFFFF;
+    const int beg = blockIdx.x * AM_PER_WG, end = min(n, beg + AM_PER_WG);
+    for (int i = beg + threadIdx.x; i < end; i += WG)
+        if (x[i] > v) { v = x[i]; idx = i; }   // ascending i per thread: first max wins
+    auto combine = [&](float ov, int oi) {
+        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    };
+    for (int o = 32; o >= 1; o >>= 1) combine(__shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    if (lane == 0) { sv[wave] = v; si[wave] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) combine(sv[w], si[w]);
+        st.cand_val[blockIdx.x] = v;
+        st.cand_idx[blockIdx.x] = idx;
+        __threadfence();
+        last = atomicAdd(st.counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    v = -INFINITY;
+    idx = 0x7FFFFFFF;
+    for (int c = threadIdx.x; c < (int)gridDim.x; c += WG)
+        combine(__builtin_nontemporal_load(st.cand_val + c), __builtin_nontemporal_load(st.cand_idx + c));
+    for (int o = 32; o >= 1; o >>= 1) combine(__shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    __syncthreads();
+    if (lane == 0) { sv[wave] = v; si[wave] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) combine(sv[w], si[w]);
+        if (idx == 0x7FFFFFFF) idx = 0;
+        *st.token_out = idx;
+        *st.counter = 0u;
+    }
+}
+
+__global__ void set_scalar_kernel(int32_t* dst, int32_t v) { *dst = v; }
+
+__global__ void fill_random_kernel(void* dst, size_t n, uint64_t seed, int fp16) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        uint64_t z = seed + 0x9E3779B97F4A7C15ull * (i + 1);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        const float u = ((float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f) - 0.5f) * 3.0f;
+        if (fp16) reinterpret_cast<_Float16*>(dst)[i] = (_Float16)u;
+        else reinterpret_cast<float*>(dst)[i] = u;
+    }
+}
+
+int grid_for(int n, int nt) {
+    int g = (n + nt - 1) / nt;
+    return g < 1 ? 1 : (g > 4096 ? 4096 : g);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const float* in, const float* w, float* out, int n, float eps, hipStream_t s) {
+    rmsnorm_kernel<<<1, WG_BIG, 0, s>>>(in, w, out, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_rope(float* q, float* k, const float* cosv, const float* sinv, int half, int same, hipStream_t s) {
+    if (half <= 0) return hipSuccess;
+    rope_kernel<<<grid_for(half, WG), WG, 0, s>>>(q, k, cosv, sinv, half, same);
+    return hipGetLastError();
+}
+hipError_t launch_softmax(float* x, int n, int has_softcap, float cap, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    softmax_kernel<<<1, WG_BIG, 0, s>>>(x, n, has_softcap, cap);
+    return hipGetLastError();
+}
+hipError_t launch_silu(const float* in, float* out, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    silu_kernel<<<grid_for(n, WG), WG, 0, s>>>(in, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_binary(int op, const float* a, const float* b, float* out, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    binary_kernel<<<grid_for(n, WG), WG, 0, s>>>(op, a, b, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_scale(const float* in, float sc, float* out, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    scale_kernel<<<grid_for(n, WG), WG, 0, s>>>(in, sc, out, n);
+    return hipGetLastError();
+}
+int argmax_grid(int n) { return (n + AM_PER_WG - 1) / AM_PER_WG; }
+hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream_t s) {
+    if (n <= 0) return hipErrorInvalidValue;
+    argmax_kernel<<<argmax_grid(n), WG, 0, s>>>(x, n, st);
+    return hipGetLastError();
+}
+hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s) {
+    set_scalar_kernel<<<1, 1, 0, s>>>(dst, v);
+    return hipGetLastError();
+}
+hipError_t launch_fill_random_half(void* dst, size_t n, uint64_t seed, int fp16, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    size_t g = (n + WG - 1) / WG;
+    fill_random_kernel<<<(unsigned)(g > 65536 ? 65536 : g), WG, 0, s>>>(dst, n, seed, fp16);
+    return hipGetLastError();
+}
+
+}  // namespace llmdot

@@ -1,0 +1,141 @@
+"""Seeded synthetic GGUF models for the workloads this backend is measured on.
+
+The reference ships no model files and no quantizer.  These builders write
+GGUF images (in memory, optionally to disk) whose weights are N(0, sigma)
+generated from (seed, tensor name, element index) and quantized by
+``llmdot_hip_synth_weights`` into the block layouts the reference decodes.
+RMSNorm weights are F32 ones.  ``tokenizer.ggml.tokens`` defines the
+vocabulary size (ArchitectureResolver.cs:185-190) and
+``tokenizer.ggml.eos_token_id`` is -1 so greedy runs are never cut short.
+
+Shapes:
+  tiny      llama  d512  L4  H8/8   hd64  F1408  V32000   all Q8_0
+  llama1b   llama  d2048 L16 H32/8  hd64  F8192  V128256  Q4_K_M mix, theta 500000
+  mistral7b llama  d4096 L32 H32/8  hd128 F14336 V32000   Q4_K_M mix, theta 10000
+  phi3mini  phi3   d3072 L32 H32/32 hd96  F8192  V32064   Q6_K/Q8_0 mix, theta 10000
+Q4_K_M mix: Q6_K for output.weight and every attn_v, Q4_K for every other
+matrix including token_embd.  The phi3mini mix: Q6_K for token_embd, output,
+attn_v and ffn_down; Q8_0 for attn_q, attn_k, attn_output, ffn_gate, ffn_up.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import zlib
+
+import numpy as np
+
+from . import _lib, gguf
+from ._lib import F32, Q4_K, Q6_K, Q8_0, byte_count, check, lib
+
+SPECS = {
+    "tiny": dict(arch="llama", hidden=512, layers=4, heads=8, kv_heads=8, head_dim=64, ffn=1408, vocab=32000,
+                 rope_base=10000.0, context=512, mix="q8_0"),
+    "llama1b": dict(arch="llama", hidden=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192,
+                    vocab=128256, rope_base=500000.0, context=1024, mix="q4_k_m"),
+    "mistral7b": dict(arch="llama", hidden=4096, layers=32, heads=32, kv_heads=8, head_dim=128, ffn=14336,
+                      vocab=32000, rope_base=10000.0, context=4608, mix="q4_k_m"),
+    "phi3mini": dict(arch="phi3", hidden=3072, layers=32, heads=32, kv_heads=32, head_dim=96, ffn=8192,
+                     vocab=32064, rope_base=10000.0, context=2560, mix="phi3"),
+}
+
+
+def tensor_type(mix: str, name: str) -> int:
+    if name.endswith("_norm.weight"):
+        return F32
+    if mix == "q8_0":
+        return Q8_0
+    if mix == "q4_k_m":
+        return Q6_K if (name == "output.weight" or ".attn_v." in name) else Q4_K
+    if mix == "phi3":
+        if name in ("token_embd.weight", "output.weight") or ".attn_v." in name or ".ffn_down." in name:
+            return Q6_K
+        return Q8_0
+    raise ValueError(f"unknown mix {mix}")
+
+
+def tensor_list(spec: dict) -> list:
+    """(name, rows, cols, ggml_type) in file order."""
+    d, f, v = spec["hidden"], spec["ffn"], spec["vocab"]
+    q, kv = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
+    out = [("token_embd.weight", v, d)]
+    for l in range(spec["layers"]):
+        p = f"blk.{l}."
+        out += [(p + "attn_norm.weight", 1, d), (p + "attn_q.weight", q, d), (p + "attn_k.weight", kv, d),
+                (p + "attn_v.weight", kv, d), (p + "attn_output.weight", d, q), (p + "ffn_norm.weight", 1, d),
+                (p + "ffn_gate.weight", f, d), (p + "ffn_up.weight", f, d), (p + "ffn_down.weight", d, f)]
+    out += [("output_norm.weight", 1, d), ("output.weight", v, d)]
+    return [(n, r, c, tensor_type(spec["mix"], n)) for n, r, c in out]
+
+
+def tensor_seed(seed: int, name: str) -> int:
+    return (int(seed) * 0x9E3779B1 + zlib.crc32(name.encode())) & 0xFFFFFFFFFFFFFFFF
+
+
+def metadata(spec: dict, context: int | None = None) -> list:
+    a = spec["arch"]
+    ctx = int(context or spec["context"])
+    toks = [f"<t{i}>" for i in range(spec["vocab"])]
+    return [
+        ("general.architecture", gguf.STR, a),
+        ("general.name", gguf.STR, f"synthetic-{a}"),
+        ("general.alignment", gguf.U32, 32),
+        (f"{a}.embedding_length", gguf.U32, spec["hidden"]),
+        (f"{a}.block_count", gguf.U32, spec["layers"]),
+        (f"{a}.context_length", gguf.U32, ctx),
+        (f"{a}.feed_forward_length", gguf.U32, spec["ffn"]),
+        (f"{a}.attention.head_count", gguf.U32, spec["heads"]),
+        (f"{a}.attention.head_count_kv", gguf.U32, spec["kv_heads"]),
+        (f"{a}.attention.key_length", gguf.U32, spec["head_dim"]),
+        (f"{a}.attention.layer_norm_rms_epsilon", gguf.F32V, 1e-5),
+        (f"{a}.rope.freq_base", gguf.F32V, spec["rope_base"]),
+        (f"{a}.rope.dimension_count", gguf.U32, spec["head_dim"]),
+        ("tokenizer.ggml.model", gguf.STR, "gpt2"),
+        ("tokenizer.ggml.tokens", gguf.ARR, (gguf.STR, toks)),
+        ("tokenizer.ggml.bos_token_id", gguf.I32, 1),
+        ("tokenizer.ggml.eos_token_id", gguf.I32, -1),
+    ]
+
+
+def synth_tensor(ggml_type: int, rows: int, cols: int, seed: int, out: np.ndarray, sigma: float = 0.02,
+                 threads: int | None = None) -> None:
+    """Fills ``out`` (uint8, exactly ByteCount bytes) with a seeded quantized tensor."""
+    nt = int(threads or min(16, os.cpu_count() or 1))
+    check(lib().llmdot_hip_synth_weights(ggml_type, rows, cols, seed, sigma, C.c_void_p(out.ctypes.data), nt))
+
+
+def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
+                threads: int | None = None, spec: dict | None = None) -> np.ndarray:
+    """Builds the whole GGUF file image in memory (uint8 numpy array)."""
+    spec = spec or SPECS[name]
+    tl = tensor_list(spec)
+    infos = [(n, (c,) if r == 1 else (c, r), t, byte_count(t, r * c)) for n, r, c, t in tl]
+    hdr, offsets, total = gguf.header_bytes(metadata(spec, context), infos)
+    img = np.empty(total, dtype=np.uint8)
+    img[:len(hdr)] = np.frombuffer(hdr, dtype=np.uint8)
+    base = len(hdr)
+    for (n, r, c, t), off, info in zip(tl, offsets, infos):
+        nb = info[3]
+        view = img[base + off: base + off + nb]
+        if n.endswith("_norm.weight"):
+            view.view(np.float32)[:] = 1.0
+        else:
+            synth_tensor(t, r, c, tensor_seed(seed, n), view, sigma, threads)
+        nxt = base + off + nb
+        pad = (32 - nxt % 32) % 32
+        img[nxt:nxt + pad] = 0
+    return img
+
+
+def prompt(vocab: int, n: int, seed: int = 7) -> list:
+    """Uniform random token ids in [0, vocab)."""
+    return np.random.Generator(np.random.PCG64(seed)).integers(0, vocab, size=n).astype(np.int32).tolist()
+
+
+def quantize(ggml_type: int, x: np.ndarray) -> np.ndarray:
+    """Quantizes a [rows, cols] float32 matrix into GGUF blocks (reference layouts)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = (1, x.size) if x.ndim == 1 else x.shape
+    out = np.zeros(rows * byte_count(ggml_type, cols), dtype=np.uint8)
+    check(lib().llmdot_hip_quantize(ggml_type, _lib.ptr(x), rows, cols, _lib.ptr(out)))
+    return out

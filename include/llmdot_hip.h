@@ -1,0 +1,214 @@
+/*
+ * llmdot_hip.h -- C ABI of libllmdot_hip.so, the MI355X (gfx950) backend for
+ * the llmdot decode token loop.
+ *
+ * Conventions
+ *   - Every function returns int32 status: 0 = OK, < 0 = error (LLMDOT_E_*).
+ *     llmdot_hip_last_error() returns a thread-local message for the last
+ *     failing call on the calling thread.  No C++ exception crosses the ABI.
+ *   - Host pointers are borrowed for the duration of the call.  Synchronous
+ *     calls return after results are written to host memory.
+ *   - Device memory is owned by the context / model handle.
+ *   - One context per device; a context and its models are not thread-safe
+ *     (the reference engine is single-threaded too).
+ *   - Element types use the GgmlType numbering of
+ *     src/Llmdot.Core/Loading/GgmlType.cs:3-28 (F32=0, F16=1, Q4_0=2, Q8_0=8,
+ *     Q4_K=12, Q5_K=13, Q6_K=14, BF16=25).  Q4_K and Q5_K are the reference's
+ *     own block layouts (src/Llmdot.Core/Tensors/Dequantize/DequantizeK.cs:76-140),
+ *     not ggml's.
+ *
+ * References are relative to the cognisoc/dotllm repository root:
+ *   ICB = src/Llmdot.Core/Inference/Backends/IComputeBackend.cs
+ *   IE  = src/Llmdot.Core/Inference/InferenceEngine.cs
+ */
+#ifndef LLMDOT_HIP_H
+#define LLMDOT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMDOT_OK 0
+#define LLMDOT_E_INVALID (-1)      /* bad argument (ArgumentException)            */
+#define LLMDOT_E_UNSUPPORTED (-2)  /* unsupported type/shape (NotSupportedException) */
+#define LLMDOT_E_NOT_FOUND (-3)    /* unknown weight key (KeyNotFoundException)    */
+#define LLMDOT_E_RANGE (-4)        /* position/token out of range (ArgumentOutOfRangeException) */
+#define LLMDOT_E_DEVICE (-5)       /* HIP runtime error / no device                */
+#define LLMDOT_E_NOMEM (-6)        /* device or host allocation failed             */
+
+typedef struct llmdot_hip_ctx llmdot_hip_ctx;
+typedef struct llmdot_hip_model llmdot_hip_model;
+
+/* ---- context (the backend object; replaces `new MetalBackend()` /
+ *      BackendFactory.CreateBestAvailable, src/Llmdot.Extensions.AI/BackendFactory.cs:8-39,
+ *      and IDisposable.Dispose of ICB:7) ------------------------------------ */
+const char* llmdot_hip_last_error(void);
+int32_t llmdot_hip_device_count(int32_t* count);
+int32_t llmdot_hip_create(int32_t device, llmdot_hip_ctx** out);
+int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx);
+
+typedef struct llmdot_hip_device_info {
+    char name[64];
+    char arch[32];          /* e.g. "gfx950" */
+    int32_t compute_units;
+    int32_t clock_mhz;
+    uint64_t hbm_bytes;
+} llmdot_hip_device_info;
+int32_t llmdot_hip_get_device_info(llmdot_hip_ctx* ctx, llmdot_hip_device_info* out);
+
+/* ---- persistent weights (the weightKey cache of MatMul, ICB:9; the Metal
+ *      backend's UploadPersistentBytes("w_"+name), src/Llmdot.Metal/MetalBackend.cs:92-100).
+ *      The bytes are the tensor's GGUF blocks, [rows][ByteCount(type, cols)],
+ *      kept in HBM in that native layout.  Uploading an existing key replaces it. */
+int32_t llmdot_hip_upload_weight(llmdot_hip_ctx* ctx, const char* key, uint32_t ggml_type,
+                                 const void* bytes, size_t nbytes, int64_t rows, int64_t cols);
+int32_t llmdot_hip_release_weight(llmdot_hip_ctx* ctx, const char* key);
+int32_t llmdot_hip_has_weight(llmdot_hip_ctx* ctx, const char* key, int32_t* present);
+
+/* ---- op level: one entry point per IComputeBackend member on the LLaMA
+ *      decode path.  Inputs/outputs are host spans, as in the interface. */
+
+/* ICB:9  MatMul(a, b, result, bType, aCols, bCols, weightKey).
+ * result_len = aRows * bCols.  When weight_key names an uploaded weight, b may
+ * be NULL and the resident copy is used; otherwise b is uploaded for this call
+ * (and kept under weight_key when weight_key is non-NULL). */
+int32_t llmdot_hip_matmul(llmdot_hip_ctx* ctx, const float* a, const void* b, float* result,
+                          int64_t result_len, uint32_t b_type, int32_t a_cols, int32_t b_cols,
+                          const char* weight_key);
+/* ICB:10 MatMulF32(a, b, result, aCols, bCols, weightKey); b is [bCols][aCols] fp32. */
+int32_t llmdot_hip_matmul_f32(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result,
+                              int64_t result_len, int32_t a_cols, int32_t b_cols,
+                              const char* weight_key);
+/* ICB:11 RmsNorm(input, weights, output, epsilon) */
+int32_t llmdot_hip_rms_norm(llmdot_hip_ctx* ctx, const float* input, const float* weights,
+                            float* output, int32_t n, float epsilon);
+/* ICB:14 ApplyRoPE(query, key, headDim, position, freqTable); NeoX half split
+ * over 2*half_dim dims.  same_span != 0 means query and key alias (rotate once). */
+int32_t llmdot_hip_apply_rope(llmdot_hip_ctx* ctx, float* query, float* key, int32_t head_dim,
+                              int32_t position, const float* freq_table, int32_t half_dim,
+                              int32_t same_span);
+/* ICB:13 ApplyRoPE(query, key, headDim, position, freqBase, rotaryDim) */
+int32_t llmdot_hip_apply_rope_base(llmdot_hip_ctx* ctx, float* query, float* key, int32_t head_dim,
+                                   int32_t position, float freq_base, int32_t rotary_dim,
+                                   int32_t same_span);
+/* ICB:15 Softmax(input, softcap) in place; has_softcap = 0 for null. */
+int32_t llmdot_hip_softmax(llmdot_hip_ctx* ctx, float* input, int32_t n, int32_t has_softcap,
+                           float softcap);
+/* ICB:16 Silu(input, result) and ICB:17 SiluInPlace(input) (pass input == result). */
+int32_t llmdot_hip_silu(llmdot_hip_ctx* ctx, const float* input, float* result, int32_t n);
+/* ICB:20 Add(a, b) in place (result == a) and ICB:21 Add(a, b, result). */
+int32_t llmdot_hip_add(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result, int32_t n);
+/* ICB:22/23 Scale(input, scale[, result]) */
+int32_t llmdot_hip_scale(llmdot_hip_ctx* ctx, const float* input, float scale, float* result, int32_t n);
+/* ICB:24 Mul(a, b, result) */
+int32_t llmdot_hip_mul(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result, int32_t n);
+/* ICB:27 DequantizeToFloat(src, dst, type, numRows, rowElements); bit-exact. */
+int32_t llmdot_hip_dequantize(llmdot_hip_ctx* ctx, const void* src, float* dst, uint32_t ggml_type,
+                              int32_t num_rows, int32_t row_elements);
+/* ICB:28 ArgMax(input): first index of the strict maximum. */
+int32_t llmdot_hip_argmax(llmdot_hip_ctx* ctx, const float* input, int32_t n, int32_t* index);
+
+/* ---- device-pointer variants (inputs already resident in HBM; used by
+ *      harnesses that time kernels without PCIe traffic). ------------------- */
+int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, void** dptr);
+int32_t llmdot_hip_device_free(llmdot_hip_ctx* ctx, void* dptr);
+int32_t llmdot_hip_memcpy_h2d(llmdot_hip_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int32_t llmdot_hip_memcpy_d2h(llmdot_hip_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int32_t llmdot_hip_synchronize(llmdot_hip_ctx* ctx);
+/* y[rows] = W[rows x cols] . x[cols] on the context stream, all pointers in HBM
+ * (W padded by the allocator as device_alloc does).  Asynchronous. */
+int32_t llmdot_hip_gemv_device(llmdot_hip_ctx* ctx, uint32_t ggml_type, const void* w_dev,
+                               const float* x_dev, float* y_dev, int32_t rows, int32_t cols);
+/* Elapsed milliseconds of `iters` back-to-back gemv_device launches cycling
+ * through n_weights weight copies, timed with HIP events on the context stream. */
+int32_t llmdot_hip_time_gemv(llmdot_hip_ctx* ctx, uint32_t ggml_type, const void* const* w_devs,
+                             int32_t n_weights, const float* x_dev, float* y_dev, int32_t rows,
+                             int32_t cols, int32_t iters, float* ms);
+
+/* ---- model level: the device-resident decode step (InferenceEngine.ProcessToken,
+ *      IE:134-146, LLaMA-like template IE:184-196) and greedy Generate (IE:74-132). */
+typedef struct llmdot_hip_model_desc {
+    int32_t hidden;          /* TransformerConfig.HiddenSize          */
+    int32_t layers;          /* LayerCount                            */
+    int32_t heads;           /* HeadCount                             */
+    int32_t kv_heads;        /* HeadCountKv                           */
+    int32_t head_dim;        /* HeadDim                               */
+    int32_t ffn;             /* FfnDim                                */
+    int32_t vocab;           /* VocabSize                             */
+    int32_t context;         /* KV capacity in positions (ContextLength) */
+    int32_t rope_dim;        /* RopeDimensionCount (0 = head_dim)     */
+    float eps;               /* NormEpsilon                           */
+    float rope_base;         /* RopeFreqBase                          */
+    float rope_linear_factor;/* RopeScalingFactor when type is Linear, else 1 */
+    int32_t kv_fp16;         /* 1: fp16 KV cache (default), 0: fp32 as the reference */
+    int32_t bos;             /* BosTokenId (used when the prompt is empty) */
+    /* Weight keys follow GGUF tensor names (src/Llmdot.Core/Loading/TensorNameResolver.cs:22-107):
+     * token_embd.weight, output_norm.weight, output.weight (optional: tied to
+     * token_embd), blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,
+     * ffn_gate,ffn_up,ffn_down}.weight, each optionally prefixed by key_prefix. */
+    const char* key_prefix;  /* may be NULL */
+} llmdot_hip_model_desc;
+
+int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip_model_desc* desc,
+                                llmdot_hip_model** out);
+int32_t llmdot_hip_model_destroy(llmdot_hip_model* model);
+/* KvCache.Reset (src/Llmdot.Core/Inference/KvCache.cs:40). */
+int32_t llmdot_hip_model_reset(llmdot_hip_model* model);
+/* ProcessToken(token, position): logits_or_null receives vocab floats;
+ * argmax_or_null receives ArgMax(logits). */
+int32_t llmdot_hip_decode_step(llmdot_hip_model* model, int32_t token, int32_t position,
+                               float* logits_or_null, int32_t* argmax_or_null);
+/* Sequential prompt processing (IE:84-88): tokens[i] at position pos0 + i.
+ * Outputs refer to the last token. */
+int32_t llmdot_hip_prefill(llmdot_hip_model* model, const int32_t* tokens, int32_t n, int32_t pos0,
+                           float* logits_or_null, int32_t* argmax_or_null);
+/* Greedy Generate (IE:74-132, Sampler.cs:26-27): resets the cache, processes the
+ * prompt, then yields max_tokens tokens (stopping after eos when eos >= 0).
+ * The decode loop runs on the device (token feedback stays in HBM).
+ * logits_out (nullable) receives [max_tokens][vocab]: the logits each token was
+ * sampled from. */
+int32_t llmdot_hip_generate(llmdot_hip_model* model, const int32_t* prompt, int32_t n_prompt,
+                            int32_t max_tokens, int32_t eos, int32_t* tokens_out, int32_t* n_out,
+                            float* logits_out);
+/* Reads KV slot (layer, position) as fp32, kv_heads*head_dim floats each. */
+int32_t llmdot_hip_kv_read(llmdot_hip_model* model, int32_t layer, int32_t position, float* k,
+                           float* v);
+
+/* ---- measurement hooks for the decode step --------------------------------
+ * Runs `steps` greedy decode steps from the current state (token feedback on
+ * the device) and returns the elapsed milliseconds measured with HIP events on
+ * the model's stream.  With per_kernel != 0 every launch of the dominant
+ * quantized GEMV class is additionally bracketed with HIP events and their
+ * summed duration / launch count / algorithmic bytes are reported. */
+typedef struct llmdot_hip_step_timing {
+    float total_ms;
+    float gemv_ms;           /* summed duration of the bracketed GEMV launches */
+    int32_t gemv_launches;
+    double gemv_bytes;       /* algorithmic bytes of those launches (weights + x + y) */
+} llmdot_hip_step_timing;
+int32_t llmdot_hip_model_time_decode(llmdot_hip_model* model, int32_t first_token, int32_t position,
+                                     int32_t steps, int32_t per_kernel, llmdot_hip_step_timing* out);
+/* Algorithmic HBM bytes of one decode step at `position`: quantized weights read
+ * once + the KV rows read + one embedding row. */
+int32_t llmdot_hip_model_step_bytes(llmdot_hip_model* model, int32_t position, double* bytes);
+/* Fills KV positions [0, n) with seeded values (timing at a given context without
+ * running the prompt). */
+int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* model, int32_t n, uint64_t seed);
+
+/* ---- GGUF tooling: reference-layout quantizers and seeded synthetic weights
+ *      (the reference ships no quantizer).  Host-only; no device needed. */
+int32_t llmdot_hip_quantize(uint32_t ggml_type, const float* src, int64_t rows, int64_t cols,
+                            void* dst);
+/* Fills dst with rows x cols weights ~ N(0, sigma), generated from (seed, element
+ * index) so the result is independent of thread count, quantized to ggml_type.
+ * ggml_type F32 writes the floats themselves. */
+int32_t llmdot_hip_synth_weights(uint32_t ggml_type, int64_t rows, int64_t cols, uint64_t seed,
+                                 float sigma, void* dst, int32_t threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
