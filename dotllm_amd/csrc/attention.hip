@@ -44,8 +44,9 @@ __device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int
 
 // NeoX rotation of element d of a head (pairs (i, i + half), dims >= 2*half untouched).
 __device__ __forceinline__ float rope_elem(const float* x, int d, int half, float c_lo, float s_lo) {
-    if (d < half) return __fsub_rn(__fmul_rn(x[d], c_lo), __fmul_rn(x[d + half], s_lo));
-    if (d < 2 * half) return __fadd_rn(__fmul_rn(x[d - half], s_lo), __fmul_rn(x[d], c_lo));
+#pragma clang fp contract(off)
+    if (d < half) return ((x[d] * c_lo) - (x[d + half] * s_lo));
+    if (d < 2 * half) return ((x[d - half] * s_lo) + (x[d] * c_lo));
     return x[d];
 }
 
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a, int C, int 
     }
     for (int o = 1; o < TPD; o <<= 1) s += __shfl_xor(s, o, 64);
     const float inv_sqrt = 1.0f / sqrtf((float)HD);
-    float score = __fmul_rn(s, inv_sqrt);
+    float score = (s * inv_sqrt);
     const bool live = h < G && p < cnt && sub == 0;
     if (live) a.scores[(int64_t)(kvh * G + h) * a.context + p0 + p] = score;
     // per-head max over this chunk: head h owns threads [h*C*TPD, (h+1)*C*TPD)
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a, int C, int G) {
         float e = 0.f;
         if (p < cnt) {
             const int sidx = p0 + p;
-            const float x = __fsub_rn(a.scores[(int64_t)(kvh * G + h) * a.context + sidx], gmax[h]);
+            const float x = (a.scores[(int64_t)(kvh * G + h) * a.context + sidx] - gmax[h]);
             e = sidx < n8 ? exp_approx(x) : expf(x);
         }
         p_s[idx] = e;

@@ -99,24 +99,28 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // One lane of ExpApproxVector (src/Llmdot.Core/Tensors/Numeric/VectorMath.cs:137-166),
-// bit-exact: every operation is a separately rounded fp32 op (no contraction).
+// bit-exact: every operation is a separately rounded fp32 op (contraction is
+// switched off in the function body; the __f*_rn spellings alone do not stop it).
 __device__ __forceinline__ float exp_approx(float x) {
+#pragma clang fp contract(off)
     float c = x > -87.3f ? x : -87.3f;
     c = c < 88.4f ? c : 88.4f;
-    int k = (int)__fadd_rn(__fmul_rn(c, 1.4426950408889634f), 0.5f);   // truncates
+    int k = (int)((c * 1.4426950408889634f) + 0.5f);   // truncates
     float kf = (float)k;
-    float y = __fsub_rn(__fsub_rn(c, __fmul_rn(kf, 0.693145751953125f)), __fmul_rn(kf, 1.42860677e-6f));
-    float cc = __fmul_rn(__fmul_rn(y, y), 0.5f);
-    float cy = __fmul_rn(cc, y);
-    float pade = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(1.0f, y), cc), __fmul_rn(cy, 0.3333333f)),
-                           __fmul_rn(__fmul_rn(cy, y), 0.2f));
-    float r = __fmul_rn(pade, __uint_as_float((uint32_t)(k + 127) << 23));
+    float y = ((c - (kf * 0.693145751953125f)) - (kf * 1.42860677e-6f));
+    float cc = ((y * y) * 0.5f);
+    float cy = (cc * y);
+    float pade = ((((1.0f + y) + cc) + (cy * 0.3333333f)) + ((cy * y) * 0.2f));
+    float r = (pade * __uint_as_float((uint32_t)(k + 127) << 23));
     if (x < -87.3f) r = 0.0f;
     if (x > 88.4f) r = __uint_as_float(0x7F800000u);
     return r;
 }
 
 // Vector lanes of VectorMath.SiluInPlace (VM:118-135): x / (1 + ExpApprox(-x)).
-__device__ __forceinline__ float silu_ref(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, exp_approx(-x))); }
+__device__ __forceinline__ float silu_ref(float x) {
+#pragma clang fp contract(off)
+    return (x / (1.0f + exp_approx(-x)));
+}
 
 }  // namespace llmdot

@@ -6,6 +6,9 @@
 #include "common.h"
 #include "kernels.h"
 
+// Reference rounding everywhere in this file: no FMA contraction.
+#pragma clang fp contract(off)
+
 namespace llmdot {
 
 __device__ __forceinline__ float h2f_at(const uint8_t* p) { return half_bits_to_float(p[0] | (p[1] << 8)); }
@@ -29,11 +32,11 @@ __device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
         float d = h2f_at(b);
         int qs = b[2 + (j & 15)];
         int q = j < 16 ? (qs & 0x0F) : ((qs >> 4) & 0x0F);
-        return __fmul_rn((float)(q - 8), d);
+        return ((float)(q - 8) * d);
     }
     case GGML_Q8_0: {  // DB:36-59
         const uint8_t* b = row + (i >> 5) * 34;
-        return __fmul_rn((float)(int8_t)b[2 + (i & 31)], h2f_at(b));
+        return ((float)(int8_t)b[2 + (i & 31)] * h2f_at(b));
     }
     case GGML_Q4_K: {  // DK:76-106
         const uint8_t* b = row + (i >> 8) * 144;
@@ -41,7 +44,7 @@ __device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
         float d = h2f_at(b), dmin = h2f_at(b + 2);
         int sc = extract6(b + 4, g * 12), mi = extract6(b + 4, g * 12 + 6);
         int q = (b[16 + (j >> 1)] >> ((j & 1) * 4)) & 0xF;
-        return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)(q - 8)), __fmul_rn(dmin, (float)mi));
+        return (((d * (float)sc) * (float)(q - 8)) - (dmin * (float)mi));
     }
     case GGML_Q5_K: {  // DK:108-140
         const uint8_t* b = row + (i >> 8) * 176;
@@ -51,7 +54,7 @@ __device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
         int ql = (b[48 + (j >> 1)] >> ((j & 1) * 4)) & 0xF;
         int qh = (b[16 + (j >> 3)] >> (j & 7)) & 0x1;
         int q5 = ql + (qh << 4);
-        return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)(q5 - 16)), __fmul_rn(dmin, (float)mi));
+        return (((d * (float)sc) * (float)(q5 - 16)) - (dmin * (float)mi));
     }
     case GGML_Q6_K: {  // DK:142-187
         const uint8_t* b = row + (i >> 8) * 210;
@@ -63,7 +66,7 @@ __device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
         int nib = (t & 2) ? (lo >> 4) : (lo & 0xF);
         int q = (nib | (((qh[l] >> (2 * t)) & 3) << 4)) - 32;
         int sc = (int8_t)b[192 + n / 16 + (l >> 4) + 2 * t];
-        return __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+        return ((d * (float)sc) * (float)q);
     }
     default: return 0.0f;
     }

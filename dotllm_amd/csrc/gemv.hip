@@ -223,6 +223,7 @@ template <> struct UnitOf<GGML_F16> { using type = UF16; };
 
 // sum(h^2) over n with all 256 threads; returns 1 / sqrt(ss / n + eps) to every thread.
 __device__ float block_rms_inv(const float* __restrict__ h, int n, float eps, float* red) {
+#pragma clang fp contract(off)
     float ss = 0.f;
     const int n4 = n >> 2;
     const float4* h4 = reinterpret_cast<const float4*>(h);
@@ -236,22 +237,23 @@ __device__ float block_rms_inv(const float* __restrict__ h, int n, float eps, fl
     __syncthreads();
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     __syncthreads();
-    return __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+    return (1.0f / (sqrtf(((ss / (float)n) + eps))));
 }
 
 // x element i for the prologue in use.
 template <int PRO>
 __device__ __forceinline__ float4 xload4(const GemvArgs& a, int i, float inv, int n8) {
+#pragma clang fp contract(off)
     float4 h = *reinterpret_cast<const float4*>(a.x + i);
     if (PRO == PRO_NONE) return h;
     float4 w = *reinterpret_cast<const float4*>(a.norm_w + i);
     float4 r;
     if (i + 4 <= n8) {  // Vector<float> part: (w * x) * inv
-        r.x = __fmul_rn(__fmul_rn(w.x, h.x), inv); r.y = __fmul_rn(__fmul_rn(w.y, h.y), inv);
-        r.z = __fmul_rn(__fmul_rn(w.z, h.z), inv); r.w = __fmul_rn(__fmul_rn(w.w, h.w), inv);
+        r.x = ((w.x * h.x) * inv); r.y = ((w.y * h.y) * inv);
+        r.z = ((w.z * h.z) * inv); r.w = ((w.w * h.w) * inv);
     } else {            // scalar tail: w * (x * inv)
-        r.x = __fmul_rn(w.x, __fmul_rn(h.x, inv)); r.y = __fmul_rn(w.y, __fmul_rn(h.y, inv));
-        r.z = __fmul_rn(w.z, __fmul_rn(h.z, inv)); r.w = __fmul_rn(w.w, __fmul_rn(h.w, inv));
+        r.x = (w.x * (h.x * inv)); r.y = (w.y * (h.y * inv));
+        r.z = (w.z * (h.z * inv)); r.w = (w.w * (h.w * inv));
     }
     return r;
 }
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
         for (int r = 0; r < 4; r++) {
             if (lane == r && valid[r]) {
                 float* o = seg.out + row0 + r;
-                *o = (EPI == EPI_ADD) ? __fadd_rn(*o, acc[r]) : acc[r];
+                *o = (EPI == EPI_ADD) ? (*o + acc[r]) : acc[r];
             }
         }
     } else {  // EPI_SWIGLU
@@ -344,8 +346,8 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
             if (lane == r && valid[r]) {
                 const int rr = row0 + r;
                 float g = acc[r], up = acc[r + 2];
-                float sg = rr < f8 ? silu_ref(g) : __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
-                seg.out[rr] = __fmul_rn(sg, up);
+                float sg = rr < f8 ? silu_ref(g) : (g / (1.0f + expf(-g)));
+                seg.out[rr] = (sg * up);
             }
         }
     }

@@ -7,6 +7,9 @@
 #include "common.h"
 #include "kernels.h"
 
+// Reference rounding everywhere in this file: no FMA contraction.
+#pragma clang fp contract(off)
+
 namespace llmdot {
 
 namespace {
@@ -43,10 +46,10 @@ __global__ __launch_bounds__(WG_BIG) void rmsnorm_kernel(const float* in, const 
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += WG_BIG) ss += in[i] * in[i];
     ss = block_sum<WG_BIG>(ss, red);
-    const float inv = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+    const float inv = (1.0f / (sqrtf(((ss / (float)n) + eps))));
     const int n8 = n & ~7;
     for (int i = threadIdx.x; i < n; i += WG_BIG)
-        out[i] = i < n8 ? __fmul_rn(__fmul_rn(w[i], in[i]), inv) : __fmul_rn(w[i], __fmul_rn(in[i], inv));
+        out[i] = i < n8 ? ((w[i] * in[i]) * inv) : (w[i] * (in[i] * inv));
 }
 
 // TensorOps.ApplyRoPECore, TO:699-743 (cos/sin supplied by the host).
@@ -55,18 +58,18 @@ __global__ void rope_kernel(float* q, float* k, const float* cosv, const float* 
     if (i >= half) return;
     const float c = cosv[i], s = sinv[i];
     float q0 = q[i], q1 = q[i + half];
-    q[i] = __fsub_rn(__fmul_rn(q0, c), __fmul_rn(q1, s));
-    q[i + half] = __fadd_rn(__fmul_rn(q0, s), __fmul_rn(q1, c));
+    q[i] = ((q0 * c) - (q1 * s));
+    q[i + half] = ((q0 * s) + (q1 * c));
     if (same) return;
     float k0 = k[i], k1 = k[i + half];
-    k[i] = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
-    k[i + half] = __fadd_rn(__fmul_rn(k0, s), __fmul_rn(k1, c));
+    k[i] = ((k0 * c) - (k1 * s));
+    k[i + half] = ((k0 * s) + (k1 * c));
 }
 
 // TanhApproxVector, VM:196-209.
 __device__ __forceinline__ float tanh_approx(float x) {
-    const float x2 = __fmul_rn(x, x);
-    const float ap = __fdiv_rn(__fmul_rn(x, __fadd_rn(27.0f, x2)), __fadd_rn(27.0f, __fmul_rn(9.0f, x2)));
+    const float x2 = (x * x);
+    const float ap = ((x * (27.0f + x2)) / (27.0f + (9.0f * x2)));
     return fabsf(x) > 4.0f ? (x > 0.0f ? 1.0f : -1.0f) : ap;
 }
 
@@ -75,9 +78,9 @@ __global__ __launch_bounds__(WG_BIG) void softmax_kernel(float* x, int n, int ha
     __shared__ float red[16];
     const int n8 = n & ~7;
     if (has_cap) {
-        const float inv_cap = __frcp_rn(cap);
+        const float inv_cap = (1.0f / (cap));
         for (int i = threadIdx.x; i < n; i += WG_BIG)
-            x[i] = i < n8 ? __fmul_rn(cap, tanh_approx(__fmul_rn(x[i], inv_cap))) : __fmul_rn(cap, tanhf(__fdiv_rn(x[i], cap)));
+            x[i] = i < n8 ? (cap * tanh_approx((x[i] * inv_cap))) : (cap * tanhf((x[i] / cap)));
         __syncthreads();
     }
     float m = -INFINITY;
@@ -85,14 +88,14 @@ __global__ __launch_bounds__(WG_BIG) void softmax_kernel(float* x, int n, int ha
     m = block_max<WG_BIG>(m, red);
     float s = 0.f;
     for (int i = threadIdx.x; i < n; i += WG_BIG) {
-        const float d = __fsub_rn(x[i], m);
+        const float d = (x[i] - m);
         const float e = i < n8 ? exp_approx(d) : expf(d);
         x[i] = e;
         s += e;
     }
     s = block_sum<WG_BIG>(s, red);
-    const float inv = __frcp_rn(s);
-    for (int i = threadIdx.x; i < n; i += WG_BIG) x[i] = __fmul_rn(x[i], inv);
+    const float inv = (1.0f / (s));
+    for (int i = threadIdx.x; i < n; i += WG_BIG) x[i] = (x[i] * inv);
 }
 
 // VectorMath.Silu / SiluInPlace, VM:99-135.
@@ -100,18 +103,18 @@ __global__ void silu_kernel(const float* in, float* out, int n) {
     const int n8 = n & ~7;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         const float v = in[i];
-        out[i] = i < n8 ? silu_ref(v) : __fdiv_rn(v, __fadd_rn(1.0f, expf(-v)));
+        out[i] = i < n8 ? silu_ref(v) : (v / (1.0f + expf(-v)));
     }
 }
 
 __global__ void binary_kernel(int op, const float* a, const float* b, float* out, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        out[i] = op == 0 ? __fadd_rn(a[i], b[i]) : __fmul_rn(a[i], b[i]);
+        out[i] = op == 0 ? (a[i] + b[i]) : (a[i] * b[i]);
 }
 
 __global__ void scale_kernel(const float* in, float sc, float* out, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        out[i] = __fmul_rn(in[i], sc);
+        out[i] = (in[i] * sc);
 }
 
 constexpr int AM_PER_WG = 4096;
