@@ -57,7 +57,12 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step kernel by kernel instead of replaying the captured HIP graph "
+                         "(rocprofv3 cannot trace graph launches on this image)")
     args = ap.parse_args()
+    if args.eager:
+        os.environ["LLMDOT_HIP_NO_GRAPH"] = "1"
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode path is a single-GPU "
               f"batch-1 loop and no multi-GPU figure is produced.", file=sys.stderr)
@@ -115,6 +120,7 @@ def main() -> int:
         "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": f"{args.config}-shape Q4_K_M greedy decode, batch 1, context {args.ctx}, fp16 KV",
+                   "launch": "eager" if args.eager else "hip-graph",
                    "hidden": spec["hidden"], "layers": spec["layers"], "heads": spec["heads"],
                    "kv_heads": spec["kv_heads"], "head_dim": spec["head_dim"], "ffn": spec["ffn"],
                    "vocab": spec["vocab"], "context": args.ctx, "batch": 1},

@@ -10,31 +10,31 @@
 //
 // The reference's ExpApprox is not multiplicative, so an online (rescaling)
 // softmax cannot reproduce it; the global max must be known before any
-// exponent.  Two kernels therefore split the sequence into chunks of C
-// positions per kv head:
-//   phase 1: RoPE + KV write + scores of the chunk + per-chunk max (per q head)
+// exponent.  Two kernels therefore split the sequence into chunks of 64
+// positions per kv head (grid = chunks x kv heads; chunks past T exit):
+//   phase 1: RoPE + KV write + scores of the chunk + per-chunk max (per q head).
+//            4 threads per position, each loading a quarter of the K row with
+//            16-byte loads; every K row is read once for all G q heads.
 //   phase 2: global max from the chunk maxima, exponentials, chunk partial
-//            sum(e) and sum(e V); the last workgroup of each kv head combines
-//            the chunk partials (out = sum(eV) / sum(e)).
-// Each K/V row is read from HBM exactly once per layer.  cos/sin come from a
-// host table computed with the same libm calls as the reference, so RoPE is
-// bit-exact.
+//            sum(e) and sum(e V) (16-byte V loads), and the last workgroup of
+//            each kv head combines the chunk partials (out = sum(eV) / sum(e))
+//            and writes the activation records for the O projection.
+// cos/sin come from a host table built with the same libm calls as the
+// reference, so RoPE is bit-exact.
 #include "common.h"
 #include "kernels.h"
+#include "xrec.h"
 
 namespace llmdot {
 
 namespace {
 
 constexpr int WG = 256;
+constexpr int CH = 64;   // positions per chunk
 
-__device__ __forceinline__ float load_kv(const void* cache, int64_t idx, int fp16) {
-    if (fp16) return (float)reinterpret_cast<const _Float16*>(cache)[idx];
-    return reinterpret_cast<const float*>(cache)[idx];
-}
 __device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int fp16) {
     if (fp16) {
-        _Float16 h = (_Float16)v;                       // round to nearest even
+        const _Float16 h = (_Float16)v;                 // round to nearest even
         reinterpret_cast<_Float16*>(cache)[idx] = h;
         return (float)h;
     }
@@ -42,193 +42,267 @@ __device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int
     return v;
 }
 
+// N consecutive cache elements starting at element idx (16-byte aligned) as floats.
+template <int N>
+__device__ __forceinline__ void load_kv_row(const void* cache, int64_t idx, int fp16, float* out) {
+    if (fp16) {
+        const _Float16* p = reinterpret_cast<const _Float16*>(cache) + idx;
+        if constexpr (N % 8 == 0) {
+#pragma unroll
+            for (int i = 0; i < N / 8; i++) {
+                const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    out[8 * i + 2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] & 0xFFFFu));
+                    out[8 * i + 2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] >> 16));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N / 2; i++) {
+                const uint32_t w = reinterpret_cast<const uint32_t*>(p)[i];
+                out[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+                out[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+            }
+        }
+    } else {
+        const float* p = reinterpret_cast<const float*>(cache) + idx;
+        if constexpr (N % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < N / 4; i++) {
+                const float4 v = reinterpret_cast<const float4*>(p)[i];
+                out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; i++) out[i] = p[i];
+        }
+    }
+}
+
 // NeoX rotation of element d of a head (pairs (i, i + half), dims >= 2*half untouched).
-__device__ __forceinline__ float rope_elem(const float* x, int d, int half, float c_lo, float s_lo) {
+__device__ __forceinline__ float rope_elem(const float* x, int d, int half, const float* cs, const float* sn) {
 #pragma clang fp contract(off)
-    if (d < half) return ((x[d] * c_lo) - (x[d + half] * s_lo));
-    if (d < 2 * half) return ((x[d - half] * s_lo) + (x[d] * c_lo));
+    if (d < half) return x[d] * cs[d] - x[d + half] * sn[d];
+    if (d < 2 * half) return x[d - half] * sn[d - half] + x[d] * cs[d - half];
     return x[d];
 }
 
-template <int HD>
-__global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a, int C, int G) {
-    extern __shared__ float smem[];
-    float* q_s = smem;                      // [G][HD]
-    float* k_s = smem + G * HD;             // [C][HD + 1]
-    __shared__ float red_max[WG / 16];
-
+template <int HD, int G>
+__global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
+    __shared__ float q_s[G * HD];
+    __shared__ float knew[HD];
+    __shared__ float wmax[4][G];
+    constexpr int DPT = HD / 4;           // K elements per thread
     const int T = *a.pos, n = T + 1;
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const int p0 = c * C;
+    const int p0 = c * CH;
     if (p0 >= n) return;
-    const int cnt = min(C, n - p0);
+    const int cnt = min(CH, n - p0);
     const int half = a.rope_half;
     const float* cs = a.cos_tab + (int64_t)T * half;
     const float* sn = a.sin_tab + (int64_t)T * half;
-
-    for (int idx = threadIdx.x; idx < G * HD; idx += WG) {
-        const int h = idx / HD, d = idx - h * HD;
-        const float* qh = a.q + (int64_t)(kvh * G + h) * HD;
-        const int i = d < half ? d : d - half;
-        const float cv = i < half ? cs[i] : 1.f, sv = i < half ? sn[i] : 0.f;
-        q_s[idx] = rope_elem(qh, d, half, cv, sv);
-    }
     const int64_t cache_base = (int64_t)kvh * a.context * HD;
-    for (int idx = threadIdx.x; idx < cnt * HD; idx += WG) {
-        const int p = idx / HD, d = idx - p * HD;
-        k_s[p * (HD + 1) + d] = load_kv(a.kcache, cache_base + (int64_t)(p0 + p) * HD + d, a.kv_fp16);
-    }
-    __syncthreads();
-    if (T >= p0 && T < p0 + C) {
-        // this workgroup owns the new token: rotate k, store K/V slot T
-        const float* kh = a.k + (int64_t)kvh * HD;
-        const float* vh = a.v + (int64_t)kvh * HD;
-        for (int d = threadIdx.x; d < HD; d += WG) {
-            const int i = d < half ? d : d - half;
-            const float cv = i < half ? cs[i] : 1.f, sv = i < half ? sn[i] : 0.f;
-            float kr = rope_elem(kh, d, half, cv, sv);
-            const int64_t slot = cache_base + (int64_t)T * HD + d;
-            k_s[(T - p0) * (HD + 1) + d] = store_kv(a.kcache, slot, kr, a.kv_fp16);
-            store_kv(a.vcache, slot, vh[d], a.kv_fp16);
-        }
-        __syncthreads();
-    }
 
-    // dot products: TPD threads per (head, position)
-    const int TPD = WG / (G * C);
-    const int di = threadIdx.x / TPD, sub = threadIdx.x - di * TPD;
-    const int h = di / C, p = di - h * C;
-    const int per = HD / TPD;
-    float s = 0.f;
-    if (h < G && p < cnt) {
-        const float* qv = q_s + h * HD + sub * per;
-        const float* kv = k_s + p * (HD + 1) + sub * per;
-        for (int d = 0; d < per; d++) s += qv[d] * kv[d];
+    // K row of this thread's position, issued first
+    const int t = threadIdx.x, p = t >> 2, sub = t & 3;
+    const bool live = p < cnt;
+    const bool is_new = p0 + p == T;
+    float kv[DPT];
+#pragma unroll
+    for (int d = 0; d < DPT; d++) kv[d] = 0.f;
+    if (live && !is_new) load_kv_row<DPT>(a.kcache, cache_base + (int64_t)(p0 + p) * HD + sub * DPT, a.kv_fp16, kv);
+
+    for (int idx = t; idx < G * HD; idx += WG) {
+        const int h = idx / HD, d = idx - h * HD;
+        q_s[idx] = rope_elem(a.q + (int64_t)(kvh * G + h) * HD, d, half, cs, sn);
     }
-    for (int o = 1; o < TPD; o <<= 1) s += __shfl_xor(s, o, 64);
-    const float inv_sqrt = 1.0f / sqrtf((float)HD);
-    float score = (s * inv_sqrt);
-    const bool live = h < G && p < cnt && sub == 0;
-    if (live) a.scores[(int64_t)(kvh * G + h) * a.context + p0 + p] = score;
-    // per-head max over this chunk: head h owns threads [h*C*TPD, (h+1)*C*TPD)
-    const int span = C * TPD, width = span < 64 ? span : 64;
-    float m = live ? score : -INFINITY;
-    for (int o = 1; o < width; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if ((threadIdx.x & (width - 1)) == 0) red_max[threadIdx.x / width] = m;
+    if (T >= p0 && T < p0 + CH) {   // this workgroup owns the new token: store K/V slot T
+        for (int d = t; d < HD; d += WG) {
+            const int64_t slot = cache_base + (int64_t)T * HD + d;
+            knew[d] = store_kv(a.kcache, slot, rope_elem(a.k + (int64_t)kvh * HD, d, half, cs, sn), a.kv_fp16);
+            store_kv(a.vcache, slot, a.v[(int64_t)kvh * HD + d], a.kv_fp16);
+        }
+    }
     __syncthreads();
-    if (threadIdx.x < G) {
-        const int gph = span / width;
-        float mm = -INFINITY;
-        for (int i = 0; i < gph; i++) mm = fmaxf(mm, red_max[threadIdx.x * gph + i]);
-        a.chunk_max[(int64_t)(kvh * G + threadIdx.x) * gridDim.x + c] = mm;
+    if (live && is_new) {
+#pragma unroll
+        for (int d = 0; d < DPT; d++) kv[d] = knew[sub * DPT + d];
+    }
+    const float inv_sqrt = 1.0f / sqrtf((float)HD);
+    const int lane = t & 63, wave = t >> 6;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float* qv = q_s + h * HD + sub * DPT;
+        float s = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPT; d++) s += qv[d] * kv[d];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        const float score = s * inv_sqrt;
+        if (live && sub == 0) a.scores[(int64_t)(kvh * G + h) * a.context + p0 + p] = score;
+        float m = live ? score : -INFINITY;
+        m = wave_max(m);
+        if (lane == 0) wmax[wave][h] = m;
+    }
+    __syncthreads();
+    if (t < G) {
+        const float m = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
+        a.chunk_max[(int64_t)(kvh * G + t) * gridDim.x + c] = m;
     }
 }
 
-template <int HD>
-__global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a, int C, int G) {
-    extern __shared__ float smem[];
-    float* v_s = smem;                      // [C][HD + 1]
-    float* p_s = smem + C * (HD + 1);       // [G][C]
-    __shared__ float gmax[16];
+template <int HD, int G>
+__global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
+    constexpr int DPG = HD / 16;          // V elements per thread and position
+    __shared__ float p_s[G][CH];
+    __shared__ float red[4][G * HD];
+    __shared__ float gmax[G];
     __shared__ int is_last;
-
     const int T = *a.pos, n = T + 1, n8 = n & ~7;
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const int p0 = c * C;
+    const int p0 = c * CH;
     if (p0 >= n) return;
-    const int cnt = min(C, n - p0);
-    const int nch = (n + C - 1) / C;
+    const int cnt = min(CH, n - p0);
+    const int nch = (n + CH - 1) / CH;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int dg = t & 15, pg = t >> 4;
+    const int64_t cache_base = (int64_t)kvh * a.context * HD;
 
-    if (threadIdx.x < G) {
-        const float* cm = a.chunk_max + (int64_t)(kvh * G + threadIdx.x) * gridDim.x;
+    float vv[4][DPG];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int p = pg + 16 * i;
+        if (p < cnt) {
+            load_kv_row<DPG>(a.vcache, cache_base + (int64_t)(p0 + p) * HD + dg * DPG, a.kv_fp16, vv[i]);
+        } else {
+#pragma unroll
+            for (int d = 0; d < DPG; d++) vv[i][d] = 0.f;
+        }
+    }
+    if (t < G) {
+        const float* cm = a.chunk_max + (int64_t)(kvh * G + t) * gridDim.x;
         float m = -INFINITY;
         for (int i = 0; i < nch; i++) m = fmaxf(m, cm[i]);
-        gmax[threadIdx.x] = m;
-    }
-    const int64_t cache_base = (int64_t)kvh * a.context * HD;
-    for (int idx = threadIdx.x; idx < cnt * HD; idx += WG) {
-        const int p = idx / HD, d = idx - p * HD;
-        v_s[p * (HD + 1) + d] = load_kv(a.vcache, cache_base + (int64_t)(p0 + p) * HD + d, a.kv_fp16);
+        gmax[t] = m;
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * C; idx += WG) {
-        const int h = idx / C, p = idx - h * C;
+    for (int idx = t; idx < G * CH; idx += WG) {
+        const int h = idx / CH, p = idx - h * CH;
         float e = 0.f;
         if (p < cnt) {
+#pragma clang fp contract(off)
             const int sidx = p0 + p;
-            const float x = (a.scores[(int64_t)(kvh * G + h) * a.context + sidx] - gmax[h]);
+            const float x = a.scores[(int64_t)(kvh * G + h) * a.context + sidx] - gmax[h];
             e = sidx < n8 ? exp_approx(x) : expf(x);
         }
-        p_s[idx] = e;
+        p_s[h][p] = e;
     }
     __syncthreads();
-    if (threadIdx.x < G) {
+    if (t < G) {
         float z = 0.f;
-        for (int p = 0; p < cnt; p++) z += p_s[threadIdx.x * C + p];
-        a.part_sum[(int64_t)c * a.heads + kvh * G + threadIdx.x] = z;
+        for (int p = 0; p < cnt; p++) z += p_s[t][p];
+        a.part_sum[(int64_t)c * a.heads + kvh * G + t] = z;
     }
-    for (int idx = threadIdx.x; idx < G * HD; idx += WG) {
-        const int h = idx / HD, d = idx - h * HD;
-        float acc = 0.f;
-        const float* pr = p_s + h * C;
-        for (int p = 0; p < cnt; p++) acc += pr[p] * v_s[p * (HD + 1) + d];
-        a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = acc;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float acc[DPG];
+#pragma unroll
+        for (int d = 0; d < DPG; d++) acc[d] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float pr = p_s[h][pg + 16 * i];
+#pragma unroll
+            for (int d = 0; d < DPG; d++) acc[d] += pr * vv[i][d];
+        }
+#pragma unroll
+        for (int d = 0; d < DPG; d++) {
+            float v = acc[d];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (lane < 16) red[wave][h * HD + dg * DPG + d] = v;
+        }
     }
-    __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = atomicAdd(a.counters + kvh, 1u);
-        is_last = (prev == (unsigned)nch - 1u);
+    for (int idx = t; idx < G * HD; idx += WG) {
+        const int h = idx / HD, d = idx - h * HD;
+        a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = (red[0][idx] + red[1][idx]) + (red[2][idx] + red[3][idx]);
+    }
+    __syncthreads();
+    if (t == 0) {   // one release by thread 0 publishes the workgroup's partials
+        __threadfence();
+        is_last = atomicAdd(a.counters + kvh, 1u) == (unsigned)nch - 1u;
+        if (is_last) __threadfence();
     }
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
-    for (int idx = threadIdx.x; idx < G * HD; idx += WG) {
+    float* outs = &red[0][0];   // reused: the G*HD combined outputs
+    for (int idx = t; idx < G * HD; idx += WG) {
         const int h = idx / HD, d = idx - h * HD;
         const int hq = kvh * G + h;
-        float acc = 0.f, z = 0.f;
+        float acc2 = 0.f, z = 0.f;
         for (int i = 0; i < nch; i++) {
-            acc += __builtin_nontemporal_load(a.part_out + ((int64_t)i * a.heads + hq) * HD + d);
+            acc2 += __builtin_nontemporal_load(a.part_out + ((int64_t)i * a.heads + hq) * HD + d);
             z += __builtin_nontemporal_load(a.part_sum + (int64_t)i * a.heads + hq);
         }
-        a.out[(int64_t)hq * HD + d] = acc * (1.0f / z);
+        const float o = acc2 * (1.0f / z);
+        a.out[(int64_t)hq * HD + d] = o;
+        outs[idx] = o;
     }
-    if (threadIdx.x == 0) a.counters[kvh] = 0u;
+    if (t == 0) a.counters[kvh] = 0u;
+    if (a.rec_out) {
+        __syncthreads();
+        constexpr int NU = G * HD / 32;     // units of this kv head's outputs
+        const int ubase = kvh * NU;
+        for (int kb = wave * 2; kb < NU; kb += 8) {
+            const int k = kb + (lane >> 5);
+            const bool act = k < NU;
+            const float v = act ? outs[k * 32 + (lane & 31)] : 0.f;
+            build_xrec(v, v * v, a.rec_out + ubase + (act ? k : 0), act);
+        }
+    }
+}
+
+template <int HD, int G>
+hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
+    const int nchunks = attn_max_chunks(a.heads, a.kv_heads, a.context);
+    dim3 grid(nchunks, a.kv_heads);
+    attn_scores_kernel<HD, G><<<grid, WG, 0, s>>>(a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_pv_kernel<HD, G><<<grid, WG, 0, s>>>(a);
+    return hipGetLastError();
 }
 
 template <int HD>
 hipError_t launch_hd(const AttnArgs& a, hipStream_t s) {
-    const int G = a.heads / a.kv_heads;
-    const int C = attn_chunk(a.heads, a.kv_heads);
-    const int nchunks = attn_max_chunks(a.heads, a.kv_heads, a.context);
-    dim3 grid(nchunks, a.kv_heads);
-    size_t sm1 = sizeof(float) * (size_t)(G * HD + C * (HD + 1));
-    size_t sm2 = sizeof(float) * (size_t)(C * (HD + 1) + G * C);
-    attn_scores_kernel<HD><<<grid, WG, sm1, s>>>(a, C, G);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    attn_pv_kernel<HD><<<grid, WG, sm2, s>>>(a, C, G);
-    return hipGetLastError();
+    switch (a.heads / a.kv_heads) {
+    case 1: return launch_hg<HD, 1>(a, s);
+    case 2: return launch_hg<HD, 2>(a, s);
+    case 4: return launch_hg<HD, 4>(a, s);
+    case 8: return launch_hg<HD, 8>(a, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
 
-int attn_chunk(int heads, int kv_heads) {
-    const int G = heads / kv_heads;
-    return G <= 4 ? 64 : WG / G;
-}
+int attn_chunk(int, int) { return CH; }
 
 int attn_max_chunks(int heads, int kv_heads, int context) {
-    const int C = attn_chunk(heads, kv_heads);
-    return (context + C - 1) / C;
+    (void)heads; (void)kv_heads;
+    return (context + CH - 1) / CH;
+}
+
+bool attn_supported(int heads, int kv_heads, int head_dim) {
+    if (kv_heads <= 0 || heads % kv_heads != 0) return false;
+    const int g = heads / kv_heads;
+    return (g == 1 || g == 2 || g == 4 || g == 8) && (head_dim == 64 || head_dim == 96 || head_dim == 128);
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-    if (a.kv_heads <= 0 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
-    const int G = a.heads / a.kv_heads;
-    if (G > 16) return hipErrorInvalidValue;
-    const int C = attn_chunk(a.heads, a.kv_heads);
-    if ((WG / (G * C)) < 1 || a.head_dim % (WG / (G * C)) != 0) return hipErrorInvalidValue;
+    if (!attn_supported(a.heads, a.kv_heads, a.head_dim)) return hipErrorInvalidValue;
     switch (a.head_dim) {
     case 64: return launch_hd<64>(a, s);
     case 96: return launch_hd<96>(a, s);

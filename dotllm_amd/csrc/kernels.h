@@ -17,17 +17,19 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const i
                         float* out, hipStream_t s);
 
 // ---- gemv.hip ----
-enum GemvPro : int { PRO_NONE = 0, PRO_RMSNORM = 1 };
+struct XRec;   // xrec.h
 enum GemvEpi : int { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 
 struct GemvSeg {
     const uint8_t* w;   // [rows][row_bytes] blocks
+    const uint8_t* w2;  // EPI_SWIGLU: the up matrix (w is the gate)
     float* out;         // rows outputs
     int rows;
+    int groups;         // gemv_groups(rows)
 };
 
 struct ArgmaxState {
-    float* cand_val;      // per workgroup
+    float* cand_val;      // per 32-row group
     int32_t* cand_idx;
     uint32_t* counter;    // zero before launch; the last workgroup resets it
     int32_t* token_out;   // argmax result (next token)
@@ -40,18 +42,28 @@ struct ArgmaxState {
 struct GemvArgs {
     GemvSeg seg[3];
     int nseg;
-    int cols;
-    const float* x;       // input vector (PRO_NONE) or hidden state (PRO_RMSNORM)
-    const float* norm_w;  // PRO_RMSNORM weights
+    int cols;             // reduction length K
+    int splitk;           // K splits per 32-row group (gemv_pick_splitk)
+    const float* x;       // fp32 input (the hidden state when norm != 0)
+    const float* norm_w;  // RmsNorm weights applied on the fly by the fp32 path
+    const XRec* xrec;     // input records (Q4_K path; ssq source when norm != 0)
+    int norm;             // apply RmsNorm (1/rms from the records' ssq)
     float eps;
-    // EPI_SWIGLU: seg[0] = gate, seg[1] = up (equal rows), output to seg[0].out.
+    XRec* rec_out;        // EPI_ADD / EPI_SWIGLU: records of the output vector
+    const float* rec_w;   // norm weights of the output's consumer (nullable)
+    float* partial;       // split-K scratch [groups][splitk][64]
+    uint32_t* counters;   // split-K arrival counters [groups], zero between launches
     ArgmaxState am;       // EPI_ARGMAX
 };
 
-// Number of workgroups launch_gemv will use (for sizing ArgmaxState arrays).
-int gemv_grid(uint32_t type, int epi, const GemvArgs& a);
-hipError_t launch_gemv(uint32_t type, int pro, int epi, const GemvArgs& a, hipStream_t s);
 bool gemv_supported(uint32_t type);
+int gemv_unit_elems(uint32_t type);
+int gemv_groups(int rows);
+int gemv_pick_splitk(uint32_t type, int cols, int rows_total);
+int gemv_grid(const GemvArgs& a);
+hipError_t launch_gemv(uint32_t type, int epi, const GemvArgs& a, hipStream_t s);
+// Records of x (optionally multiplied by norm weights w) for n elements.
+hipError_t launch_make_xrec(const float* x, const float* w, int n, XRec* out, hipStream_t s);
 
 // ---- ops.hip (op-level IComputeBackend members) ----
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, int n, float eps, hipStream_t s);
@@ -84,10 +96,12 @@ struct AttnArgs {
     float* part_sum;        // [max_chunks][heads]
     uint32_t* counters;     // [kv_heads], zero; the last workgroup of each kv head resets its own
     float* out;             // [heads][head_dim]
+    XRec* rec_out;          // records of out (nullable)
     int heads, kv_heads, head_dim, rope_half, context, kv_fp16;
 };
 int attn_chunk(int heads, int kv_heads);
 int attn_max_chunks(int heads, int kv_heads, int context);
+bool attn_supported(int heads, int kv_heads, int head_dim);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 }  // namespace llmdot
