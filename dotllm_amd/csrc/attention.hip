@@ -10,20 +10,21 @@
 //
 // The reference's ExpApprox is not multiplicative, so an online (rescaling)
 // softmax cannot reproduce it; the global max must be known before any
-// exponent.  Two kernels therefore split the sequence into chunks of 64
-// positions per kv head (grid = chunks x kv heads; chunks past T exit):
-//   phase 1: RoPE + KV write + scores of the chunk + per-chunk max (per q head).
+// exponent.  The sequence is split into chunks of 64 positions per kv head
+// (grid = chunks x kv heads; chunks past T exit), over three launches (each
+// reads what the previous wrote, so no fences or atomics are needed):
+//   scores:  RoPE + KV write + scores of the chunk + per-chunk max (per q head).
 //            4 threads per position, each loading a quarter of the K row with
 //            16-byte loads; every K row is read once for all G q heads.
-//   phase 2: global max from the chunk maxima, exponentials, chunk partial
-//            sum(e) and sum(e V) (16-byte V loads), and the last workgroup of
-//            each kv head combines the chunk partials (out = sum(eV) / sum(e))
-//            and writes the activation records for the O projection.
+//   pv:      global max from the chunk maxima, exponentials, chunk partial
+//            sum(e) and sum(e V) (16-byte V loads).
+//   combine: out = sum(eV) / sum(e) over the chunks, one q head per workgroup.
+// Loads carry no branches (positions past T read a written row and are
+// masked), so each thread's loads are all in flight together.
 // cos/sin come from a host table built with the same libm calls as the
 // reference, so RoPE is bit-exact.
 #include "common.h"
 #include "kernels.h"
-#include "xrec.h"
 
 namespace llmdot {
 
@@ -99,20 +100,19 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
     const int c = blockIdx.x, kvh = blockIdx.y;
     const int p0 = c * CH;
     if (p0 >= n) return;
-    const int cnt = min(CH, n - p0);
     const int half = a.rope_half;
     const float* cs = a.cos_tab + (int64_t)T * half;
     const float* sn = a.sin_tab + (int64_t)T * half;
     const int64_t cache_base = (int64_t)kvh * a.context * HD;
 
-    // K row of this thread's position, issued first
+    // this thread's K quarter-row, issued first; positions past T read row p0
+    // (always written) and are masked afterwards
     const int t = threadIdx.x, p = t >> 2, sub = t & 3;
-    const bool live = p < cnt;
-    const bool is_new = p0 + p == T;
+    const int pos = p0 + p;
+    const bool live = pos < n;
+    const bool is_new = pos == T;
     float kv[DPT];
-#pragma unroll
-    for (int d = 0; d < DPT; d++) kv[d] = 0.f;
-    if (live && !is_new) load_kv_row<DPT>(a.kcache, cache_base + (int64_t)(p0 + p) * HD + sub * DPT, a.kv_fp16, kv);
+    load_kv_row<DPT>(a.kcache, cache_base + (int64_t)(live && !is_new ? pos : p0) * HD + sub * DPT, a.kv_fp16, kv);
 
     for (int idx = t; idx < G * HD; idx += WG) {
         const int h = idx / HD, d = idx - h * HD;
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    if (live && is_new) {
+    if (is_new) {
 #pragma unroll
         for (int d = 0; d < DPT; d++) kv[d] = knew[sub * DPT + d];
     }
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
         const float score = s * inv_sqrt;
-        if (live && sub == 0) a.scores[(int64_t)(kvh * G + h) * a.context + p0 + p] = score;
+        if (live && sub == 0) a.scores[(int64_t)(kvh * G + h) * a.context + pos] = score;
         float m = live ? score : -INFINITY;
         m = wave_max(m);
         if (lane == 0) wmax[wave][h] = m;
@@ -159,7 +159,6 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     __shared__ float p_s[G][CH];
     __shared__ float red[4][G * HD];
     __shared__ float gmax[G];
-    __shared__ int is_last;
     const int T = *a.pos, n = T + 1, n8 = n & ~7;
     const int c = blockIdx.x, kvh = blockIdx.y;
     const int p0 = c * CH;
@@ -170,40 +169,39 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     const int dg = t & 15, pg = t >> 4;
     const int64_t cache_base = (int64_t)kvh * a.context * HD;
 
+    // V rows of positions pg + 16 i, issued first (rows past T read row p0)
     float vv[4][DPG];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int p = pg + 16 * i;
-        if (p < cnt) {
-            load_kv_row<DPG>(a.vcache, cache_base + (int64_t)(p0 + p) * HD + dg * DPG, a.kv_fp16, vv[i]);
-        } else {
-#pragma unroll
-            for (int d = 0; d < DPG; d++) vv[i][d] = 0.f;
-        }
+        load_kv_row<DPG>(a.vcache, cache_base + (int64_t)(p0 + (p < cnt ? p : 0)) * HD + dg * DPG, a.kv_fp16, vv[i]);
     }
-    if (t < G) {
-        const float* cm = a.chunk_max + (int64_t)(kvh * G + t) * gridDim.x;
+    // global max of each head's scores (Softmax's max over all n)
+    for (int h = wave; h < G; h += 4) {
+        const float* cm = a.chunk_max + (int64_t)(kvh * G + h) * gridDim.x;
         float m = -INFINITY;
-        for (int i = 0; i < nch; i++) m = fmaxf(m, cm[i]);
-        gmax[t] = m;
+        for (int i = lane; i < nch; i += 64) m = fmaxf(m, cm[i]);
+        m = wave_max(m);
+        if (lane == 0) gmax[h] = m;
     }
     __syncthreads();
     for (int idx = t; idx < G * CH; idx += WG) {
         const int h = idx / CH, p = idx - h * CH;
-        float e = 0.f;
-        if (p < cnt) {
+        const int sidx = p0 + (p < cnt ? p : 0);
+        const float sc = a.scores[(int64_t)(kvh * G + h) * a.context + sidx];
+        float e;
+        {
 #pragma clang fp contract(off)
-            const int sidx = p0 + p;
-            const float x = a.scores[(int64_t)(kvh * G + h) * a.context + sidx] - gmax[h];
+            const float x = sc - gmax[h];
+            // Softmax: ExpApprox on the vector lanes (first 8*floor(n/8)), expf on the tail
             e = sidx < n8 ? exp_approx(x) : expf(x);
         }
-        p_s[h][p] = e;
+        p_s[h][p] = p < cnt ? e : 0.f;
     }
     __syncthreads();
-    if (t < G) {
-        float z = 0.f;
-        for (int p = 0; p < cnt; p++) z += p_s[t][p];
-        a.part_sum[(int64_t)c * a.heads + kvh * G + t] = z;
+    for (int h = wave; h < G; h += 4) {   // this chunk's sum of exponentials
+        const float z = wave_sum(p_s[h][lane]);
+        if (lane == 0) a.part_sum[(int64_t)c * a.heads + kvh * G + h] = z;
     }
 #pragma unroll
     for (int h = 0; h < G; h++) {
@@ -229,39 +227,21 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
         const int h = idx / HD, d = idx - h * HD;
         a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = (red[0][idx] + red[1][idx]) + (red[2][idx] + red[3][idx]);
     }
-    __syncthreads();
-    if (t == 0) {   // one release by thread 0 publishes the workgroup's partials
-        __threadfence();
-        is_last = atomicAdd(a.counters + kvh, 1u) == (unsigned)nch - 1u;
-        if (is_last) __threadfence();
+}
+
+// out = sum_c part_out[c] / sum_c part_sum[c] for one q head per workgroup
+// (a separate launch: the chunk partials are visible without fences).
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
+    const int n = *a.pos + 1;
+    const int nch = (n + CH - 1) / CH;
+    const int hq = blockIdx.x, d = threadIdx.x;
+    float acc = 0.f, z = 0.f;
+    for (int i = 0; i < nch; i++) {
+        acc += a.part_out[((int64_t)i * a.heads + hq) * HD + d];
+        z += a.part_sum[(int64_t)i * a.heads + hq];
     }
-    __syncthreads();
-    if (!is_last) return;
-    float* outs = &red[0][0];   // reused: the G*HD combined outputs
-    for (int idx = t; idx < G * HD; idx += WG) {
-        const int h = idx / HD, d = idx - h * HD;
-        const int hq = kvh * G + h;
-        float acc2 = 0.f, z = 0.f;
-        for (int i = 0; i < nch; i++) {
-            acc2 += __builtin_nontemporal_load(a.part_out + ((int64_t)i * a.heads + hq) * HD + d);
-            z += __builtin_nontemporal_load(a.part_sum + (int64_t)i * a.heads + hq);
-        }
-        const float o = acc2 * (1.0f / z);
-        a.out[(int64_t)hq * HD + d] = o;
-        outs[idx] = o;
-    }
-    if (t == 0) a.counters[kvh] = 0u;
-    if (a.rec_out) {
-        __syncthreads();
-        constexpr int NU = G * HD / 32;     // units of this kv head's outputs
-        const int ubase = kvh * NU;
-        for (int kb = wave * 2; kb < NU; kb += 8) {
-            const int k = kb + (lane >> 5);
-            const bool act = k < NU;
-            const float v = act ? outs[k * 32 + (lane & 31)] : 0.f;
-            build_xrec(v, v * v, a.rec_out + ubase + (act ? k : 0), act);
-        }
-    }
+    a.out[(int64_t)hq * HD + d] = acc * (1.0f / z);
 }
 
 template <int HD, int G>
@@ -272,6 +252,9 @@ hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     attn_pv_kernel<HD, G><<<grid, WG, 0, s>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_combine_kernel<HD><<<a.heads, HD, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -29,7 +29,6 @@
 #include "../../include/llmdot_hip.h"
 #include "common.h"
 #include "kernels.h"
-#include "xrec.h"
 
 using namespace llmdot;
 
@@ -87,13 +86,10 @@ struct llmdot_hip_ctx {
     hipStream_t stream = nullptr;
     std::unordered_map<std::string, Weight> weights;
     DevBuf scratch[6];
-    int32_t* am_ints = nullptr;  // [0] token_out, [1..2] counter + pad
+    int32_t* am_ints = nullptr;  // [0] token_out
     float* am_val = nullptr;
     int32_t* am_idx = nullptr;
     int am_cap = 0;
-    DevBuf gemv_partial;         // split-K partial sums of op-level GEMVs
-    DevBuf gemv_counters;        // split-K arrival counters (kept zero between launches)
-    DevBuf gemv_recs;            // activation records of op-level GEMV inputs
 };
 
 namespace {
@@ -183,9 +179,6 @@ extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->weights) (void)hipFree(kv.second.dev);
     for (auto& b : ctx->scratch) b.release();
-    ctx->gemv_partial.release();
-    ctx->gemv_counters.release();
-    ctx->gemv_recs.release();
     if (ctx->am_ints) (void)hipFree(ctx->am_ints);
     if (ctx->am_val) (void)hipFree(ctx->am_val);
     if (ctx->am_idx) (void)hipFree(ctx->am_idx);
@@ -235,35 +228,15 @@ extern "C" int32_t llmdot_hip_has_weight(llmdot_hip_ctx* ctx, const char* key, i
 
 namespace {
 
-// One GEMV y = W x on the context stream (x, y, W in device memory); builds the
-// activation records Q4_K needs and sizes the split-K scratch.
-int ctx_gemv(llmdot_hip_ctx* ctx, uint32_t type, const uint8_t* w, const float* x, float* y, int rows, int cols,
-             bool records_ready = false) {
-    const int splitk = gemv_pick_splitk(type, cols, rows);
-    if (splitk <= 0) return fail(LLMDOT_E_UNSUPPORTED, "GEMV width " + std::to_string(cols) + " too large for type " + std::to_string(type));
-    const int groups = gemv_groups(rows);
-    HIPCHK(ctx->gemv_partial.ensure(sizeof(float) * 64 * (size_t)groups * splitk));
-    const size_t cbytes = sizeof(uint32_t) * (size_t)groups;
-    if (ctx->gemv_counters.cap < cbytes) {
-        HIPCHK(ctx->gemv_counters.ensure(cbytes));
-        HIPCHK(hipMemset(ctx->gemv_counters.p, 0, ctx->gemv_counters.cap));
-    }
+// One GEMV y = W x on the context stream (x, y, W in device memory).
+int ctx_gemv(llmdot_hip_ctx* ctx, uint32_t type, const uint8_t* w, const float* x, float* y, int rows, int cols) {
+    if (!gemv_width_ok(type, cols))
+        return fail(LLMDOT_E_UNSUPPORTED, "GEMV width " + std::to_string(cols) + " not supported for type " + std::to_string(type));
     GemvArgs ga{};
     ga.nseg = 1;
-    ga.seg[0] = {w, nullptr, y, rows, groups};
+    ga.seg[0] = {w, nullptr, y, rows, 0};
     ga.cols = cols;
-    ga.splitk = splitk;
     ga.x = x;
-    ga.partial = (float*)ctx->gemv_partial.p;
-    ga.counters = (uint32_t*)ctx->gemv_counters.p;
-    if (type == GGML_Q4_K) {
-        if (cols % 32) return fail(LLMDOT_E_UNSUPPORTED, "Q4_K width must be a multiple of 256");
-        if (!records_ready) {
-            HIPCHK(ctx->gemv_recs.ensure(sizeof(XRec) * (size_t)(cols / 32)));
-            HIPCHK(launch_make_xrec(x, nullptr, cols, (XRec*)ctx->gemv_recs.p, ctx->stream));
-        }
-        ga.xrec = (const XRec*)ctx->gemv_recs.p;
-    }
     HIPCHK(launch_gemv(type, EPI_STORE, ga, ctx->stream));
     return 0;
 }
@@ -288,8 +261,8 @@ int matmul_common(llmdot_hip_ctx* ctx, const float* a, const void* b, float* res
     if (a_cols <= 0 || b_cols <= 0 || result_len < b_cols || result_len % b_cols != 0)
         return fail(LLMDOT_E_INVALID, "bad MatMul shape");
     if (!gemv_supported(type)) return fail(LLMDOT_E_UNSUPPORTED, "MatMul: unsupported weight type " + std::to_string(type));
-    if (a_cols % block_elems(type) != 0 || (type != GGML_F32 && type != GGML_F16 && a_cols % (type == GGML_Q6_K ? 64 : 32) != 0))
-        return fail(LLMDOT_E_UNSUPPORTED, "MatMul: width not a multiple of the block size");
+    if (a_cols % block_elems(type) != 0) return fail(LLMDOT_E_UNSUPPORTED, "MatMul: width not a multiple of the block size");
+    if (!gemv_width_ok(type, a_cols)) return fail(LLMDOT_E_UNSUPPORTED, "MatMul: width " + std::to_string(a_cols) + " too large");
     if (int rc = ensure_device(ctx)) return rc;
     const Weight* w = nullptr;
     Weight tmp;
@@ -474,7 +447,7 @@ extern "C" int32_t llmdot_hip_argmax(llmdot_hip_ctx* ctx, const float* input, in
     if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
     ArgmaxState st{};
     st.cand_val = ctx->am_val; st.cand_idx = ctx->am_idx;
-    st.token_out = ctx->am_ints; st.counter = reinterpret_cast<uint32_t*>(ctx->am_ints + 1);
+    st.cap = ctx->am_cap; st.token_out = ctx->am_ints;
     HIPCHK(launch_argmax(dx, n, st, ctx->stream));
     return copy_out(ctx, index, ctx->am_ints, sizeof(int32_t));
 }
@@ -522,7 +495,6 @@ extern "C" int32_t llmdot_hip_time_gemv(llmdot_hip_ctx* ctx, uint32_t type, cons
                                         float* ms) {
     if (!ctx || !w_devs || n_weights <= 0 || iters <= 0 || !ms) return fail(LLMDOT_E_INVALID, "bad timing arguments");
     if (!gemv_supported(type)) return fail(LLMDOT_E_UNSUPPORTED, "unsupported gemv type");
-    // records of x (Q4_K) are built once, outside the timed region
     if (int rc = ctx_gemv(ctx, type, reinterpret_cast<const uint8_t*>(w_devs[0]), x_dev, y_dev, rows, cols)) return rc;
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0));
@@ -530,7 +502,7 @@ extern "C" int32_t llmdot_hip_time_gemv(llmdot_hip_ctx* ctx, uint32_t type, cons
     HIPCHK(hipEventRecord(e0, ctx->stream));
     for (int i = 0; i < iters; i++)
         if (int rc = ctx_gemv(ctx, type, reinterpret_cast<const uint8_t*>(w_devs[i % n_weights]), x_dev, y_dev, rows,
-                              cols, true))
+                              cols))
             return rc;
     HIPCHK(hipEventRecord(e1, ctx->stream));
     HIPCHK(hipEventSynchronize(e1));
@@ -568,17 +540,12 @@ struct llmdot_hip_model {
     int rope_half = 0;
     // attention scratch
     float *scores = nullptr, *chunk_max = nullptr, *part_out = nullptr, *part_sum = nullptr;
-    uint32_t* attn_counters = nullptr;
-    // activation records of the GEMV inputs (xrec.h)
-    XRec *rec_h = nullptr, *rec_attn = nullptr, *rec_act = nullptr;
-    // split-K scratch shared by the step's GEMVs (they run one after another)
-    float* gemv_partial = nullptr;
-    uint32_t* gemv_counters = nullptr;
-    // argmax + device-side loop state: ints[0] token, [1] pos, [2] step, [3] counter
+    // argmax + device-side loop state: ints[0] token, [1] pos, [2] step
     int32_t* ints = nullptr;
     int32_t* token_log = nullptr;
     float* am_val = nullptr;
     int32_t* am_idx = nullptr;
+    int am_cap = 0;
     hipGraphExec_t graph = nullptr;
     bool use_graph = true;
     // per-kernel timing (eager mode only)
@@ -631,24 +598,14 @@ int norm_f32(llmdot_hip_model* m, const Weight* w, int n, float** out) {
 
 int check_gemv_type(const Weight* w, const std::string& name) {
     if (!gemv_supported(w->type)) return fail(LLMDOT_E_UNSUPPORTED, "tensor " + name + ": unsupported type " + std::to_string(w->type));
-    const int ue = gemv_unit_elems(w->type);
-    if (w->cols % ue != 0) return fail(LLMDOT_E_UNSUPPORTED, "tensor " + name + ": width not a multiple of " + std::to_string(ue));
-    if (gemv_pick_splitk(w->type, (int)w->cols, (int)w->rows) <= 0)
-        return fail(LLMDOT_E_UNSUPPORTED, "tensor " + name + ": width too large for the GEMV kernel");
+    if (w->cols % 32 != 0 || !gemv_width_ok(w->type, (int)w->cols))
+        return fail(LLMDOT_E_UNSUPPORTED, "tensor " + name + ": width " + std::to_string(w->cols) + " not supported by the GEMV kernel");
     return 0;
 }
 
-// GEMV launch on the model stream with the step's shared split-K scratch;
-// the dominant launches are bracketed with HIP events in timing mode.
+// GEMV launch on the model stream; the dominant launches are bracketed with
+// HIP events in timing mode.
 hipError_t step_gemv(llmdot_hip_model* m, uint32_t type, int epi, GemvArgs& a, bool dominant) {
-    int rows_total = 0;
-    for (int i = 0; i < a.nseg; i++) {
-        a.seg[i].groups = gemv_groups(a.seg[i].rows);
-        rows_total += a.seg[i].rows;
-    }
-    a.splitk = gemv_pick_splitk(type, a.cols, rows_total);
-    a.partial = m->gemv_partial;
-    a.counters = m->gemv_counters;
     a.eps = m->d.eps;
     hipStream_t s = m->ctx->stream;
     if (m->timing && dominant && m->ev_used + 2 <= (int)m->ev.size()) {
@@ -669,7 +626,6 @@ int enqueue_step(llmdot_hip_model* m) {
     hipStream_t s = m->ctx->stream;
     const int qdim = d.heads * d.head_dim, kvdim = d.kv_heads * d.head_dim;
     HIPCHK(launch_embed(m->embd->dev, m->embd->type, d.hidden, m_token(m), m->h, s));
-    HIPCHK(launch_make_xrec(m->h, m->L[0].attn_norm_f, d.hidden, m->rec_h, s));
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
         // Q, K, V projections over RmsNorm(h) (IE:185-186, IE:333-353); same-type tensors share a launch.
@@ -680,7 +636,7 @@ int enqueue_step(llmdot_hip_model* m) {
         for (int i = 0; i < 3; i++) {
             if (done[i]) continue;
             GemvArgs ga{};
-            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.attn_norm_f; ga.xrec = m->rec_h; ga.norm = 1;
+            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.attn_norm_f; ga.norm = 1;
             for (int j = i; j < 3; j++)
                 if (!done[j] && mats[j]->type == mats[i]->type) {
                     ga.seg[ga.nseg++] = {mats[j]->dev, nullptr, outs[j], rows[j], 0};
@@ -694,38 +650,34 @@ int enqueue_step(llmdot_hip_model* m) {
         aa.vcache = m->vcache + (size_t)l * m->kv_layer_bytes;
         aa.cos_tab = m->cos_tab; aa.sin_tab = m->sin_tab; aa.pos = m_pos(m);
         aa.scores = m->scores; aa.chunk_max = m->chunk_max; aa.part_out = m->part_out; aa.part_sum = m->part_sum;
-        aa.counters = m->attn_counters; aa.out = m->attn; aa.rec_out = m->rec_attn;
+        aa.out = m->attn;
         aa.heads = d.heads; aa.kv_heads = d.kv_heads; aa.head_dim = d.head_dim; aa.rope_half = m->rope_half;
         aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
         HIPCHK(launch_attention(aa, s));
-        {   // O projection + residual (IE:444-449, IE:189); records of h for the FFN RmsNorm
+        {   // O projection + residual (IE:444-449, IE:189)
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.o->dev, nullptr, m->h, d.hidden, 0};
-            ga.cols = qdim; ga.x = m->attn; ga.xrec = m->rec_attn;
-            ga.rec_out = m->rec_h; ga.rec_w = w.ffn_norm_f;
+            ga.cols = qdim; ga.x = m->attn;
             HIPCHK(step_gemv(m, w.o->type, EPI_ADD, ga, false));
         }
         {   // gate/up over RmsNorm(h), SiLU(gate) * up (IE:190, IE:463-474)
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.gate->dev, w.up->dev, m->act, d.ffn, 0};
-            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.ffn_norm_f; ga.xrec = m->rec_h; ga.norm = 1;
-            ga.rec_out = m->rec_act;
+            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.ffn_norm_f; ga.norm = 1;
             HIPCHK(step_gemv(m, w.gate->type, EPI_SWIGLU, ga, true));
         }
-        {   // down projection + residual (IE:475, IE:195); records of h for the next RmsNorm
+        {   // down projection + residual (IE:475, IE:195)
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.down->dev, nullptr, m->h, d.hidden, 0};
-            ga.cols = d.ffn; ga.x = m->act; ga.xrec = m->rec_act;
-            ga.rec_out = m->rec_h; ga.rec_w = l + 1 < d.layers ? m->L[l + 1].attn_norm_f : m->out_norm_f;
+            ga.cols = d.ffn; ga.x = m->act;
             HIPCHK(step_gemv(m, w.down->type, EPI_ADD, ga, false));
         }
     }
     {   // final RmsNorm + LM head + greedy ArgMax (IE:575-602, Sampler.cs:26-27)
         GemvArgs ga{};
         ga.nseg = 1; ga.seg[0] = {m->out->dev, nullptr, m->logits, d.vocab, 0};
-        ga.cols = d.hidden; ga.x = m->h; ga.norm_w = m->out_norm_f; ga.xrec = m->rec_h; ga.norm = 1;
-        ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx;
-        ga.am.counter = reinterpret_cast<uint32_t*>(m->ints + 3);
+        ga.cols = d.hidden; ga.x = m->h; ga.norm_w = m->out_norm_f; ga.norm = 1;
+        ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx; ga.am.cap = m->am_cap;
         ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
         ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
         HIPCHK(step_gemv(m, m->out->type, EPI_ARGMAX, ga, false));
@@ -880,35 +832,13 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     if ((rc = A(sizeof(float) * (size_t)d.heads * nch, &p))) return bail(rc); m->chunk_max = (float*)p;
     if ((rc = A(sizeof(float) * (size_t)nch * qdim, &p))) return bail(rc); m->part_out = (float*)p;
     if ((rc = A(sizeof(float) * (size_t)nch * d.heads, &p))) return bail(rc); m->part_sum = (float*)p;
-    if ((rc = A(sizeof(uint32_t) * (size_t)d.kv_heads, &p))) return bail(rc); m->attn_counters = (uint32_t*)p;
     if ((rc = A(64, &p))) return bail(rc); m->ints = (int32_t*)p;
     if ((rc = A(sizeof(int32_t) * (size_t)(d.context + 1), &p))) return bail(rc); m->token_log = (int32_t*)p;
     {
-        const int g = gemv_groups(d.vocab);
+        const int g = gemv_max_grid(m->out->type, EPI_ARGMAX, d.vocab, d.hidden);
+        m->am_cap = g;
         if ((rc = A(sizeof(float) * (size_t)g, &p))) return bail(rc); m->am_val = (float*)p;
         if ((rc = A(sizeof(int32_t) * (size_t)g, &p))) return bail(rc); m->am_idx = (int32_t*)p;
-    }
-    {   // activation records and split-K scratch
-        if ((rc = A(sizeof(XRec) * (size_t)(d.hidden / 32), &p))) return bail(rc); m->rec_h = (XRec*)p;
-        if ((rc = A(sizeof(XRec) * (size_t)(qdim / 32), &p))) return bail(rc); m->rec_attn = (XRec*)p;
-        if ((rc = A(sizeof(XRec) * (size_t)(d.ffn / 32), &p))) return bail(rc); m->rec_act = (XRec*)p;
-        size_t part = 0;
-        int groups = 0;
-        auto plan = [&](const Weight* w, int rows_total) {
-            const int sk = gemv_pick_splitk(w->type, (int)w->cols, rows_total);
-            const int gr = gemv_groups(rows_total) + 3;   // segments round up separately
-            part = std::max(part, (size_t)gr * sk * 64);
-            groups = std::max(groups, gr);
-        };
-        for (const auto& w : m->L) {
-            plan(w.q, qdim + 2 * kvdim);
-            plan(w.o, d.hidden);
-            plan(w.gate, d.ffn);
-            plan(w.down, d.hidden);
-        }
-        plan(m->out, d.vocab);
-        if ((rc = A(sizeof(float) * part, &p))) return bail(rc); m->gemv_partial = (float*)p;
-        if ((rc = A(sizeof(uint32_t) * (size_t)groups, &p))) return bail(rc); m->gemv_counters = (uint32_t*)p;
     }
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return bail(fail(LLMDOT_E_DEVICE, "synchronize failed"));
     if ((rc = build_graph(m))) {

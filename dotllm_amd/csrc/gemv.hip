@@ -4,44 +4,59 @@
 // src/Llmdot.Core/Tensors/TensorOps.cs:60-90, fused per-type kernels TO:118-431).
 // The weight blocks are read once from HBM in their GGUF layout.
 //
-// Decomposition.  A workgroup (4 wavefronts) owns a group of 32 consecutive
-// output rows and a slice of the reduction dimension (split-K); each wavefront
-// owns 8 of the rows, processed as 2 tiles of 4 rows (4 tiles of 2 gate + 2 up
-// rows for the SwiGLU form).  The 64 lanes stride over the slice in "units" (a
-// 32-element sub-block, 64 for Q6_K); a lane's units are fixed for the whole
-// workgroup, so its activations are loaded once and stay in registers while
-// all rows stream through.  A tile's 4 row sums are reduced across the
-// wavefront with a transposing butterfly (7 shuffles).  With split-K the
-// per-split partial sums go to a scratch buffer and the last workgroup of the
-// group (atomic counter) adds them in split order, so results do not depend
-// on scheduling.
+// Decomposition.  A workgroup owns a few consecutive output rows and the whole
+// reduction dimension.  It has ceil(U/64) wavefronts, U being the number of
+// 32-element "units" of a row, and lane L of wavefront w owns unit 64w + L in
+// every row, so a lane's activations are loaded once and stay in registers
+// while the rows stream through.  Rows go in batches (8 rows, or 4 gate + 4 up
+// rows for the SwiGLU form; fewer for the wide types); the loads of batch b+1
+// are issued before batch b is computed, so every wavefront keeps two batches
+// of loads in flight.  A row's lane partials are summed over 16-lane rows with
+// DPP rotations, then over quarter-wavefronts and wavefronts through LDS, in a
+// fixed order.  The loads carry no branches (lanes past the end of a row read
+// unit 0 and contribute 0), so the compiler keeps them all in flight.  Workgroups
+// do not communicate (no fences or atomics).
 //
-// Arithmetic.  Q4_K (the reference's own layout) runs on v_dot8_i32_i4 against
-// the activation records of xrec.h: weight nibble ^ 8 = q - 8 as int4, four
-// dot8 per 8 elements, exact int32; per sub-block the result is scaled by
-// (d*sc) and the dmin*m term uses the record's sum.  The other types
-// dequantise in registers (v_cvt_f32_ubyte*) and accumulate in fp32.
+// Arithmetic.  Q4_K (the reference's own layout) runs on v_dot8_i32_i4.  Each
+// lane quantises its 32 activations v (times the norm weight) to 16 bits,
+// X = rint(v / s) with s = max|v| / 30000, and splits X into four signed-nibble
+// planes: X + 0x8888 has the digits t_p + 8, so the planes hold t_p directly
+// after an XOR with 8 (X = sum_p 16^p t_p).  The weight nibble ^ 8 is q - 8 as
+// an int4, so four dot8 per 8 elements give sum (q-8) X exactly in int32; the
+// sub-block result is (d*sc) * s * S - (dmin*m) * sum(v).  The quantisation
+// error is at most s/2 per element.  The other types dequantise in registers
+// and accumulate in fp32.  RmsNorm of the input (VectorMath.RmsNorm,
+// VM:308-340) is folded in: the lanes multiply by the norm weight, the
+// workgroup reduces sum(h^2), and each row sum is scaled by 1/rms at the end.
 //
-// Epilogues: STORE; ADD (residual h += y, VectorMath.Add VM:27-42, plus the
-// records of the new h for the next consumer's RmsNorm); SWIGLU
-// (SiluInPlace(gate) * up, IE:463-474, VM:118-135, plus the records of the
-// result); ARGMAX (logits plus ArgMax VM:412-425, last-workgroup reduction).
+// Epilogues: STORE; ADD (residual h += y, VectorMath.Add VM:27-42); SWIGLU
+// (SiluInPlace(gate) * up, IE:463-474, VM:118-135); ARGMAX (logits plus
+// ArgMax VM:412-425: one candidate per workgroup, reduced by a second launch).
 #include "common.h"
 #include "kernels.h"
-#include "xrec.h"
+
+#include <stdlib.h>
+
+#include <type_traits>
 
 namespace llmdot {
 
 namespace {
 
-constexpr int WG = 256;
-constexpr int GROUP = 32;
+constexpr int MAXW = 8;   // wavefronts per workgroup: U <= 512 units
 
 __device__ __forceinline__ float h16(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 __device__ __forceinline__ float ub(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
 __device__ __forceinline__ float sb(uint32_t w, int k) { return (float)(int8_t)(w >> (8 * k)); }
+
+// fp16 value at a 2-byte-aligned address (it never straddles a dword).
+__device__ __forceinline__ uint32_t ld_h16_bits(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    return (w >> (8 * (a & 2))) & 0xFFFFu;
+}
 
 // 6-bit scale and min of sub-block g from the 96-bit LSB-first stream in
 // header words y, z, w (DequantizeK.Extract6Bit, DK:189-199).
@@ -54,480 +69,525 @@ __device__ __forceinline__ void kscale(uint32_t y, uint32_t z, uint32_t w, int g
     m = (float)((f >> 6) & 63u);
 }
 
-// ---- integer path (Q4_K) ------------------------------------------------------
-struct XI {           // a lane's activation record for one unit (s, sum already times 1/rms)
-    uint32_t pl[16];
-    float s, sum;
+struct __attribute__((aligned(4))) u32x3 { uint32_t x, y, z; };
+
+// Dword-aligned raw words covering [p, p + 4N) for a 2-byte-aligned p;
+// word i of the span is (*this)[i].
+template <int N>
+struct RawW {
+    uint32_t w[N + 1];
+    uint32_t sh;
+    __device__ __forceinline__ void load(const uint8_t* p) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+        sh = (uint32_t)(a & 3u);
+        if constexpr (N + 1 == 3) {
+            const u32x3 v = *reinterpret_cast<const u32x3*>(base);
+            w[0] = v.x; w[1] = v.y; w[2] = v.z;
+        } else {
+#pragma unroll
+            for (int i = 0; i + 4 <= N + 1; i += 4) {
+                const u32x4 v = ld16_a4(base + 4 * i);
+                w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+            }
+#pragma unroll
+            for (int i = ((N + 1) / 4) * 4; i < N + 1; i++) w[i] = ld4_a4(base + 4 * i);
+        }
+    }
+    __device__ __forceinline__ uint32_t operator[](int i) const { return __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh); }
 };
 
-__device__ __forceinline__ float q4k_int(const uint8_t* row, int u, const XI& x) {
-    const uint8_t* blk = row + (u >> 3) * 144;
-    const int g = u & 7;
-    const u32x4 h = ld16_a4(blk);
-    const u32x4 q = ld16_a4(blk + 16 + 16 * g);
-    const uint32_t w[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
-    int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+// ---- activations of one lane -----------------------------------------------------
+
+struct XQ {            // Q4_K path
+    uint32_t pl[16];   // pl[4p + j]: nibble k = digit p of X[8j + k] as a signed int4
+    float s, sum;      // v ~= s * X;  sum = sum(v)
+};
+
+__device__ __forceinline__ void quantize32(const float* v, XQ& q) {
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    const float scale = amax > 0.f ? 30000.0f / amax : 0.f;
+    q.s = amax > 0.f ? amax / 30000.0f : 0.f;
+    q.sum = sum;
+    uint32_t Y[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        // rint through the 1.5 * 2^23 constant: the low bits of the sum hold X
+        // (|v * scale| <= 30000 + rounding), so Y = X + 0x8888 lies in [0, 65535].
+        const float f = v[i] * scale + 12582912.0f;
+        Y[i] = __float_as_uint(f) - (0x4B400000u - 0x8888u);
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        a0 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[j], a0, false);
-        a1 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 + j], a1, false);
-        a2 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[8 + j], a2, false);
-        a3 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[12 + j], a3, false);
+        const uint32_t* y = Y + 8 * j;
+        const uint32_t q02 = y[0] | (y[2] << 16), q46 = y[4] | (y[6] << 16);
+        const uint32_t q13 = y[1] | (y[3] << 16), q57 = y[5] | (y[7] << 16);
+        // byte i of E / O: low byte of Y[2i] / Y[2i+1]; Eh / Oh the high bytes
+        const uint32_t E = __builtin_amdgcn_perm(q46, q02, 0x06040200u);
+        const uint32_t Eh = __builtin_amdgcn_perm(q46, q02, 0x07050301u);
+        const uint32_t O = __builtin_amdgcn_perm(q57, q13, 0x06040200u);
+        const uint32_t Oh = __builtin_amdgcn_perm(q57, q13, 0x07050301u);
+        const uint32_t m = 0x0F0F0F0Fu;
+        q.pl[0 + j] = ((E & m) | ((O << 4) & ~m)) ^ 0x88888888u;
+        q.pl[4 + j] = (((E >> 4) & m) | (O & ~m)) ^ 0x88888888u;
+        q.pl[8 + j] = ((Eh & m) | ((Oh << 4) & ~m)) ^ 0x88888888u;
+        q.pl[12 + j] = (((Eh >> 4) & m) | (Oh & ~m)) ^ 0x88888888u;
     }
-    const int S = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);
-    float sc, m;
-    kscale(h.y, h.z, h.w, g, sc, m);
-    const float d = h16(h.x & 0xFFFFu), dm = h16(h.x >> 16);
-    return (d * sc) * (x.s * (float)S) - (dm * m) * x.sum;
 }
 
-// ---- fp32 path decoders ------------------------------------------------------------
-// Unit u of a row; x holds the unit's UE activations in the unit's element
-// order; xs the NS partial sums the type's offset needs.
+// fp32 path: the unit's 32 activations in its element order, and the sums
+// its offsets need.
+template <int NS>
+struct XF {
+    float v[32];
+    float s[NS];
+};
 
-struct UQ5K {  // reference Q5_K: 176 B / 256; unit = sub-block g
-    static constexpr int UE = 32, NS = 1;
-    __device__ static int xoff(int u, int run) { return u * 32 + run * 16; }
-    __device__ static float dot(const uint8_t* row, int u, const float* x, const float* xs) {
+// ---- per-type row units -----------------------------------------------------------
+// RUN: contiguous elements per run of a unit; xoff(u, run) its first element.
+
+struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
+    static constexpr int RB = 8, NS = 1, PRE = 2;
+    struct Raw { u32x4 h, q; };
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const uint8_t* blk = row + (u >> 3) * 144;
+        r.h = ld16_a4(blk);
+        r.q = ld16_a4(blk + 16 + 16 * (u & 7));
+    }
+    __device__ static float dot(const Raw& r, int u, const XQ& x) {
+        const uint32_t w[4] = {r.q.x ^ 0x88888888u, r.q.y ^ 0x88888888u, r.q.z ^ 0x88888888u, r.q.w ^ 0x88888888u};
+        int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a0 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[j], a0, false);
+            a1 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 + j], a1, false);
+            a2 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[8 + j], a2, false);
+            a3 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[12 + j], a3, false);
+        }
+        const int S = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);
+        float sc, m;
+        kscale(r.h.y, r.h.z, r.h.w, u & 7, sc, m);
+        const float d = h16(r.h.x & 0xFFFFu), dm = h16(r.h.x >> 16);
+        return (d * sc) * (x.s * (float)S) - (dm * m) * x.sum;
+    }
+};
+
+struct TQ5K {   // reference Q5_K, 176 B / 256: unit = sub-block g
+    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 2;
+    struct Raw { u32x4 h, q; uint32_t qh; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
         const uint8_t* blk = row + (u >> 3) * 176;
         const int g = u & 7;
-        const u32x4 h = ld16_a4(blk);
-        const uint32_t qh = ld4_a4(blk + 16 + 4 * g);
-        const u32x4 q = ld16_a4(blk + 48 + 16 * g);
+        r.h = ld16_a4(blk);
+        r.qh = ld4_a4(blk + 16 + 4 * g);
+        r.q = ld16_a4(blk + 48 + 16 * g);
+    }
+    __device__ static float dot(const Raw& r, int u, const XF<NS>& x) {
         float sc, m;
-        kscale(h.y, h.z, h.w, g, sc, m);
-        const float d = h16(h.x & 0xFFFFu), dm = h16(h.x >> 16);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        kscale(r.h.y, r.h.z, r.h.w, u & 7, sc, m);
+        const float d = h16(r.h.x & 0xFFFFu), dm = h16(r.h.x >> 16);
+        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t hb = qh >> (8 * j);
+            const uint32_t hb = r.qh >> (8 * j);
             // bits 0,2,4,6 of hb -> bit 4 of bytes 0..3 (even elements), bits 1,3,5,7 -> odd
             const uint32_t he = ((hb & 0x55u) * 0x410410u) & 0x10101010u;
             const uint32_t ho = (((hb >> 1) & 0x55u) * 0x410410u) & 0x10101010u;
             const uint32_t e = (w[j] & 0x0F0F0F0Fu) | he, o = ((w[j] >> 4) & 0x0F0F0F0Fu) | ho;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                s0 += x[8 * j + 2 * k] * ub(e, k);
-                s1 += x[8 * j + 2 * k + 1] * ub(o, k);
+                s0 += x.v[8 * j + 2 * k] * ub(e, k);
+                s1 += x.v[8 * j + 2 * k + 1] * ub(o, k);
             }
         }
-        return (d * sc) * ((s0 + s1) - 16.f * xs[0]) - (dm * m) * xs[0];
+        return (d * sc) * ((s0 + s1) - 16.f * x.s[0]) - (dm * m) * x.s[0];
     }
 };
 
-struct UQ6K {  // Q6_K: 210 B / 256; unit = (half n, l-range l0..l0+15) -> 64 elements
-    static constexpr int UE = 64, NS = 4;
-    // run t (0..3) of 16 elements: n + l0 + 32 t + [0, 16)
-    __device__ static int xoff(int u, int t) {
-        const int sub = u & 3;
-        return (u >> 2) * 256 + (sub >> 1) * 128 + (sub & 1) * 16 + 32 * t;
+// Q6_K, 210 B / 256 (ql[128], qh[64], sc[16], d).  Unit u of a block: half
+// n = 128 ((u >> 2) & 1), l-range l0 = 8 (u & 3) .. l0 + 7, four runs t = 0..3 of 8
+// elements at n + l0 + 32 t (the q1..q4 groups of the reference loop).
+struct TQ6K {
+    static constexpr int RB = 4, NS = 4, RUN = 8, PRE = 1;   // PRE: batches issued before the activations' arithmetic
+    // A, B: ql bytes of runs 0/2 and 1/3; C: qh bytes; S: scales.  A, B, C sit
+    // at multiples of 8 from the 2-aligned block start and share one shift.
+    struct Raw { uint32_t A[3], B[3], C[3], S[3], d, sh; };
+    __device__ static int xoff(int u, int t) { return (u >> 3) * 256 + ((u >> 2) & 1) * 128 + (u & 3) * 8 + 32 * t; }
+    __device__ static void ld3(uint32_t* w, const uint8_t* p) {
+        const u32x3 v = *reinterpret_cast<const u32x3*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+        w[0] = v.x; w[1] = v.y; w[2] = v.z;
     }
-    __device__ static float dot(const uint8_t* row, int u, const float* x, const float* xs) {
-        const uint8_t* blk = row + (u >> 2) * 210;
-        const int sub = u & 3, n = (sub >> 1) * 128, l0 = (sub & 1) * 16;
-        uint32_t A[4], B[4], C[4], S[2], Dw[1];
-        ld_realign<4>(blk + n / 2 + l0, A);
-        ld_realign<4>(blk + n / 2 + l0 + 32, B);
-        ld_realign<4>(blk + 128 + n / 4 + l0, C);
-        ld_realign<2>(blk + 192 + n / 16 + l0 / 16, S);
-        ld_realign<1>(blk + 208, Dw);
-        const float d = h16(Dw[0] & 0xFFFFu);
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const uint8_t* blk = row + (u >> 3) * 210;
+        const int half = (u >> 2) & 1, l0 = (u & 3) * 8;
+        const uint8_t* ps = blk + 192 + 8 * half + (l0 >> 4);
+        ld3(r.A, blk + 64 * half + l0);
+        ld3(r.B, blk + 64 * half + l0 + 32);
+        ld3(r.C, blk + 128 + 32 * half + l0);
+        ld3(r.S, ps);
+        r.d = ld_h16_bits(blk + 208);
+        r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u) | ((uint32_t)(reinterpret_cast<uintptr_t>(ps) & 3u) << 8);
+    }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
+        const float d = h16(r.d);
+        const uint32_t sa = r.sh & 3u, ss = r.sh >> 8;
         float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t q0 = (A[j] & 0x0F0F0F0Fu) | ((C[j] & 0x03030303u) << 4);
-            const uint32_t q1 = (B[j] & 0x0F0F0F0Fu) | ((C[j] & 0x0C0C0C0Cu) << 2);
-            const uint32_t q2 = ((A[j] >> 4) & 0x0F0F0F0Fu) | (C[j] & 0x30303030u);
-            const uint32_t q3 = ((B[j] >> 4) & 0x0F0F0F0Fu) | ((C[j] >> 2) & 0x30303030u);
+        for (int j = 0; j < 2; j++) {
+            const uint32_t A = __builtin_amdgcn_alignbyte(r.A[j + 1], r.A[j], sa);
+            const uint32_t B = __builtin_amdgcn_alignbyte(r.B[j + 1], r.B[j], sa);
+            const uint32_t C = __builtin_amdgcn_alignbyte(r.C[j + 1], r.C[j], sa);
+            const uint32_t q0 = (A & 0x0F0F0F0Fu) | ((C & 0x03030303u) << 4);
+            const uint32_t q1 = (B & 0x0F0F0F0Fu) | ((C & 0x0C0C0C0Cu) << 2);
+            const uint32_t q2 = ((A >> 4) & 0x0F0F0F0Fu) | (C & 0x30303030u);
+            const uint32_t q3 = ((B >> 4) & 0x0F0F0F0Fu) | ((C >> 2) & 0x30303030u);
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                s[0] += x[0 * 16 + 4 * j + k] * ub(q0, k);
-                s[1] += x[1 * 16 + 4 * j + k] * ub(q1, k);
-                s[2] += x[2 * 16 + 4 * j + k] * ub(q2, k);
-                s[3] += x[3 * 16 + 4 * j + k] * ub(q3, k);
+                s[0] += x.v[0 * 8 + 4 * j + k] * ub(q0, k);
+                s[1] += x.v[1 * 8 + 4 * j + k] * ub(q1, k);
+                s[2] += x.v[2 * 8 + 4 * j + k] * ub(q2, k);
+                s[3] += x.v[3 * 8 + 4 * j + k] * ub(q3, k);
             }
         }
-        float r = 0.f;
+        const uint32_t S0 = __builtin_amdgcn_alignbyte(r.S[1], r.S[0], ss);
+        const uint32_t S1 = __builtin_amdgcn_alignbyte(r.S[2], r.S[1], ss);
+        const uint32_t S[2] = {S0, S1};
+        float res = 0.f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) r += (d * sb(S[t >> 1], 2 * (t & 1))) * (s[t] - 32.f * xs[t]);
-        return r;
+        for (int t = 0; t < 4; t++) res += (d * sb(S[t >> 1], 2 * (t & 1))) * (s[t] - 32.f * x.s[t]);
+        return res;
     }
 };
 
-struct UQ8_0 {  // Q8_0: 34 B / 32; unit = block
-    static constexpr int UE = 32, NS = 0;
-    __device__ static int xoff(int u, int run) { return u * 32 + run * 16; }
-    __device__ static float dot(const uint8_t* row, int u, const float* x, const float*) {
+struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block
+    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2;
+    struct Raw { RawW<8> Q; uint32_t d; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
         const uint8_t* blk = row + u * 34;
-        uint32_t Dw[1], Q[8];
-        ld_realign<1>(blk, Dw);
-        ld_realign<8>(blk + 2, Q);
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j += 2)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                s0 += x[4 * j + k] * sb(Q[j], k);
-                s1 += x[4 * j + 4 + k] * sb(Q[j + 1], k);
-            }
-        return h16(Dw[0] & 0xFFFFu) * (s0 + s1);
+        r.d = ld_h16_bits(blk);
+        r.Q.load(blk + 2);
     }
-};
-
-struct UQ4_0 {  // Q4_0: 18 B / 32; unit = block; low nibbles -> j, high -> j + 16
-    static constexpr int UE = 32, NS = 1;
-    __device__ static int xoff(int u, int run) { return u * 32 + run * 16; }
-    __device__ static float dot(const uint8_t* row, int u, const float* x, const float* xs) {
-        const uint8_t* blk = row + u * 18;
-        uint32_t Dw[1], Q[4];
-        ld_realign<1>(blk, Dw);
-        ld_realign<4>(blk + 2, Q);
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t lo = Q[j] & 0x0F0F0F0Fu, hi = (Q[j] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                s0 += x[4 * j + k] * ub(lo, k);
-                s1 += x[16 + 4 * j + k] * ub(hi, k);
-            }
-        }
-        return h16(Dw[0] & 0xFFFFu) * ((s0 + s1) - 8.f * xs[0]);
-    }
-};
-
-struct UF32 {
-    static constexpr int UE = 32, NS = 0;
-    __device__ static int xoff(int u, int run) { return u * 32 + run * 16; }
-    __device__ static float dot(const uint8_t* row, int u, const float* x, const float*) {
-        const float4* p = reinterpret_cast<const float4*>(row + (int64_t)u * 128);
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-            const float4 a = p[j], b = p[j + 1];
-            s0 += x[4 * j] * a.x + x[4 * j + 1] * a.y + x[4 * j + 2] * a.z + x[4 * j + 3] * a.w;
-            s1 += x[4 * j + 4] * b.x + x[4 * j + 5] * b.y + x[4 * j + 6] * b.z + x[4 * j + 7] * b.w;
+            const uint32_t a = r.Q[j], b = r.Q[j + 1];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s0 += x.v[4 * j + k] * sb(a, k);
+                s1 += x.v[4 * j + 4 + k] * sb(b, k);
+            }
+        }
+        return h16(r.d) * (s0 + s1);
+    }
+};
+
+struct TQ4_0 {   // Q4_0, 18 B / 32: unit = block; low nibbles -> j, high -> j + 16
+    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 1;
+    struct Raw { RawW<4> Q; uint32_t d; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const uint8_t* blk = row + u * 18;
+        r.d = ld_h16_bits(blk);
+        r.Q.load(blk + 2);
+    }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t q = r.Q[j];
+            const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s0 += x.v[4 * j + k] * ub(lo, k);
+                s1 += x.v[16 + 4 * j + k] * ub(hi, k);
+            }
+        }
+        return h16(r.d) * ((s0 + s1) - 8.f * x.s[0]);
+    }
+};
+
+struct TF32 {
+    static constexpr int RB = 2, NS = 1, RUN = 32, PRE = 2;
+    struct Raw { float4 f[8]; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const float4* p = reinterpret_cast<const float4*>(row + (int64_t)u * 128);
+#pragma unroll
+        for (int j = 0; j < 8; j++) r.f[j] = p[j];
+    }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const float4 a = r.f[j], b = r.f[j + 1];
+            s0 += x.v[4 * j] * a.x + x.v[4 * j + 1] * a.y + x.v[4 * j + 2] * a.z + x.v[4 * j + 3] * a.w;
+            s1 += x.v[4 * j + 4] * b.x + x.v[4 * j + 5] * b.y + x.v[4 * j + 6] * b.z + x.v[4 * j + 7] * b.w;
         }
         return s0 + s1;
     }
 };
 
-struct UF16 {
-    static constexpr int UE = 32, NS = 0;
-    __device__ static int xoff(int u, int run) { return u * 32 + run * 16; }
-    __device__ static float dot(const uint8_t* row, int u, const float* x, const float*) {
+struct TF16 {
+    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2;
+    struct Raw { u32x4 q[4]; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
         const uint8_t* p = row + (int64_t)u * 64;
+#pragma unroll
+        for (int j = 0; j < 4; j++) r.q[j] = ld16_a4(p + 16 * j);
+    }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const u32x4 v = ld16_a4(p + 16 * j);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t w[4] = {r.q[j].x, r.q[j].y, r.q[j].z, r.q[j].w};
 #pragma unroll
             for (int k = 0; k < 4; k++)
-                s += x[8 * j + 2 * k] * h16(w[k] & 0xFFFFu) + x[8 * j + 2 * k + 1] * h16(w[k] >> 16);
+                s += x.v[8 * j + 2 * k] * h16(w[k] & 0xFFFFu) + x.v[8 * j + 2 * k + 1] * h16(w[k] >> 16);
         }
         return s;
     }
 };
 
-template <uint32_t T> struct UnitOf;
-template <> struct UnitOf<GGML_Q5_K> { using type = UQ5K; };
-template <> struct UnitOf<GGML_Q6_K> { using type = UQ6K; };
-template <> struct UnitOf<GGML_Q8_0> { using type = UQ8_0; };
-template <> struct UnitOf<GGML_Q4_0> { using type = UQ4_0; };
-template <> struct UnitOf<GGML_F32> { using type = UF32; };
-template <> struct UnitOf<GGML_F16> { using type = UF16; };
+template <uint32_t T> struct TypeOf;
+template <> struct TypeOf<GGML_Q4_K> { using type = TQ4K; };
+template <> struct TypeOf<GGML_Q5_K> { using type = TQ5K; };
+template <> struct TypeOf<GGML_Q6_K> { using type = TQ6K; };
+template <> struct TypeOf<GGML_Q8_0> { using type = TQ8_0; };
+template <> struct TypeOf<GGML_Q4_0> { using type = TQ4_0; };
+template <> struct TypeOf<GGML_F32> { using type = TF32; };
+template <> struct TypeOf<GGML_F16> { using type = TF16; };
 
-// Sum of 4 per-lane values for 4 rows: lanes 16 r .. 16 r + 15 end with row r's total.
-__device__ __forceinline__ float reduce4(float a0, float a1, float a2, float a3, int lane) {
-    const bool hi = lane & 32;
-    float k0 = hi ? a2 : a0, k1 = hi ? a3 : a1;
-    const float s0 = hi ? a0 : a2, s1 = hi ? a1 : a3;
-    k0 += __shfl_xor(s0, 32, 64);
-    k1 += __shfl_xor(s1, 32, 64);
-    const bool b4 = lane & 16;
-    float k = b4 ? k1 : k0;
-    const float s = b4 ? k0 : k1;
-    k += __shfl_xor(s, 16, 64);
-    k += __shfl_xor(k, 8, 64);
-    k += __shfl_xor(k, 4, 64);
-    k += __shfl_xor(k, 2, 64);
-    k += __shfl_xor(k, 1, 64);
-    return k;
+// Sum of v over each row of 16 lanes, in every lane of the row (DPP row
+// rotations by 8, 4, 2, 1; all 64 lanes must be active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f32<0x128>(v);   // row_ror:8
+    v += dpp_f32<0x124>(v);   // row_ror:4
+    v += dpp_f32<0x122>(v);   // row_ror:2
+    v += dpp_f32<0x121>(v);   // row_ror:1
+    return v;
 }
 
-// 1/rms of the vector whose records are xrec[0 .. nrec) (every lane gets it):
-// RmsNorm's ss = sum(x^2); ss /= n; ss += eps; inv = 1 / sqrt(ss).
-__device__ __forceinline__ float rms_inv_from_records(const XRec* xrec, int nrec, int n, float eps) {
+// Raw activations of a lane: the unit's 32 values of x (and of the norm
+// weights), in the unit's element order.
+template <bool NORM>
+struct XRaw {
+    float4 h[8];
+    float4 w[NORM ? 8 : 1];
+};
+
+template <int RUN, bool NORM, typename XOff>
+__device__ __forceinline__ void issue_x(const GemvArgs& a, XOff&& xoff, XRaw<NORM>& r) {
+#pragma unroll
+    for (int run = 0; run < 32 / RUN; run++) {
+        const int off = xoff(run);
+#pragma unroll
+        for (int q = 0; q < RUN / 4; q++) {
+            r.h[run * (RUN / 4) + q] = *reinterpret_cast<const float4*>(a.x + off + 4 * q);
+            if (NORM) r.w[run * (RUN / 4) + q] = *reinterpret_cast<const float4*>(a.norm_w + off + 4 * q);
+        }
+    }
+}
+
+// v = w * h (VectorMath.RmsNorm's vector lanes compute (w * x) * inv; the
+// 1/rms factor is applied to the row sums), 0 past the row end; returns sum(h^2).
+template <bool NORM>
+__device__ __forceinline__ float finish_x(const XRaw<NORM>& r, bool has, float* v) {
+    float hsq = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        float4 e = r.h[q];
+        e.x = has ? e.x : 0.f; e.y = has ? e.y : 0.f; e.z = has ? e.z : 0.f; e.w = has ? e.w : 0.f;
+        hsq += e.x * e.x + e.y * e.y + e.z * e.z + e.w * e.w;
+        if (NORM) {
 #pragma clang fp contract(off)
-    float ss = 0.f;
-    for (int i = threadIdx.x & 63; i < nrec; i += 64) ss += xrec[i].ssq;
-    ss = wave_sum(ss);
-    return 1.0f / sqrtf(ss / (float)n + eps);
-}
-
-struct Place {   // this workgroup's segment, row group and K split
-    int seg, group, split;
-};
-
-__device__ __forceinline__ Place locate(const GemvArgs& a) {
-    int b = blockIdx.x, s = 0;
-    for (; s < a.nseg - 1; s++) {
-        const int nb = a.seg[s].groups * a.splitk;
-        if (b < nb) break;
-        b -= nb;
+            const float4 g = r.w[q];
+            e.x = g.x * e.x; e.y = g.y * e.y; e.z = g.z * e.z; e.w = g.w * e.w;
+        }
+        v[4 * q] = e.x; v[4 * q + 1] = e.y; v[4 * q + 2] = e.z; v[4 * q + 3] = e.w;
     }
-    return Place{s, b / a.splitk, b % a.splitk};
+    return hsq;
 }
 
-template <int UPL>
-struct Units {   // a lane's units in this split: u0 + lane + 64 i below u1
-    int u[UPL];
-    bool ok[UPL];
-};
-
-// The 8 rows (or 8 gate + 8 up rows) of this wavefront; sums go to
-// part_lds[wave*8 + i] (and part_lds[32 + wave*8 + i] for up).
-template <int UPL, bool SWIGLU, typename DotFn>
-__device__ __forceinline__ void rows_body(const GemvSeg& seg, const Place& pl, int64_t rb, DotFn&& dotfn,
-                                          const Units<UPL>& un, float* part_lds) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row_base = pl.group * GROUP + wave * 8;
-    constexpr int TILES = SWIGLU ? 4 : 2;
+template <int NS>
+__device__ __forceinline__ void run_sums(XF<NS>& x) {
+    constexpr int PER = 32 / NS;
 #pragma unroll
-    for (int t = 0; t < TILES; t++) {
-        const uint8_t* wr[4];
+    for (int t = 0; t < NS; t++) {
+        float z = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = SWIGLU ? row_base + 2 * t + (r & 1) : row_base + 4 * t + r;
-            const uint8_t* base = (SWIGLU && r >= 2) ? seg.w2 : seg.w;
-            wr[r] = base + (int64_t)(row < seg.rows ? row : 0) * rb;
-        }
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < UPL; i++)
-            if (un.ok[i]) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[r] += dotfn(wr[r], un.u[i], i);
-            }
-        const float tot = reduce4(acc[0], acc[1], acc[2], acc[3], lane);
-        if ((lane & 15) == 0) {
-            const int r = lane >> 4;
-            if (SWIGLU) part_lds[(r >= 2 ? 32 : 0) + wave * 8 + 2 * t + (r & 1)] = tot;
-            else part_lds[wave * 8 + 4 * t + r] = tot;
-        }
+        for (int e = 0; e < PER; e++) z += x.v[PER * t + e];
+        x.s[t] = z;
     }
 }
 
-// Split-K combine and epilogue for one 32-row group.
-template <int EPI>
-__device__ __forceinline__ void finish_group(const GemvArgs& a, const Place& pl, const GemvSeg& seg, float* part_lds) {
-    __shared__ int last;
-    constexpr int NV = EPI == EPI_SWIGLU ? 64 : 32;
-    const int tid = threadIdx.x;
-    if (a.splitk > 1) {
-        float* slot = a.partial + ((int64_t)pl.group * a.splitk + pl.split) * 64;
-        if (tid < NV) slot[tid] = part_lds[tid];
-        // One agent-scope release by thread 0 after the barrier publishes the
-        // whole workgroup's stores (the barrier orders them before it); the
-        // last arrival's acquire likewise covers the reads of all its threads.
-        __syncthreads();
-        if (tid == 0) {
-            __threadfence();
-            last = atomicAdd(a.counters + pl.group, 1u) == (unsigned)(a.splitk - 1);
-            if (last) __threadfence();
-        }
-        __syncthreads();
-        if (!last) return;
-        if (tid < NV) {
-            float s = 0.f;
-            const float* base = a.partial + (int64_t)pl.group * a.splitk * 64;
-            for (int k = 0; k < a.splitk; k++) s += __builtin_nontemporal_load(base + k * 64 + tid);
-            part_lds[tid] = s;
-        }
-        if (tid == 0) a.counters[pl.group] = 0u;
-        __syncthreads();
+// One workgroup's rows.  Issue order: the activations, then the first two
+// batches of weights (one for types with large raw blocks); a scheduling barrier keeps the activation arithmetic
+// (quantisation) after those issues, so it overlaps the weight loads.  Each
+// computed batch frees its registers for the batch two ahead.  Every lane
+// loads (lanes past the row end read unit 0 and contribute 0): no branches,
+// so no load is serialised behind another.  Row i's per-quarter-wavefront
+// sums go to red_w[i][0..3]; returns the lane's sum(h^2).
+template <typename TT, int NB, bool NORM, typename RowPtr>
+__device__ __forceinline__ float gemv_rows(const GemvArgs& a, int uu, bool has, RowPtr&& row_ptr, float (*red_w)[4]) {
+    constexpr int RB = TT::RB;
+    constexpr bool INT = std::is_same<TT, TQ4K>::value;
+    const int lane = threadIdx.x & 63;
+    XRaw<NORM> xr;
+    if constexpr (INT) issue_x<32, NORM>(a, [&](int) { return uu * 32; }, xr);
+    else issue_x<TT::RUN, NORM>(a, [&](int run) { return TT::xoff(uu, run); }, xr);
+    typename TT::Raw buf[2][RB];
+#pragma unroll
+    for (int i = 0; i < RB; i++) TT::load(buf[0][i], row_ptr(i), uu);
+    if (NB > 1 && TT::PRE > 1) {
+#pragma unroll
+        for (int i = 0; i < RB; i++) TT::load(buf[1][i], row_ptr(RB + i), uu);
     }
-    if (tid >= 64) return;   // wavefront 0 finishes: lane e < 32 owns row group*32 + e
-    const int e = tid & 31;
-    const int row = pl.group * GROUP + e;
-    const bool valid = row < seg.rows && tid < 32;
-    const float y = part_lds[e];
+    __builtin_amdgcn_sched_barrier(0);
+    float v[32];
+    const float hsq = finish_x<NORM>(xr, has, v);
+    if (NB > 1 && TT::PRE == 1) {
+#pragma unroll
+        for (int i = 0; i < RB; i++) TT::load(buf[1][i], row_ptr(RB + i), uu);
+    }
+    typename std::conditional<INT, XQ, XF<INT ? 1 : TT::NS>>::type x;
+    if constexpr (INT) {
+        quantize32(v, x);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 32; e++) x.v[e] = v[e];
+        run_sums(x);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int i = 0; i < RB; i++) {
+            float d = TT::dot(buf[b & 1][i], uu, x);
+            d = row_sum16(has ? d : 0.f);
+            if ((lane & 15) == 0) red_w[b * RB + i][lane >> 4] = d;
+        }
+        if (b + 2 < NB) {
+#pragma unroll
+            for (int i = 0; i < RB; i++) TT::load(buf[b & 1][i], row_ptr((b + 2) * RB + i), uu);
+        }
+    }
+    return hsq;
+}
+
+// ---- the kernel -------------------------------------------------------------------
+// NB batches of RB dot rows; SwiGLU batches hold RB/2 gate then RB/2 up rows.
+template <uint32_t T, int EPI, int NB, bool NORM>
+__global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
+    using TT = typename TypeOf<T>::type;
+    constexpr int RB = TT::RB;
+    constexpr bool SW = EPI == EPI_SWIGLU;
+    constexpr int OPB = SW ? RB / 2 : RB;     // output rows per batch
+    constexpr int ROWS_WG = NB * OPB;
+    constexpr int NSUM = NB * RB;
+    static_assert(ROWS_WG <= 64, "epilogue uses one wavefront");
+    __shared__ float red[MAXW][NSUM][4];
+    __shared__ float ssq[MAXW];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    // segment and first row of this workgroup
+    int blk = blockIdx.x, si = 0;
+    for (; si < a.nseg - 1; si++) {
+        if (blk < a.seg[si].wgs) break;
+        blk -= a.seg[si].wgs;
+    }
+    const GemvSeg seg = a.seg[si];
+    const int row0 = blk * ROWS_WG;
+    const int K = a.cols;
+    const int u = wave * 64 + lane;
+    const bool has = u < K / 32;
+    const int uu = has ? u : 0;
+    const int64_t rbytes = (int64_t)(K / block_elems(T)) * block_bytes(T);
+
+    auto row_ptr = [&](int i) -> const uint8_t* {   // dot row i of this workgroup
+        const int b = i / RB, k = i % RB;
+        const uint8_t* base = seg.w;
+        int r;
+        if (SW) {
+            r = row0 + b * OPB + (k % OPB);
+            if (k >= OPB) base = seg.w2;
+        } else {
+            r = row0 + i;
+        }
+        return base + (int64_t)(r < seg.rows ? r : 0) * rbytes;
+    };
+
+    const float hsq = gemv_rows<TT, NB, NORM>(a, uu, has, row_ptr, red[wave]);
+    if (NORM) {
+        const float w = wave_sum(hsq);
+        if (lane == 0) ssq[wave] = w;
+    }
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+
+    // epilogue (wavefront 0): lane t < ROWS_WG owns output row row0 + t
+    const int t = threadIdx.x;
+    float inv = 1.f;
+    if (NORM) {
+#pragma clang fp contract(off)
+        float ss = 0.f;
+        for (int w = 0; w < nw; w++) ss += ssq[w];
+        inv = 1.0f / sqrtf(ss / (float)K + a.eps);   // RmsNorm: 1 / sqrt(sum/n + eps)
+    }
+    auto total = [&](int i) {
+        float s = 0.f;
+        for (int w = 0; w < nw; w++) s += (red[w][i][0] + red[w][i][1]) + (red[w][i][2] + red[w][i][3]);
+        return s * inv;
+    };
+    const int row = row0 + t;
+    const bool valid = t < ROWS_WG && row < seg.rows;
+    const int b = t / OPB, k = t % OPB;
     if (EPI == EPI_STORE) {
-        if (valid) seg.out[row] = y;
-    } else if (EPI == EPI_ADD || EPI == EPI_SWIGLU) {
-        float outv = 0.f;
+        if (valid) seg.out[row] = total(b * RB + k);
+    } else if (EPI == EPI_ADD) {
+        if (valid) seg.out[row] = seg.out[row] + total(b * RB + k);
+    } else if (EPI == EPI_SWIGLU) {
         if (valid) {
 #pragma clang fp contract(off)
-            if (EPI == EPI_ADD) {
-                outv = seg.out[row] + y;      // residual: a[i] + b[i]
-            } else {
-                const float up = part_lds[32 + e];
-                const float sg = row < (seg.rows & ~7) ? silu_ref(y) : y / (1.0f + expf(-y));
-                outv = sg * up;
-            }
-            seg.out[row] = outv;
-        }
-        if (a.rec_out) {
-            float v = outv;
-            if (a.rec_w && valid) {
-#pragma clang fp contract(off)
-                v = a.rec_w[row] * outv;
-            }
-            build_xrec(v, outv * outv, a.rec_out + pl.group, tid < 32);
+            const float g = total(b * RB + k), up = total(b * RB + OPB + k);
+            // SiluInPlace: vector lanes (ExpApprox) for the first 8*floor(n/8), expf tail
+            const float sg = row < (seg.rows & ~7) ? silu_ref(g) : g / (1.0f + expf(-g));
+            seg.out[row] = sg * up;
         }
     } else if (EPI == EPI_ARGMAX) {
+        const float y = valid ? total(t) : -INFINITY;
         if (valid) seg.out[row] = y;
-        float bv = valid ? y : -INFINITY;
+        float bv = y;
         int bi = valid ? row : 0x7FFFFFFF;
 #pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) {
+        for (int o = 32; o >= 1; o >>= 1) {
             const float ov = __shfl_xor(bv, o, 64);
             const int oi = __shfl_xor(bi, o, 64);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        int is_last = 0;
-        if (tid == 0) {
-            a.am.cand_val[pl.group] = bv;
-            a.am.cand_idx[pl.group] = bi;
-            __threadfence();
-            is_last = atomicAdd(a.am.counter, 1u) == (unsigned)(seg.groups - 1);
-        }
-        is_last = __shfl(is_last, 0, 64);
-        if (!is_last) return;
-        if (tid == 0) __threadfence();
-        __builtin_amdgcn_wave_barrier();
-        float v = -INFINITY;
-        int idx = 0x7FFFFFFF;
-        for (int c = tid; c < seg.groups; c += 64) {
-            const float cv = __builtin_nontemporal_load(a.am.cand_val + c);
-            const int ci = __builtin_nontemporal_load(a.am.cand_idx + c);
-            if (cv > v || (cv == v && ci < idx)) { v = cv; idx = ci; }
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(v, o, 64);
-            const int oi = __shfl_xor(idx, o, 64);
-            if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
-        }
-        if (tid == 0) {
-            if (idx == 0x7FFFFFFF) idx = 0;   // all NaN: ArgMax returns 0
-            *a.am.token_out = idx;
-            if (a.am.token_log && *a.am.step >= 0 && *a.am.step < a.am.log_cap) a.am.token_log[*a.am.step] = idx;
-            if (a.am.step) *a.am.step += 1;
-            if (a.am.pos) *a.am.pos += 1;
-            *a.am.counter = 0u;
+        if (t == 0) {   // one candidate per workgroup; launch_argmax_finish reduces them
+            a.am.cand_val[blockIdx.x] = bv;
+            a.am.cand_idx[blockIdx.x] = bi;
         }
     }
-}
-
-template <uint32_t T, int EPI>
-__global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
-    __shared__ float part_lds[64];
-    const Place pl = locate(a);
-    const GemvSeg seg = a.seg[pl.seg];
-    constexpr bool SWIGLU = EPI == EPI_SWIGLU;
-    const int lane = threadIdx.x & 63;
-    const int K = a.cols;
-    if constexpr (T == GGML_Q4_K) {
-        constexpr int UPL = 2;
-        const int U = K / 32, per = U / a.splitk;
-        const int u0 = pl.split * per, u1 = u0 + per;
-        const int64_t rb = (int64_t)(K / 256) * 144;
-        const float inv = a.norm ? rms_inv_from_records(a.xrec, U, K, a.eps) : 1.f;
-        Units<UPL> un;
-        XI xi[UPL];
-#pragma unroll
-        for (int i = 0; i < UPL; i++) {
-            un.u[i] = u0 + lane + 64 * i;
-            un.ok[i] = un.u[i] < u1;
-            const XRec* r = a.xrec + (un.ok[i] ? un.u[i] : 0);
-            const u32x4* p = reinterpret_cast<const u32x4*>(r);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const u32x4 v = p[q];
-                xi[i].pl[4 * q] = v.x; xi[i].pl[4 * q + 1] = v.y; xi[i].pl[4 * q + 2] = v.z; xi[i].pl[4 * q + 3] = v.w;
-            }
-            xi[i].s = r->s * inv;
-            xi[i].sum = r->sum * inv;
-        }
-        auto fn = [&](const uint8_t* row, int u, int i) { return q4k_int(row, u, xi[i]); };
-        rows_body<UPL, SWIGLU>(seg, pl, rb, fn, un, part_lds);
-    } else {
-        using U_ = typename UnitOf<T>::type;
-        constexpr int UE = U_::UE;
-        constexpr int UPL = UE == 64 ? 1 : 2;
-        const int U = K / UE, per = U / a.splitk;
-        const int u0 = pl.split * per, u1 = u0 + per;
-        const int64_t rb = (int64_t)(K / block_elems(T)) * block_bytes(T);
-        const float inv = a.norm ? rms_inv_from_records(a.xrec, K / 32, K, a.eps) : 1.f;
-        Units<UPL> un;
-        float xv[UPL][UE];
-        float xs[UPL][U_::NS > 0 ? U_::NS : 1];
-#pragma unroll
-        for (int i = 0; i < UPL; i++) {
-            un.u[i] = u0 + lane + 64 * i;
-            un.ok[i] = un.u[i] < u1;
-            const int uu = un.ok[i] ? un.u[i] : 0;
-#pragma unroll
-            for (int run = 0; run < UE / 16; run++) {
-                const int off = U_::xoff(uu, run);
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    float4 h = *reinterpret_cast<const float4*>(a.x + off + 4 * q);
-                    if (a.norm) {   // VectorMath.RmsNorm vector lanes: (w * x) * inv
-#pragma clang fp contract(off)
-                        const float4 w = *reinterpret_cast<const float4*>(a.norm_w + off + 4 * q);
-                        h.x = (w.x * h.x) * inv; h.y = (w.y * h.y) * inv;
-                        h.z = (w.z * h.z) * inv; h.w = (w.w * h.w) * inv;
-                    }
-                    xv[i][run * 16 + 4 * q] = h.x; xv[i][run * 16 + 4 * q + 1] = h.y;
-                    xv[i][run * 16 + 4 * q + 2] = h.z; xv[i][run * 16 + 4 * q + 3] = h.w;
-                }
-            }
-            if constexpr (U_::NS == 1) {
-                float t = 0.f;
-#pragma unroll
-                for (int e = 0; e < UE; e++) t += xv[i][e];
-                xs[i][0] = t;
-            } else if constexpr (U_::NS == 4) {
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    float z = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) z += xv[i][16 * t + e];
-                    xs[i][t] = z;
-                }
-            }
-        }
-        auto fn = [&](const uint8_t* row, int u, int i) { return U_::dot(row, u, xv[i], xs[i]); };
-        rows_body<UPL, SWIGLU>(seg, pl, rb, fn, un, part_lds);
-    }
-    __syncthreads();
-    finish_group<EPI>(a, pl, seg, part_lds);
-}
-
-// Records of a plain vector (op-level calls): one 32-lane half-wavefront per unit.
-__global__ __launch_bounds__(64) void make_xrec_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                        int n, XRec* __restrict__ out) {
-    const int unit = blockIdx.x * 2 + (threadIdx.x >> 5);
-    const int e = threadIdx.x & 31;
-    const int i = unit * 32 + e;
-    const bool ok = i < n;
-    const float h = ok ? x[i] : 0.f;
-    float v = h;
-    if (w && ok) {
-#pragma clang fp contract(off)
-        v = w[i] * h;
-    }
-    build_xrec(v, h * h, out + unit, unit * 32 < n);
 }
 
 // Generic fallback for F32/F16 weights whose width is not a multiple of 32
 // (MatMulF32 with small shapes, TO:437-504): one wavefront per output row.
-__global__ __launch_bounds__(WG) void gemv_generic_kernel(const uint8_t* w, uint32_t type, const float* x,
-                                                          float* y, int rows, int cols) {
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* w, uint32_t type, const float* x,
+                                                           float* y, int rows, int cols) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
@@ -541,17 +601,44 @@ __global__ __launch_bounds__(WG) void gemv_generic_kernel(const uint8_t* w, uint
     if (lane == 0) y[r] = s;
 }
 
-template <uint32_t T>
-hipError_t launch_t(int epi, const GemvArgs& a, int grid, hipStream_t s) {
-    switch (epi) {
-    case EPI_STORE: gemv_kernel<T, EPI_STORE><<<grid, WG, 0, s>>>(a); break;
-    case EPI_ADD: gemv_kernel<T, EPI_ADD><<<grid, WG, 0, s>>>(a); break;
-    case EPI_SWIGLU: gemv_kernel<T, EPI_SWIGLU><<<grid, WG, 0, s>>>(a); break;
-    case EPI_ARGMAX: gemv_kernel<T, EPI_ARGMAX><<<grid, WG, 0, s>>>(a); break;
+int type_rb(uint32_t t) {
+    switch (t) {
+    case GGML_Q6_K: return TQ6K::RB;
+    case GGML_Q8_0: return TQ8_0::RB;
+    case GGML_F32: return TF32::RB;
+    case GGML_F16: return TF16::RB;
+    default: return 8;
+    }
+}
+
+template <uint32_t T, int EPI, bool NORM>
+hipError_t launch_te(const GemvArgs& a, int nb, int grid, int threads, hipStream_t s) {
+    switch (nb) {
+    case 1: gemv_kernel<T, EPI, 1, NORM><<<grid, threads, 0, s>>>(a); break;
+    case 2: gemv_kernel<T, EPI, 2, NORM><<<grid, threads, 0, s>>>(a); break;
+    case 4: gemv_kernel<T, EPI, 4, NORM><<<grid, threads, 0, s>>>(a); break;
+    case 8: gemv_kernel<T, EPI, 8, NORM><<<grid, threads, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
+
+// Instantiated forms: STORE with or without RmsNorm, ADD without, SWIGLU and
+// ARGMAX with (the decode step's uses and the op-level MatMul).
+template <uint32_t T>
+hipError_t launch_t(int epi, const GemvArgs& a, int nb, int grid, int threads, hipStream_t s) {
+    switch (epi) {
+    case EPI_STORE:
+        return a.norm ? launch_te<T, EPI_STORE, true>(a, nb, grid, threads, s)
+                      : launch_te<T, EPI_STORE, false>(a, nb, grid, threads, s);
+    case EPI_ADD: return launch_te<T, EPI_ADD, false>(a, nb, grid, threads, s);
+    case EPI_SWIGLU: return launch_te<T, EPI_SWIGLU, true>(a, nb, grid, threads, s);
+    case EPI_ARGMAX: return launch_te<T, EPI_ARGMAX, true>(a, nb, grid, threads, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+bool generic_shape(uint32_t type, int cols) { return (type == GGML_F32 || type == GGML_F16) && cols % 32 != 0; }
 
 }  // namespace
 
@@ -560,79 +647,87 @@ bool gemv_supported(uint32_t type) {
            type == GGML_Q4_0 || type == GGML_F32 || type == GGML_F16;
 }
 
-int gemv_unit_elems(uint32_t type) { return type == GGML_Q6_K ? 64 : 32; }
-
-int gemv_max_units(uint32_t type) { return 64 * (type == GGML_Q6_K ? 1 : 2); }
-
-int gemv_groups(int rows) { return (rows + GROUP - 1) / GROUP; }
-
-int gemv_pick_splitk(uint32_t type, int cols, int rows_total) {
-    if ((type == GGML_F32 || type == GGML_F16) && cols % 32 != 0) return 1;
-    const int U = cols / gemv_unit_elems(type);
-    const int groups = gemv_groups(rows_total);
-    const int maxu = gemv_max_units(type);
-    // the smallest split that fits the per-lane unit budget; then keep
-    // splitting (at least one unit per lane) until the grid covers 512 workgroups
-    int best = 0;
-    for (int s = 1; s <= 32; s++) {
-        if (U % s) continue;
-        const int per = U / s;
-        if (per > maxu) continue;
-        if (!best) {
-            best = s;
-            if (groups * s >= 512) break;
-            continue;
-        }
-        if (per < 64) break;
-        best = s;
-        if (groups * s >= 512) break;
-    }
-    return best;
+bool gemv_width_ok(uint32_t type, int cols) {
+    if (!gemv_supported(type) || cols <= 0) return false;
+    if (generic_shape(type, cols)) return true;
+    return cols % block_elems(type) == 0 && cols / 32 <= MAXW * 64;
 }
 
-int gemv_grid(const GemvArgs& a) {
-    int g = 0;
-    for (int s = 0; s < a.nseg; s++) g += a.seg[s].groups * a.splitk;
-    return g;
+// Wavefronts a launch should have at least (8 per CU); LLMDOT_GEMV_WAVES
+// overrides it for tuning.
+static int target_waves() {
+    static const int w = [] {
+        const char* e = getenv("LLMDOT_GEMV_WAVES");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 2048;
+    }();
+    return w;
 }
 
-hipError_t launch_make_xrec(const float* x, const float* w, int n, XRec* out, hipStream_t s) {
-    const int units = (n + 31) / 32;
-    make_xrec_kernel<<<(units + 1) / 2, 64, 0, s>>>(x, w, n, out);
-    return hipGetLastError();
+int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
+    if (generic_shape(type, cols)) return 0;
+    const int nw = (cols / 32 + 63) / 64;
+    const int opb = epi == EPI_SWIGLU ? type_rb(type) / 2 : type_rb(type);
+    // the most rows per workgroup that still gives the target wavefront count
+    int nb = 8;
+    while (nb > 1 && ((rows_total + nb * opb - 1) / (nb * opb)) * nw < target_waves()) nb /= 2;
+    return nb;
 }
 
-hipError_t launch_gemv(uint32_t type, int epi, const GemvArgs& a, hipStream_t s) {
-    if (a.cols <= 0) return hipErrorInvalidValue;
-    if ((type == GGML_F32 || type == GGML_F16) && (a.cols % 32 != 0)) {
+int gemv_rows_per_wg(uint32_t type, int epi, int nb) {
+    return nb * (epi == EPI_SWIGLU ? type_rb(type) / 2 : type_rb(type));
+}
+
+int gemv_max_grid(uint32_t type, int epi, int rows, int cols) {
+    if (generic_shape(type, cols)) return (rows + 3) / 4;
+    const int rwg = gemv_rows_per_wg(type, epi, gemv_plan(type, epi, rows, cols));
+    return (rows + rwg - 1) / rwg + 2;   // segments round up separately
+}
+
+hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
+    if (a.cols <= 0 || a.nseg < 1 || a.nseg > 3) return hipErrorInvalidValue;
+    if (generic_shape(type, a.cols)) {
         if (epi != EPI_STORE || a.nseg != 1 || a.norm) return hipErrorInvalidValue;
-        gemv_generic_kernel<<<(a.seg[0].rows + 3) / 4, WG, 0, s>>>(a.seg[0].w, type, a.x, a.seg[0].out,
-                                                                  a.seg[0].rows, a.cols);
+        if (a.seg[0].rows <= 0) return hipSuccess;
+        gemv_generic_kernel<<<(a.seg[0].rows + 3) / 4, 256, 0, s>>>(a.seg[0].w, type, a.x, a.seg[0].out,
+                                                                   a.seg[0].rows, a.cols);
         return hipGetLastError();
     }
-    if (!gemv_supported(type) || a.cols % gemv_unit_elems(type) != 0 || a.cols % block_elems(type) != 0)
-        return hipErrorInvalidValue;
-    const int U = a.cols / gemv_unit_elems(type);
-    if (a.splitk < 1 || U % a.splitk != 0 || U / a.splitk > gemv_max_units(type)) return hipErrorInvalidValue;
-    if (type == GGML_Q4_K && !a.xrec) return hipErrorInvalidValue;
-    if (a.norm && !a.xrec) return hipErrorInvalidValue;
-    if (a.splitk > 1 && (!a.partial || !a.counters)) return hipErrorInvalidValue;
+    if (!gemv_width_ok(type, a.cols)) return hipErrorInvalidValue;
     if (epi == EPI_SWIGLU && (a.nseg != 1 || !a.seg[0].w2)) return hipErrorInvalidValue;
-    if ((epi == EPI_ADD || epi == EPI_SWIGLU) && a.rec_out && a.nseg != 1) return hipErrorInvalidValue;
-    for (int i = 0; i < a.nseg; i++)
-        if (a.seg[i].groups != gemv_groups(a.seg[i].rows)) return hipErrorInvalidValue;
-    const int grid = gemv_grid(a);
+    if (epi == EPI_ARGMAX && (a.nseg != 1 || !a.am.cand_val || !a.am.cand_idx || !a.am.token_out))
+        return hipErrorInvalidValue;
+    if (a.norm && !a.norm_w) return hipErrorInvalidValue;
+    if (epi == EPI_ADD && a.norm) return hipErrorInvalidValue;
+    if ((epi == EPI_SWIGLU || epi == EPI_ARGMAX) && !a.norm) return hipErrorInvalidValue;
+    int rows_total = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        if (a.seg[i].rows < 0) return hipErrorInvalidValue;
+        rows_total += a.seg[i].rows;
+    }
+    const int nb = gemv_plan(type, epi, rows_total, a.cols);
+    const int rwg = gemv_rows_per_wg(type, epi, nb);
+    int grid = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        a.seg[i].wgs = (a.seg[i].rows + rwg - 1) / rwg;
+        grid += a.seg[i].wgs;
+    }
     if (grid <= 0) return hipSuccess;
+    if (epi == EPI_ARGMAX && a.am.cap < grid) return hipErrorInvalidValue;
+    const int threads = 64 * ((a.cols / 32 + 63) / 64);
+    hipError_t e;
     switch (type) {
-    case GGML_Q4_K: return launch_t<GGML_Q4_K>(epi, a, grid, s);
-    case GGML_Q5_K: return launch_t<GGML_Q5_K>(epi, a, grid, s);
-    case GGML_Q6_K: return launch_t<GGML_Q6_K>(epi, a, grid, s);
-    case GGML_Q8_0: return launch_t<GGML_Q8_0>(epi, a, grid, s);
-    case GGML_Q4_0: return launch_t<GGML_Q4_0>(epi, a, grid, s);
-    case GGML_F32: return launch_t<GGML_F32>(epi, a, grid, s);
-    case GGML_F16: return launch_t<GGML_F16>(epi, a, grid, s);
+    case GGML_Q4_K: e = launch_t<GGML_Q4_K>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q5_K: e = launch_t<GGML_Q5_K>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q6_K: e = launch_t<GGML_Q6_K>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q8_0: e = launch_t<GGML_Q8_0>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q4_0: e = launch_t<GGML_Q4_0>(epi, a, nb, grid, threads, s); break;
+    case GGML_F32: e = launch_t<GGML_F32>(epi, a, nb, grid, threads, s); break;
+    case GGML_F16: e = launch_t<GGML_F16>(epi, a, nb, grid, threads, s); break;
     default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess || epi != EPI_ARGMAX) return e;
+    return launch_argmax_finish(a.am, grid, s);
 }
 
 }  // namespace llmdot

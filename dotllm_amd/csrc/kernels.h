@@ -17,7 +17,6 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const i
                         float* out, hipStream_t s);
 
 // ---- gemv.hip ----
-struct XRec;   // xrec.h
 enum GemvEpi : int { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 
 struct GemvSeg {
@@ -25,45 +24,40 @@ struct GemvSeg {
     const uint8_t* w2;  // EPI_SWIGLU: the up matrix (w is the gate)
     float* out;         // rows outputs
     int rows;
-    int groups;         // gemv_groups(rows)
+    int wgs;            // workgroups of this segment (set by launch_gemv)
 };
 
 struct ArgmaxState {
-    float* cand_val;      // per 32-row group
+    float* cand_val;      // one candidate per workgroup of the first pass
     int32_t* cand_idx;
-    uint32_t* counter;    // zero before launch; the last workgroup resets it
+    int32_t cap;          // capacity of cand_*
     int32_t* token_out;   // argmax result (next token)
-    int32_t* pos;         // optional: incremented by the last workgroup
+    int32_t* pos;         // optional: incremented by the second pass
     int32_t* token_log;   // optional: token_log[*step] = argmax while *step < log_cap
     int32_t log_cap;
-    int32_t* step;        // optional: incremented by the last workgroup
+    int32_t* step;        // optional: incremented by the second pass
 };
 
 struct GemvArgs {
-    GemvSeg seg[3];
+    GemvSeg seg[3];       // up to 3 matrices of the same type and width in one launch
     int nseg;
     int cols;             // reduction length K
-    int splitk;           // K splits per 32-row group (gemv_pick_splitk)
-    const float* x;       // fp32 input (the hidden state when norm != 0)
-    const float* norm_w;  // RmsNorm weights applied on the fly by the fp32 path
-    const XRec* xrec;     // input records (Q4_K path; ssq source when norm != 0)
-    int norm;             // apply RmsNorm (1/rms from the records' ssq)
+    const float* x;       // fp32 input (the unnormalised hidden state when norm != 0)
+    const float* norm_w;  // RmsNorm weights applied on the fly
+    int norm;             // apply RmsNorm to x
     float eps;
-    XRec* rec_out;        // EPI_ADD / EPI_SWIGLU: records of the output vector
-    const float* rec_w;   // norm weights of the output's consumer (nullable)
-    float* partial;       // split-K scratch [groups][splitk][64]
-    uint32_t* counters;   // split-K arrival counters [groups], zero between launches
     ArgmaxState am;       // EPI_ARGMAX
 };
 
 bool gemv_supported(uint32_t type);
-int gemv_unit_elems(uint32_t type);
-int gemv_groups(int rows);
-int gemv_pick_splitk(uint32_t type, int cols, int rows_total);
-int gemv_grid(const GemvArgs& a);
-hipError_t launch_gemv(uint32_t type, int epi, const GemvArgs& a, hipStream_t s);
-// Records of x (optionally multiplied by norm weights w) for n elements.
-hipError_t launch_make_xrec(const float* x, const float* w, int n, XRec* out, hipStream_t s);
+// Whether rows of `cols` elements fit the kernel (block multiple, <= 16384 wide).
+bool gemv_width_ok(uint32_t type, int cols);
+// Row batches per workgroup for a launch over rows_total output rows.
+int gemv_plan(uint32_t type, int epi, int rows_total, int cols);
+int gemv_rows_per_wg(uint32_t type, int epi, int nb);
+// Upper bound of the grid (argmax candidate slots) for rows output rows.
+int gemv_max_grid(uint32_t type, int epi, int rows, int cols);
+hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s);
 
 // ---- ops.hip (op-level IComputeBackend members) ----
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, int n, float eps, hipStream_t s);
@@ -73,9 +67,11 @@ hipError_t launch_softmax(float* x, int n, int has_softcap, float cap, hipStream
 hipError_t launch_silu(const float* in, float* out, int n, hipStream_t s);
 hipError_t launch_binary(int op, const float* a, const float* b, float* out, int n, hipStream_t s);  // 0 add, 1 mul
 hipError_t launch_scale(const float* in, float sc, float* out, int n, hipStream_t s);
-// ArgMax over n floats; st.cand_* sized for argmax_grid(n) workgroups.
+// ArgMax over n floats (two launches); st.cand_* sized for argmax_grid(n).
 int argmax_grid(int n);
 hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream_t s);
+// Second pass over ncand candidates: token_out, token_log/step, pos.
+hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s);
 // Position bookkeeping for a captured decode step.
 hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s);
 hipError_t launch_fill_random_half(void* dst, size_t n, uint64_t seed, int fp16, hipStream_t s);
@@ -94,9 +90,7 @@ struct AttnArgs {
     float* chunk_max;       // [heads][max_chunks]
     float* part_out;        // [max_chunks][heads][head_dim]
     float* part_sum;        // [max_chunks][heads]
-    uint32_t* counters;     // [kv_heads], zero; the last workgroup of each kv head resets its own
     float* out;             // [heads][head_dim]
-    XRec* rec_out;          // records of out (nullable)
     int heads, kv_heads, head_dim, rope_half, context, kv_fp16;
 };
 int attn_chunk(int heads, int kv_heads);

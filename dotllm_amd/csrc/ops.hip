@@ -119,47 +119,56 @@ __global__ void scale_kernel(const float* in, float sc, float* out, int n) {
 
 constexpr int AM_PER_WG = 4096;
 
-// VectorMath.ArgMax, VM:412-425: first index of the strict maximum.  Each
-// workgroup reduces AM_PER_WG elements; the last one reduces the candidates.
+// (v, i) beats (bv, bi): larger value, or equal value and smaller index
+// (VectorMath.ArgMax keeps the first strict maximum; NaN never wins).
+__device__ __forceinline__ void am_combine(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+// VectorMath.ArgMax, VM:412-425, first pass: each workgroup reduces
+// AM_PER_WG elements to one candidate.
 __global__ __launch_bounds__(WG) void argmax_kernel(const float* x, int n, ArgmaxState st) {
     __shared__ float sv[4];
     __shared__ int si[4];
-    __shared__ int last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
     const int beg = blockIdx.x * AM_PER_WG, end = min(n, beg + AM_PER_WG);
     for (int i = beg + threadIdx.x; i < end; i += WG)
         if (x[i] > v) { v = x[i]; idx = i; }   // ascending i per thread: first max wins
-    auto combine = [&](float ov, int oi) {
-        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
-    };
-    for (int o = 32; o >= 1; o >>= 1) combine(__shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    for (int o = 32; o >= 1; o >>= 1) am_combine(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
     if (lane == 0) { sv[wave] = v; si[wave] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) combine(sv[w], si[w]);
+        for (int w = 1; w < 4; w++) am_combine(v, idx, sv[w], si[w]);
         st.cand_val[blockIdx.x] = v;
         st.cand_idx[blockIdx.x] = idx;
-        __threadfence();
-        last = atomicAdd(st.counter, 1u) == gridDim.x - 1;
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    v = -INFINITY;
-    idx = 0x7FFFFFFF;
-    for (int c = threadIdx.x; c < (int)gridDim.x; c += WG)
-        combine(__builtin_nontemporal_load(st.cand_val + c), __builtin_nontemporal_load(st.cand_idx + c));
-    for (int o = 32; o >= 1; o >>= 1) combine(__shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
-    __syncthreads();
+}
+
+// Second pass over the ncand candidates (a separate launch, so the
+// candidates are visible without fences): the token, and the device-side
+// decode-loop bookkeeping (token log, step, position).
+__global__ __launch_bounds__(WG) void argmax_finish_kernel(ArgmaxState st, int ncand) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float v = -INFINITY;
+    int idx = 0x7FFFFFFF;
+    for (int c = threadIdx.x; c < ncand; c += WG) am_combine(v, idx, st.cand_val[c], st.cand_idx[c]);
+    for (int o = 32; o >= 1; o >>= 1) am_combine(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
     if (lane == 0) { sv[wave] = v; si[wave] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) combine(sv[w], si[w]);
-        if (idx == 0x7FFFFFFF) idx = 0;
+        for (int w = 1; w < 4; w++) am_combine(v, idx, sv[w], si[w]);
+        if (idx == 0x7FFFFFFF) idx = 0;   // all NaN: ArgMax returns 0
         *st.token_out = idx;
-        *st.counter = 0u;
+        if (st.step) {
+            const int k = *st.step;
+            if (st.token_log && k >= 0 && k < st.log_cap) st.token_log[k] = idx;
+            *st.step = k + 1;
+        }
+        if (st.pos) *st.pos += 1;
     }
 }
 
@@ -215,8 +224,15 @@ hipError_t launch_scale(const float* in, float sc, float* out, int n, hipStream_
 }
 int argmax_grid(int n) { return (n + AM_PER_WG - 1) / AM_PER_WG; }
 hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream_t s) {
-    if (n <= 0) return hipErrorInvalidValue;
+    if (n <= 0 || st.cap < argmax_grid(n)) return hipErrorInvalidValue;
     argmax_kernel<<<argmax_grid(n), WG, 0, s>>>(x, n, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_argmax_finish(st, argmax_grid(n), s);
+}
+hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s) {
+    if (ncand <= 0 || ncand > st.cap) return hipErrorInvalidValue;
+    argmax_finish_kernel<<<1, WG, 0, s>>>(st, ncand);
     return hipGetLastError();
 }
 hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s) {
