@@ -57,6 +57,9 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
+    ap.add_argument("--synthetic-kv", action="store_true",
+                    help="fill the KV cache of the first --ctx positions with random values instead of "
+                         "processing a --ctx-token prompt (same decode-step work; for short profiling runs)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernel by kernel instead of replaying the captured HIP graph "
                          "(rocprofv3 cannot trace graph launches on this image)")
@@ -84,10 +87,15 @@ def main() -> int:
     eng = InferenceEngine(model, be, kv_fp16=True, context=total_ctx)
     log(f"uploaded weights + built step graph in {time.perf_counter() - t0:.1f}s on {info['name']} ({info['arch']})")
 
-    prompt = synth.prompt(spec["vocab"], args.ctx, seed=7)
-    t0 = time.perf_counter()
-    _, tok = eng.prefill(prompt, 0)
-    log(f"processed {args.ctx}-token prompt in {time.perf_counter() - t0:.1f}s")
+    if args.synthetic_kv:
+        eng.kv_fill_random(args.ctx, seed=3)
+        tok = 1
+        log(f"filled {args.ctx} KV positions with random values")
+    else:
+        prompt = synth.prompt(spec["vocab"], args.ctx, seed=7)
+        t0 = time.perf_counter()
+        _, tok = eng.prefill(prompt, 0)
+        log(f"processed {args.ctx}-token prompt in {time.perf_counter() - t0:.1f}s")
     pos = args.ctx
 
     if args.warmup > 0:
@@ -121,6 +129,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": f"{args.config}-shape Q4_K_M greedy decode, batch 1, context {args.ctx}, fp16 KV",
                    "launch": "eager" if args.eager else "hip-graph",
+                   "kv": "random fill" if args.synthetic_kv else "prompt processed on device",
                    "hidden": spec["hidden"], "layers": spec["layers"], "heads": spec["heads"],
                    "kv_heads": spec["kv_heads"], "head_dim": spec["head_dim"], "ffn": spec["ffn"],
                    "vocab": spec["vocab"], "context": args.ctx, "batch": 1},

@@ -18,13 +18,13 @@
 // do not communicate (no fences or atomics).
 //
 // Arithmetic.  Q4_K (the reference's own layout) runs on v_dot8_i32_i4.  Each
-// lane quantises its 32 activations v (times the norm weight) to 16 bits,
-// X = rint(v / s) with s = max|v| / 30000, and splits X into four signed-nibble
-// planes: X + 0x8888 has the digits t_p + 8, so the planes hold t_p directly
+// lane quantises its 32 activations v (times the norm weight) to 24 bits,
+// X = rint(v / s) with s = max|v| / 4194000, and splits X into six signed-nibble
+// planes: X + 0x888888 has the digits t_p + 8, so the planes hold t_p directly
 // after an XOR with 8 (X = sum_p 16^p t_p).  The weight nibble ^ 8 is q - 8 as
-// an int4, so four dot8 per 8 elements give sum (q-8) X exactly in int32; the
+// an int4, so six dot8 per 8 elements give the plane sums exactly in int32; the
 // sub-block result is (d*sc) * s * S - (dmin*m) * sum(v).  The quantisation
-// error is at most s/2 per element.  The other types dequantise in registers
+// error is at most s/2 = 1.2e-7 max|v| per element, the size of fp32 rounding.  The other types dequantise in registers
 // and accumulate in fp32.  RmsNorm of the input (VectorMath.RmsNorm,
 // VM:308-340) is folded in: the lanes multiply by the norm weight, the
 // workgroup reduces sum(h^2), and each row sum is scaled by 1/rms at the end.
@@ -99,10 +99,21 @@ struct RawW {
 
 // ---- activations of one lane -----------------------------------------------------
 
+constexpr int XQ_PLANES = 6;            // 24-bit activations
+constexpr float XQ_MAX = 4194000.0f;    // |X| < 2^22: exact rint by the 1.5 * 2^23 constant
+
 struct XQ {            // Q4_K path
-    uint32_t pl[16];   // pl[4p + j]: nibble k = digit p of X[8j + k] as a signed int4
-    float s, sum;      // v ~= s * X;  sum = sum(v)
+    uint32_t pl[4 * XQ_PLANES];   // pl[4p + j]: nibble k = digit p of X[8j + k] as a signed int4
+    float s, sum;                 // v ~= s * X;  sum = sum(v)
 };
+
+// Byte b of Y[0], Y[2], Y[4], Y[6] (or of the odd elements) in one dword.
+__device__ __forceinline__ uint32_t gather_bytes(uint32_t y0, uint32_t y2, uint32_t y4, uint32_t y6, int b) {
+    const uint32_t sel = b == 0 ? 0x0C0C0400u : (b == 1 ? 0x0C0C0501u : 0x0C0C0602u);
+    const uint32_t lo = __builtin_amdgcn_perm(y2, y0, sel);   // [y0.b, y2.b, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm(y6, y4, sel);   // [y4.b, y6.b, 0, 0]
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);        // [y0.b, y2.b, y4.b, y6.b]
+}
 
 __device__ __forceinline__ void quantize32(const float* v, XQ& q) {
     float amax = 0.f, sum = 0.f;
@@ -111,32 +122,28 @@ __device__ __forceinline__ void quantize32(const float* v, XQ& q) {
         amax = fmaxf(amax, fabsf(v[i]));
         sum += v[i];
     }
-    const float scale = amax > 0.f ? 30000.0f / amax : 0.f;
-    q.s = amax > 0.f ? amax / 30000.0f : 0.f;
+    const float scale = amax > 0.f ? XQ_MAX / amax : 0.f;
+    q.s = amax > 0.f ? amax / XQ_MAX : 0.f;
     q.sum = sum;
     uint32_t Y[32];
 #pragma unroll
     for (int i = 0; i < 32; i++) {
-        // rint through the 1.5 * 2^23 constant: the low bits of the sum hold X
-        // (|v * scale| <= 30000 + rounding), so Y = X + 0x8888 lies in [0, 65535].
+        // rint through the 1.5 * 2^23 constant: the low 23 bits of the sum hold
+        // 2^22 + X, so Y = X + 0x888888 lies in [0, 2^24) with digits t_p + 8.
         const float f = v[i] * scale + 12582912.0f;
-        Y[i] = __float_as_uint(f) - (0x4B400000u - 0x8888u);
+        Y[i] = __float_as_uint(f) - (0x4B400000u - 0x888888u);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const uint32_t* y = Y + 8 * j;
-        const uint32_t q02 = y[0] | (y[2] << 16), q46 = y[4] | (y[6] << 16);
-        const uint32_t q13 = y[1] | (y[3] << 16), q57 = y[5] | (y[7] << 16);
-        // byte i of E / O: low byte of Y[2i] / Y[2i+1]; Eh / Oh the high bytes
-        const uint32_t E = __builtin_amdgcn_perm(q46, q02, 0x06040200u);
-        const uint32_t Eh = __builtin_amdgcn_perm(q46, q02, 0x07050301u);
-        const uint32_t O = __builtin_amdgcn_perm(q57, q13, 0x06040200u);
-        const uint32_t Oh = __builtin_amdgcn_perm(q57, q13, 0x07050301u);
-        const uint32_t m = 0x0F0F0F0Fu;
-        q.pl[0 + j] = ((E & m) | ((O << 4) & ~m)) ^ 0x88888888u;
-        q.pl[4 + j] = (((E >> 4) & m) | (O & ~m)) ^ 0x88888888u;
-        q.pl[8 + j] = ((Eh & m) | ((Oh << 4) & ~m)) ^ 0x88888888u;
-        q.pl[12 + j] = (((Eh >> 4) & m) | (Oh & ~m)) ^ 0x88888888u;
+#pragma unroll
+        for (int b = 0; b < 3; b++) {   // byte b of Y holds digits 2b (low nibble) and 2b + 1
+            const uint32_t E = gather_bytes(y[0], y[2], y[4], y[6], b);
+            const uint32_t O = gather_bytes(y[1], y[3], y[5], y[7], b);
+            const uint32_t m = 0x0F0F0F0Fu;
+            q.pl[4 * (2 * b) + j] = ((E & m) | ((O << 4) & ~m)) ^ 0x88888888u;
+            q.pl[4 * (2 * b + 1) + j] = (((E >> 4) & m) | (O & ~m)) ^ 0x88888888u;
+        }
     }
 }
 
@@ -161,19 +168,20 @@ struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
     }
     __device__ static float dot(const Raw& r, int u, const XQ& x) {
         const uint32_t w[4] = {r.q.x ^ 0x88888888u, r.q.y ^ 0x88888888u, r.q.z ^ 0x88888888u, r.q.w ^ 0x88888888u};
-        int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+        int a[XQ_PLANES];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            a0 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[j], a0, false);
-            a1 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 + j], a1, false);
-            a2 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[8 + j], a2, false);
-            a3 = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[12 + j], a3, false);
+        for (int p = 0; p < XQ_PLANES; p++) {
+            a[p] = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) a[p] = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 * p + j], a[p], false);
         }
-        const int S = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);
+        // sum (q-8) X = sum_p 16^p a_p; |a_p| <= 2048, so each half is exact in int32
+        const int lo = a[0] + (a[1] << 4) + (a[2] << 8), hi = a[3] + (a[4] << 4) + (a[5] << 8);
+        const float S = (float)lo + 4096.0f * (float)hi;
         float sc, m;
         kscale(r.h.y, r.h.z, r.h.w, u & 7, sc, m);
         const float d = h16(r.h.x & 0xFFFFu), dm = h16(r.h.x >> 16);
-        return (d * sc) * (x.s * (float)S) - (dm * m) * x.sum;
+        return (d * sc) * (x.s * S) - (dm * m) * x.sum;
     }
 };
 
@@ -653,13 +661,13 @@ bool gemv_width_ok(uint32_t type, int cols) {
     return cols % block_elems(type) == 0 && cols / 32 <= MAXW * 64;
 }
 
-// Wavefronts a launch should have at least (8 per CU); LLMDOT_GEMV_WAVES
-// overrides it for tuning.
+// Wavefronts a launch should have at least (4 per CU: fewer, longer
+// workgroups amortise the activation loads); LLMDOT_GEMV_WAVES overrides it.
 static int target_waves() {
     static const int w = [] {
         const char* e = getenv("LLMDOT_GEMV_WAVES");
         const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 2048;
+        return v > 0 ? v : 1024;
     }();
     return w;
 }

@@ -51,11 +51,22 @@ LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_
 
 
 class LoadedModel:
-    """A parsed GGUF model (tensors are zero-copy views of the file or image)."""
+    """A parsed GGUF model (tensors are zero-copy views of the file or image).
+
+    Device copies of its tensors live in a backend under `key_prefix + name`;
+    the prefix is unique per LoadedModel, so engines of different models that
+    share one backend never see each other's weights, while engines of the
+    same model share one copy.
+    """
+
+    _next_id = 0
 
     def __init__(self, g: gguf.GgufModel, config: gguf.TransformerConfig):
         self.gguf = g
         self.config = config
+        LoadedModel._next_id += 1
+        self.key_prefix = f"model{LoadedModel._next_id}/"
+        self._users = {}   # id(backend) -> number of live engines using the uploaded copy
 
     @classmethod
     def load(cls, source) -> "LoadedModel":
@@ -93,10 +104,13 @@ class InferenceEngine:
         self.backend = backend or HipBackend()
         self._own_backend = backend is None
         self.context = int(context or cfg.context_length)
+        prefix = model.key_prefix
         for name in model.decode_tensor_names():
             t = model.tensor(name)
-            if not self.backend.has_weight(name):
-                self.backend.upload_weight(name, t.ggml_type, t.data, t.rows, t.cols)
+            if not self.backend.has_weight(prefix + name):
+                self.backend.upload_weight(prefix + name, t.ggml_type, t.data, t.rows, t.cols)
+        model._users[id(self.backend)] = model._users.get(id(self.backend), 0) + 1
+        self._weights_held = True
         d = _lib.ModelDesc()
         d.hidden, d.layers = cfg.hidden_size, cfg.layer_count
         d.heads, d.kv_heads, d.head_dim = cfg.head_count, cfg.head_count_kv, cfg.head_dim
@@ -107,7 +121,7 @@ class InferenceEngine:
                                 if cfg.rope_scaling_type == "linear" and cfg.rope_scaling_factor > 1 else 1.0)
         d.kv_fp16 = 1 if kv_fp16 else 0
         d.bos = cfg.bos_token_id
-        d.key_prefix = None
+        d.key_prefix = prefix.encode()
         self._m = C.c_void_p()
         _call(lib().llmdot_hip_model_create(self.backend.handle, C.byref(d), C.byref(self._m)))
         self.vocab = cfg.vocab_size
@@ -116,6 +130,15 @@ class InferenceEngine:
         if getattr(self, "_m", None):
             lib().llmdot_hip_model_destroy(self._m)
             self._m = C.c_void_p()
+        if getattr(self, "_weights_held", False) and self.backend is not None:
+            # the last engine of this model on this backend frees the device copy
+            self._weights_held = False
+            users = self.model._users
+            users[id(self.backend)] -= 1
+            if users[id(self.backend)] == 0:
+                del users[id(self.backend)]
+                for name in self.model.decode_tensor_names():
+                    self.backend.release_weight(self.model.key_prefix + name)
         if getattr(self, "_own_backend", False) and self.backend is not None:
             self.backend.dispose()
             self.backend = None

@@ -104,8 +104,18 @@ def synth_tensor(ggml_type: int, rows: int, cols: int, seed: int, out: np.ndarra
     check(lib().llmdot_hip_synth_weights(ggml_type, rows, cols, seed, sigma, C.c_void_p(out.ctypes.data), nt))
 
 
+def tensor_sigma(name: str, spec: dict, sigma: float, scaled_init: bool) -> float:
+    """Init std of a tensor: sigma, and sigma / sqrt(2 L) for the two projections
+    that write into the residual stream (attn_output, ffn_down) when
+    scaled_init, the usual scaled initialisation of an L-layer transformer; it
+    keeps the residual stream from growing layer by layer."""
+    if scaled_init and (".attn_output." in name or ".ffn_down." in name):
+        return sigma / float(np.sqrt(2.0 * spec["layers"]))
+    return sigma
+
+
 def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
-                threads: int | None = None, spec: dict | None = None) -> np.ndarray:
+                threads: int | None = None, spec: dict | None = None, scaled_init: bool = True) -> np.ndarray:
     """Builds the whole GGUF file image in memory (uint8 numpy array)."""
     spec = spec or SPECS[name]
     tl = tensor_list(spec)
@@ -120,7 +130,7 @@ def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int |
         if n.endswith("_norm.weight"):
             view.view(np.float32)[:] = 1.0
         else:
-            synth_tensor(t, r, c, tensor_seed(seed, n), view, sigma, threads)
+            synth_tensor(t, r, c, tensor_seed(seed, n), view, tensor_sigma(n, spec, sigma, scaled_init), threads)
         nxt = base + off + nb
         pad = (32 - nxt % 32) % 32
         img[nxt:nxt + pad] = 0
