@@ -19,6 +19,18 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_q4k_mistral7b_traffic.md")
+
+
+def measured_traffic(config: str):
+    """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (counters cannot be read inside a normal run)."""
+    if config != "mistral7b" or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    for line in open(TRAFFIC_PROFILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def log(msg: str) -> None:
@@ -109,6 +121,9 @@ def main() -> int:
 
     # dominant kernel: the fused gate/up SwiGLU GEMV, bracketed with HIP events
     kr = eng.time_decode(tok, pos + args.warmup + args.steps, args.kernel_steps, per_kernel=True)
+    from dotllm_amd.measure import stream_peak_gbps
+    stream = stream_peak_gbps(be, 1 << 30, 10)
+    log(f"streaming probe over 1 GiB: read {stream['read']:.0f} GB/s, write {stream['write']:.0f} GB/s")
     per_launch_ms = kr["gemv_ms"] / max(kr["gemv_launches"], 1)
     per_launch_bytes = kr["gemv_bytes"] / max(kr["gemv_launches"], 1)
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
@@ -135,10 +150,11 @@ def main() -> int:
                    "vocab": spec["vocab"], "context": args.ctx, "batch": 1},
         "step_hbm": {"bytes_per_token": step_bytes, "achieved_gbps": round(step_bytes / ms_step / 1e6, 1),
                      "peak_gbps": HBM_PEAK_GBPS, "frac": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBPS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<Q4_K, RMSNORM, SWIGLU> (ffn gate+up)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<Q4_K, SWIGLU, RmsNorm> (ffn gate+up, 14336x4096 x2)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "bytes_per_launch": per_launch_bytes, "us_per_launch": round(per_launch_ms * 1e3, 2)},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.config),
+                     "bytes_per_launch": per_launch_bytes, "us_per_launch": round(per_launch_ms * 1e3, 2),
+                     "stream_probe_gbps": {k: round(v, 1) for k, v in stream.items()}},
         "cpu_baseline": None,
     }
     eng.dispose()

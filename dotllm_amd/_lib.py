@@ -104,6 +104,7 @@ SIGNATURES = {
     "llmdot_hip_synchronize": [_P],
     "llmdot_hip_gemv_device": [_P, _U32, _P, _P, _P, _I32, _I32],
     "llmdot_hip_time_gemv": [_P, _U32, _PP, _I32, _P, _P, _I32, _I32, _I32, C.POINTER(C.c_float)],
+    "llmdot_hip_stream_bench": [_P, C.c_size_t, _I32, _I32, C.POINTER(C.c_float)],
     "llmdot_hip_model_create": [_P, C.POINTER(ModelDesc), _PP],
     "llmdot_hip_model_destroy": [_P],
     "llmdot_hip_model_reset": [_P],

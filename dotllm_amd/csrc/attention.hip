@@ -155,7 +155,8 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
 
 template <int HD, int G>
 __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
-    constexpr int DPG = HD / 16;          // V elements per thread and position
+    constexpr int DPG = HD / 16;                 // V elements per thread and position
+    constexpr int SPT = (G * CH + WG - 1) / WG;  // scores per thread
     __shared__ float p_s[G][CH];
     __shared__ float red[4][G * HD];
     __shared__ float gmax[G];
@@ -169,34 +170,56 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     const int dg = t & 15, pg = t >> 4;
     const int64_t cache_base = (int64_t)kvh * a.context * HD;
 
-    // V rows of positions pg + 16 i, issued first (rows past T read row p0)
+    // Every global load is issued before any is used: the V rows of positions
+    // pg + 16 i (rows past T read row p0), this chunk's scores, and the chunk
+    // maxima of this wavefront's heads.
     float vv[4][DPG];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int p = pg + 16 * i;
         load_kv_row<DPG>(a.vcache, cache_base + (int64_t)(p0 + (p < cnt ? p : 0)) * HD + dg * DPG, a.kv_fp16, vv[i]);
     }
+    float sc[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int idx = min(t + k * WG, G * CH - 1);
+        const int h = idx / CH, p = idx - h * CH;
+        sc[k] = a.scores[(int64_t)(kvh * G + h) * a.context + p0 + (p < cnt ? p : 0)];
+    }
+    constexpr int HPW = (G + 3) / 4;             // heads per wavefront for the global max
+    float cm[HPW][2];
+#pragma unroll
+    for (int j = 0; j < HPW; j++) {
+        const int h = min(wave + 4 * j, G - 1);
+        const float* row = a.chunk_max + (int64_t)(kvh * G + h) * gridDim.x;
+        cm[j][0] = row[min(lane, nch - 1)];        // repeats of entry nch-1 do not change the max
+        cm[j][1] = row[min(lane + 64, nch - 1)];
+    }
     // global max of each head's scores (Softmax's max over all n)
-    for (int h = wave; h < G; h += 4) {
-        const float* cm = a.chunk_max + (int64_t)(kvh * G + h) * gridDim.x;
-        float m = -INFINITY;
-        for (int i = lane; i < nch; i += 64) m = fmaxf(m, cm[i]);
+#pragma unroll
+    for (int j = 0; j < HPW; j++) {
+        const int h = wave + 4 * j;
+        float m = fmaxf(cm[j][0], cm[j][1]);
+        for (int i = lane + 128; i < nch; i += 64) m = fmaxf(m, a.chunk_max[(int64_t)(kvh * G + min(h, G - 1)) * gridDim.x + i]);
         m = wave_max(m);
-        if (lane == 0) gmax[h] = m;
+        if (h < G && lane == 0) gmax[h] = m;
     }
     __syncthreads();
-    for (int idx = t; idx < G * CH; idx += WG) {
-        const int h = idx / CH, p = idx - h * CH;
-        const int sidx = p0 + (p < cnt ? p : 0);
-        const float sc = a.scores[(int64_t)(kvh * G + h) * a.context + sidx];
-        float e;
-        {
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int idx = t + k * WG;
+        if (idx < G * CH) {
+            const int h = idx / CH, p = idx - h * CH;
+            const int sidx = p0 + p;
+            float e;
+            {
 #pragma clang fp contract(off)
-            const float x = sc - gmax[h];
-            // Softmax: ExpApprox on the vector lanes (first 8*floor(n/8)), expf on the tail
-            e = sidx < n8 ? exp_approx(x) : expf(x);
+                const float x = sc[k] - gmax[h];
+                // Softmax: ExpApprox on the vector lanes (first 8*floor(n/8)), expf on the tail
+                e = sidx < n8 ? exp_approx(x) : expf(x);
+            }
+            p_s[h][p] = p < cnt ? e : 0.f;
         }
-        p_s[h][p] = p < cnt ? e : 0.f;
     }
     __syncthreads();
     for (int h = wave; h < G; h += 4) {   // this chunk's sum of exponentials
@@ -230,18 +253,35 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
 }
 
 // out = sum_c part_out[c] / sum_c part_sum[c] for one q head per workgroup
-// (a separate launch: the chunk partials are visible without fences).
+// (a separate launch: the chunk partials are visible without fences).  NG
+// groups of HD threads each take every NG-th chunk; the group sums are then
+// added in group order.
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(1024) void attn_combine_kernel(AttnArgs a) {
+    constexpr int NG = 1024 / HD;
+    __shared__ float acc_s[NG][HD];
+    __shared__ float z_s[NG];
     const int n = *a.pos + 1;
     const int nch = (n + CH - 1) / CH;
-    const int hq = blockIdx.x, d = threadIdx.x;
+    const int hq = blockIdx.x, g = threadIdx.x / HD, d = threadIdx.x - g * HD;
     float acc = 0.f, z = 0.f;
-    for (int i = 0; i < nch; i++) {
+#pragma unroll 4
+    for (int i = g; i < nch; i += NG) {
         acc += a.part_out[((int64_t)i * a.heads + hq) * HD + d];
         z += a.part_sum[(int64_t)i * a.heads + hq];
     }
-    a.out[(int64_t)hq * HD + d] = acc * (1.0f / z);
+    acc_s[g][d] = acc;
+    if (d == 0) z_s[g] = z;
+    __syncthreads();
+    if (g == 0) {
+        float at = 0.f, zt = 0.f;
+#pragma unroll
+        for (int k = 0; k < NG; k++) {
+            at += acc_s[k][d];
+            zt += z_s[k];
+        }
+        a.out[(int64_t)hq * HD + d] = at * (1.0f / zt);
+    }
 }
 
 template <int HD, int G>
@@ -254,7 +294,7 @@ hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
     attn_pv_kernel<HD, G><<<grid, WG, 0, s>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_combine_kernel<HD><<<a.heads, HD, 0, s>>>(a);
+    attn_combine_kernel<HD><<<a.heads, (1024 / HD) * HD, 0, s>>>(a);
     return hipGetLastError();
 }
 

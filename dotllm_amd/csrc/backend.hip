@@ -512,6 +512,39 @@ extern "C" int32_t llmdot_hip_time_gemv(llmdot_hip_ctx* ctx, uint32_t type, cons
     return 0;
 }
 
+extern "C" int32_t llmdot_hip_stream_bench(llmdot_hip_ctx* ctx, size_t nbytes, int32_t mode, int32_t iters, float* ms) {
+    if (!ctx || !ms || nbytes < 16 || iters <= 0 || (mode != 0 && mode != 1))
+        return fail(LLMDOT_E_INVALID, "bad stream_bench arguments");
+    if (int rc = ensure_device(ctx)) return rc;
+    void* buf = nullptr;
+    uint32_t* sink = nullptr;
+    hipError_t e = hipMalloc(&buf, nbytes);
+    if (e != hipSuccess) return fail(LLMDOT_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    int rc = 0;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto run = [&]() -> hipError_t {
+        hipError_t r;
+        if ((r = hipMalloc(&sink, 4)) != hipSuccess) return r;
+        if ((r = hipMemsetAsync(buf, 0, nbytes, ctx->stream)) != hipSuccess) return r;
+        if ((r = hipEventCreate(&e0)) != hipSuccess || (r = hipEventCreate(&e1)) != hipSuccess) return r;
+        if ((r = launch_stream_probe(buf, nbytes, mode, sink, ctx->stream)) != hipSuccess) return r;   // warm-up
+        if ((r = hipEventRecord(e0, ctx->stream)) != hipSuccess) return r;
+        for (int i = 0; i < iters; i++)
+            if ((r = launch_stream_probe(buf, nbytes, mode, sink, ctx->stream)) != hipSuccess) return r;
+        if ((r = hipEventRecord(e1, ctx->stream)) != hipSuccess) return r;
+        if ((r = hipEventSynchronize(e1)) != hipSuccess) return r;
+        return hipEventElapsedTime(ms, e0, e1);
+    };
+    e = run();
+    if (e != hipSuccess) rc = fail(LLMDOT_E_DEVICE, std::string("stream_bench: ") + hipGetErrorString(e));
+    (void)hipStreamSynchronize(ctx->stream);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (sink) (void)hipFree(sink);
+    (void)hipFree(buf);
+    return rc;
+}
+
 // ================================================================== model ==
 
 namespace {
@@ -548,11 +581,6 @@ struct llmdot_hip_model {
     int am_cap = 0;
     hipGraphExec_t graph = nullptr;
     bool use_graph = true;
-    // per-kernel timing (eager mode only)
-    std::vector<hipEvent_t> ev;
-    int ev_used = 0;
-    bool timing = false;
-    double gemv_bytes_per_launch = 0;
 };
 
 namespace {
@@ -603,21 +631,20 @@ int check_gemv_type(const Weight* w, const std::string& name) {
     return 0;
 }
 
-// GEMV launch on the model stream; the dominant launches are bracketed with
-// HIP events in timing mode.
-hipError_t step_gemv(llmdot_hip_model* m, uint32_t type, int epi, GemvArgs& a, bool dominant) {
+// GEMV launch on the model stream.
+hipError_t step_gemv(llmdot_hip_model* m, uint32_t type, int epi, GemvArgs& a) {
     a.eps = m->d.eps;
-    hipStream_t s = m->ctx->stream;
-    if (m->timing && dominant && m->ev_used + 2 <= (int)m->ev.size()) {
-        hipError_t e = hipEventRecord(m->ev[m->ev_used], s);
-        if (e != hipSuccess) return e;
-        e = launch_gemv(type, epi, a, s);
-        if (e != hipSuccess) return e;
-        e = hipEventRecord(m->ev[m->ev_used + 1], s);
-        m->ev_used += 2;
-        return e;
-    }
-    return launch_gemv(type, epi, a, s);
+    return launch_gemv(type, epi, a, m->ctx->stream);
+}
+
+// FFN gate/up over RmsNorm(h), SiLU(gate) * up (IE:190, IE:463-474): the
+// step's dominant launch.
+hipError_t launch_gate_up(llmdot_hip_model* m, int l) {
+    const LayerW& w = m->L[l];
+    GemvArgs ga{};
+    ga.nseg = 1; ga.seg[0] = {w.gate->dev, w.up->dev, m->act, m->d.ffn, 0};
+    ga.cols = m->d.hidden; ga.x = m->h; ga.norm_w = w.ffn_norm_f; ga.norm = 1;
+    return step_gemv(m, w.gate->type, EPI_SWIGLU, ga);
 }
 
 // Enqueues one decode step on the model stream (token and position on the device).
@@ -628,21 +655,28 @@ int enqueue_step(llmdot_hip_model* m) {
     HIPCHK(launch_embed(m->embd->dev, m->embd->type, d.hidden, m_token(m), m->h, s));
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
-        // Q, K, V projections over RmsNorm(h) (IE:185-186, IE:333-353); same-type tensors share a launch.
+        // Q, K, V projections over RmsNorm(h) (IE:185-186, IE:333-353) in one launch when the
+        // types allow (one type, or the Q4_K_M mix of Q4_K and Q6_K), else one per type.
         const Weight* mats[3] = {w.q, w.k, w.v};
         float* outs[3] = {m->q, m->k, m->v};
         int rows[3] = {qdim, kvdim, kvdim};
+        bool mixed_ok = true, any_q4k = false;
+        for (int i = 0; i < 3; i++) {
+            mixed_ok = mixed_ok && (mats[i]->type == GGML_Q4_K || mats[i]->type == GGML_Q6_K);
+            any_q4k = any_q4k || mats[i]->type == GGML_Q4_K;
+        }
         bool done[3] = {false, false, false};
         for (int i = 0; i < 3; i++) {
             if (done[i]) continue;
             GemvArgs ga{};
             ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.attn_norm_f; ga.norm = 1;
+            const uint32_t lt = mixed_ok && any_q4k ? (uint32_t)GGML_Q4_K : mats[i]->type;
             for (int j = i; j < 3; j++)
-                if (!done[j] && mats[j]->type == mats[i]->type) {
-                    ga.seg[ga.nseg++] = {mats[j]->dev, nullptr, outs[j], rows[j], 0};
+                if (!done[j] && (mats[j]->type == mats[i]->type || (mixed_ok && any_q4k))) {
+                    ga.seg[ga.nseg++] = {mats[j]->dev, nullptr, outs[j], rows[j], 0, mats[j]->type};
                     done[j] = true;
                 }
-            HIPCHK(step_gemv(m, mats[i]->type, EPI_STORE, ga, false));
+            HIPCHK(step_gemv(m, lt, EPI_STORE, ga));
         }
         AttnArgs aa{};
         aa.q = m->q; aa.k = m->k; aa.v = m->v;
@@ -658,19 +692,14 @@ int enqueue_step(llmdot_hip_model* m) {
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.o->dev, nullptr, m->h, d.hidden, 0};
             ga.cols = qdim; ga.x = m->attn;
-            HIPCHK(step_gemv(m, w.o->type, EPI_ADD, ga, false));
+            HIPCHK(step_gemv(m, w.o->type, EPI_ADD, ga));
         }
-        {   // gate/up over RmsNorm(h), SiLU(gate) * up (IE:190, IE:463-474)
-            GemvArgs ga{};
-            ga.nseg = 1; ga.seg[0] = {w.gate->dev, w.up->dev, m->act, d.ffn, 0};
-            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.ffn_norm_f; ga.norm = 1;
-            HIPCHK(step_gemv(m, w.gate->type, EPI_SWIGLU, ga, true));
-        }
+        HIPCHK(launch_gate_up(m, l));
         {   // down projection + residual (IE:475, IE:195)
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.down->dev, nullptr, m->h, d.hidden, 0};
             ga.cols = d.ffn; ga.x = m->act;
-            HIPCHK(step_gemv(m, w.down->type, EPI_ADD, ga, false));
+            HIPCHK(step_gemv(m, w.down->type, EPI_ADD, ga));
         }
     }
     {   // final RmsNorm + LM head + greedy ArgMax (IE:575-602, Sampler.cs:26-27)
@@ -680,7 +709,7 @@ int enqueue_step(llmdot_hip_model* m) {
         ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx; ga.am.cap = m->am_cap;
         ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
         ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
-        HIPCHK(step_gemv(m, m->out->type, EPI_ARGMAX, ga, false));
+        HIPCHK(step_gemv(m, m->out->type, EPI_ARGMAX, ga));
     }
     return 0;
 }
@@ -702,7 +731,7 @@ int build_graph(llmdot_hip_model* m) {
 }
 
 int run_step(llmdot_hip_model* m) {
-    if (m->graph && !m->timing) {
+    if (m->graph) {
         HIPCHK(hipGraphLaunch(m->graph, m->ctx->stream));
         return 0;
     }
@@ -721,7 +750,6 @@ extern "C" int32_t llmdot_hip_model_destroy(llmdot_hip_model* m) {
     (void)hipSetDevice(m->ctx->device);
     (void)hipStreamSynchronize(m->ctx->stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
-    for (auto e : m->ev) (void)hipEventDestroy(e);
     for (void* p : m->owned) (void)hipFree(p);
     delete m;
     return 0;
@@ -1016,40 +1044,28 @@ extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t fir
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0));
     HIPCHK(hipEventCreate(&e1));
-    if (per_kernel) {
-        const int need = 2 * m->d.layers;
-        while ((int)m->ev.size() < need) {
-            hipEvent_t e;
-            HIPCHK(hipEventCreate(&e));
-            m->ev.push_back(e);
-        }
-        m->timing = true;
-    }
-    double gemv_ms = 0;
-    int launches = 0;
     HIPCHK(hipStreamSynchronize(s));
     HIPCHK(hipEventRecord(e0, s));
+    int launches = 0;
     for (int i = 0; i < steps; i++) {
-        m->ev_used = 0;
-        int rc = run_step(m);
-        if (rc) { m->timing = false; return rc; }
         if (per_kernel) {
-            HIPCHK(hipStreamSynchronize(s));
-            for (int j = 0; j + 1 < m->ev_used; j += 2) {
-                float ms = 0;
-                HIPCHK(hipEventElapsedTime(&ms, m->ev[j], m->ev[j + 1]));
-                gemv_ms += ms;
+            // the dominant kernel alone: every layer's gate/up launch back to
+            // back (2 GB of distinct weights per pass, past any cache)
+            for (int l = 0; l < m->d.layers; l++) {
+                HIPCHK(launch_gate_up(m, l));
                 launches++;
             }
+        } else if (int rc = run_step(m)) {
+            return rc;
         }
     }
     HIPCHK(hipEventRecord(e1, s));
     HIPCHK(hipEventSynchronize(e1));
-    m->timing = false;
     float total = 0;
     HIPCHK(hipEventElapsedTime(&total, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    const double gemv_ms = per_kernel ? total : 0.0;
     out->total_ms = total;
     out->gemv_ms = (float)gemv_ms;
     out->gemv_launches = launches;

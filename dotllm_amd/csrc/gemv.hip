@@ -8,10 +8,11 @@
 // reduction dimension.  It has ceil(U/64) wavefronts, U being the number of
 // 32-element "units" of a row, and lane L of wavefront w owns unit 64w + L in
 // every row, so a lane's activations are loaded once and stay in registers
-// while the rows stream through.  Rows go in batches (8 rows, or 4 gate + 4 up
-// rows for the SwiGLU form; fewer for the wide types); the loads of batch b+1
-// are issued before batch b is computed, so every wavefront keeps two batches
-// of loads in flight.  A row's lane partials are summed over 16-lane rows with
+// while the rows stream through.  Rows go in batches (2 to 8 rows by type, half
+// gate and half up rows for the SwiGLU form); the loads of batch b+1 are
+// issued before batch b is computed, so every wavefront keeps two batches of
+// loads in flight.  One launch may cover up to three matrices (segments),
+// e.g. Q, K and V, also of two types with equal batch geometry (Q4_K + Q6_K).  A row's lane partials are summed over 16-lane rows with
 // DPP rotations, then over quarter-wavefronts and wavefronts through LDS, in a
 // fixed order.  The loads carry no branches (lanes past the end of a row read
 // unit 0 and contribute 0), so the compiler keeps them all in flight.  Workgroups
@@ -158,29 +159,39 @@ struct XF {
 // ---- per-type row units -----------------------------------------------------------
 // RUN: contiguous elements per run of a unit; xoff(u, run) its first element.
 
+struct __attribute__((aligned(4))) u32x2 { uint32_t x, y; };
+
 struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
-    static constexpr int RB = 8, NS = 1, PRE = 2;
-    struct Raw { u32x4 h, q; };
+    // 4 rows per batch keep the kernel near 100 VGPRs (4 wavefronts per SIMD)
+    static constexpr int RB = 4, NS = 1, PRE = 2;
+    // dd: d | dmin << 16; f: the two header words holding sub-block g's
+    // 12-bit (sc, m) field, which starts at bit 32 + 12 g of the block (the
+    // 6-bit stream begins at byte 4, LSB first), i.e. at bit (12 g) mod 32 of
+    // word 1 + 12 g / 32; q: the sub-block's 16 nibble bytes.
+    struct Raw { uint32_t dd; u32x2 f; u32x4 q; };
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
         const uint8_t* blk = row + (u >> 3) * 144;
-        r.h = ld16_a4(blk);
-        r.q = ld16_a4(blk + 16 + 16 * (u & 7));
+        const int g = u & 7;
+        r.dd = ld4_a4(blk);
+        r.f = *reinterpret_cast<const u32x2*>(blk + 4 + 4 * ((12 * g) >> 5));
+        r.q = ld16_a4(blk + 16 + 16 * g);
     }
     __device__ static float dot(const Raw& r, int u, const XQ& x) {
         const uint32_t w[4] = {r.q.x ^ 0x88888888u, r.q.y ^ 0x88888888u, r.q.z ^ 0x88888888u, r.q.w ^ 0x88888888u};
-        int a[XQ_PLANES];
+        // S = sum (q-8) X = sum_p 16^p a_p by Horner over the planes.  |S| <=
+        // 32 * 8 * 4194000 < 2^31, and int32 wrap-around is exact modulo 2^32,
+        // so the result is exact whatever the intermediate values.
+        int acc = 0;
 #pragma unroll
-        for (int p = 0; p < XQ_PLANES; p++) {
-            a[p] = 0;
+        for (int p = XQ_PLANES - 1; p >= 0; p--) {
+            if (p < XQ_PLANES - 1) acc <<= 4;
 #pragma unroll
-            for (int j = 0; j < 4; j++) a[p] = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 * p + j], a[p], false);
+            for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 * p + j], acc, false);
         }
-        // sum (q-8) X = sum_p 16^p a_p; |a_p| <= 2048, so each half is exact in int32
-        const int lo = a[0] + (a[1] << 4) + (a[2] << 8), hi = a[3] + (a[4] << 4) + (a[5] << 8);
-        const float S = (float)lo + 4096.0f * (float)hi;
-        float sc, m;
-        kscale(r.h.y, r.h.z, r.h.w, u & 7, sc, m);
-        const float d = h16(r.h.x & 0xFFFFu), dm = h16(r.h.x >> 16);
+        const float S = (float)acc;
+        const uint32_t fld = __builtin_amdgcn_alignbit(r.f.y, r.f.x, (uint32_t)((12 * (u & 7)) & 31));
+        const float sc = (float)(fld & 63u), m = (float)((fld >> 6) & 63u);
+        const float d = h16(r.dd & 0xFFFFu), dm = h16(r.dd >> 16);
         return (d * sc) * (x.s * S) - (dm * m) * x.sum;
     }
 };
@@ -381,12 +392,16 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float row_sum16(float v) {
-    v += dpp_f32<0x128>(v);   // row_ror:8
-    v += dpp_f32<0x124>(v);   // row_ror:4
-    v += dpp_f32<0x122>(v);   // row_ror:2
-    v += dpp_f32<0x121>(v);   // row_ror:1
-    return v;
+template <int N>
+__device__ __forceinline__ void row_sums16(float* v) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f32<0x128>(v[i]);   // row_ror:8
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f32<0x124>(v[i]);   // row_ror:4
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f32<0x122>(v[i]);   // row_ror:2
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f32<0x121>(v[i]);   // row_ror:1
 }
 
 // Raw activations of a lane: the unit's 32 values of x (and of the norm
@@ -481,11 +496,16 @@ __device__ __forceinline__ float gemv_rows(const GemvArgs& a, int uu, bool has, 
     }
 #pragma unroll
     for (int b = 0; b < NB; b++) {
+        float dv[RB];
 #pragma unroll
         for (int i = 0; i < RB; i++) {
-            float d = TT::dot(buf[b & 1][i], uu, x);
-            d = row_sum16(has ? d : 0.f);
-            if ((lane & 15) == 0) red_w[b * RB + i][lane >> 4] = d;
+            const float d = TT::dot(buf[b & 1][i], uu, x);
+            dv[i] = has ? d : 0.f;
+        }
+        row_sums16<RB>(dv);   // all rows level by level: no DPP hazard stalls
+        if ((lane & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < RB; i++) red_w[b * RB + i][lane >> 4] = dv[i];
         }
         if (b + 2 < NB) {
 #pragma unroll
@@ -497,9 +517,11 @@ __device__ __forceinline__ float gemv_rows(const GemvArgs& a, int uu, bool has, 
 
 // ---- the kernel -------------------------------------------------------------------
 // NB batches of RB dot rows; SwiGLU batches hold RB/2 gate then RB/2 up rows.
-template <uint32_t T, int EPI, int NB, bool NORM>
+template <uint32_t T, int EPI, int NB, bool NORM, uint32_t T2 = T>
 __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     using TT = typename TypeOf<T>::type;
+    using TT2 = typename TypeOf<T2>::type;
+    static_assert(TT2::RB == TT::RB, "mixed-type launches need equal batch geometry");
     constexpr int RB = TT::RB;
     constexpr bool SW = EPI == EPI_SWIGLU;
     constexpr int OPB = SW ? RB / 2 : RB;     // output rows per batch
@@ -522,7 +544,9 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     const int u = wave * 64 + lane;
     const bool has = u < K / 32;
     const int uu = has ? u : 0;
-    const int64_t rbytes = (int64_t)(K / block_elems(T)) * block_bytes(T);
+    const bool second = T2 != T && seg.type == T2;   // uniform per workgroup
+    const int64_t rbytes = second ? (int64_t)(K / block_elems(T2)) * block_bytes(T2)
+                                  : (int64_t)(K / block_elems(T)) * block_bytes(T);
 
     auto row_ptr = [&](int i) -> const uint8_t* {   // dot row i of this workgroup
         const int b = i / RB, k = i % RB;
@@ -537,7 +561,9 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         return base + (int64_t)(r < seg.rows ? r : 0) * rbytes;
     };
 
-    const float hsq = gemv_rows<TT, NB, NORM>(a, uu, has, row_ptr, red[wave]);
+    float hsq;
+    if (T2 != T && second) hsq = gemv_rows<TT2, NB, NORM>(a, uu, has, row_ptr, red[wave]);
+    else hsq = gemv_rows<TT, NB, NORM>(a, uu, has, row_ptr, red[wave]);
     if (NORM) {
         const float w = wave_sum(hsq);
         if (lane == 0) ssq[wave] = w;
@@ -613,6 +639,7 @@ int type_rb(uint32_t t) {
     switch (t) {
     case GGML_Q6_K: return TQ6K::RB;
     case GGML_Q8_0: return TQ8_0::RB;
+    case GGML_Q4_K: return TQ4K::RB;
     case GGML_F32: return TF32::RB;
     case GGML_F16: return TF16::RB;
     default: return 8;
@@ -694,6 +721,18 @@ int gemv_max_grid(uint32_t type, int epi, int rows, int cols) {
 
 hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     if (a.cols <= 0 || a.nseg < 1 || a.nseg > 3) return hipErrorInvalidValue;
+    // segment types: 0 means `type`; a second type is supported for Q4_K + Q6_K
+    uint32_t t2 = type;
+    for (int i = 0; i < a.nseg; i++) {
+        if (a.seg[i].type == 0) a.seg[i].type = type;
+        if (a.seg[i].type != type) {
+            if (t2 != type && a.seg[i].type != t2) return hipErrorInvalidValue;
+            t2 = a.seg[i].type;
+        }
+    }
+    if (t2 != type && !(type == GGML_Q4_K && t2 == GGML_Q6_K && epi == EPI_STORE && a.norm))
+        return hipErrorInvalidValue;
+    if (t2 != type && !gemv_width_ok(t2, a.cols)) return hipErrorInvalidValue;
     if (generic_shape(type, a.cols)) {
         if (epi != EPI_STORE || a.nseg != 1 || a.norm) return hipErrorInvalidValue;
         if (a.seg[0].rows <= 0) return hipSuccess;
@@ -724,6 +763,16 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     if (epi == EPI_ARGMAX && a.am.cap < grid) return hipErrorInvalidValue;
     const int threads = 64 * ((a.cols / 32 + 63) / 64);
     hipError_t e;
+    if (t2 != type) {   // Q4_K with Q6_K segments (Q/K/V of the Q4_K_M mix)
+        switch (nb) {
+        case 1: gemv_kernel<GGML_Q4_K, EPI_STORE, 1, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
+        case 2: gemv_kernel<GGML_Q4_K, EPI_STORE, 2, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
+        case 4: gemv_kernel<GGML_Q4_K, EPI_STORE, 4, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
+        case 8: gemv_kernel<GGML_Q4_K, EPI_STORE, 8, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (type) {
     case GGML_Q4_K: e = launch_t<GGML_Q4_K>(epi, a, nb, grid, threads, s); break;
     case GGML_Q5_K: e = launch_t<GGML_Q5_K>(epi, a, nb, grid, threads, s); break;

@@ -25,6 +25,7 @@ struct GemvSeg {
     float* out;         // rows outputs
     int rows;
     int wgs;            // workgroups of this segment (set by launch_gemv)
+    uint32_t type;      // ggml type; 0 = the launch's type (Q4_K launches accept Q6_K segments)
 };
 
 struct ArgmaxState {
@@ -72,6 +73,8 @@ int argmax_grid(int n);
 hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream_t s);
 // Second pass over ncand candidates: token_out, token_log/step, pos.
 hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s);
+// Streaming probe: reads (mode 0) or writes (mode 1) nbytes (16 B per thread).
+hipError_t launch_stream_probe(void* buf, size_t nbytes, int mode, uint32_t* sink, hipStream_t s);
 // Position bookkeeping for a captured decode step.
 hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s);
 hipError_t launch_fill_random_half(void* dst, size_t n, uint64_t seed, int fp16, hipStream_t s);

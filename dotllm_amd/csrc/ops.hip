@@ -174,6 +174,17 @@ __global__ __launch_bounds__(WG) void argmax_finish_kernel(ArgmaxState st, int n
 
 __global__ void set_scalar_kernel(int32_t* dst, int32_t v) { *dst = v; }
 
+// Streaming probes: one 16-byte load (or store) per thread.
+__global__ __launch_bounds__(WG) void stream_read_kernel(const uint4* __restrict__ p, size_t n, uint32_t* sink) {
+    const size_t i = blockIdx.x * (size_t)WG + threadIdx.x;
+    const uint4 v = i < n ? p[i] : make_uint4(0u, 0u, 0u, 0u);
+    if ((v.x ^ v.y ^ v.z ^ v.w) == 0x9E3779B9u) sink[0] = 1u;   // keeps the load
+}
+__global__ __launch_bounds__(WG) void stream_write_kernel(uint4* __restrict__ p, size_t n) {
+    const size_t i = blockIdx.x * (size_t)WG + threadIdx.x;
+    if (i < n) p[i] = make_uint4((uint32_t)i, 1u, 2u, 3u);
+}
+
 __global__ void fill_random_kernel(void* dst, size_t n, uint64_t seed, int fp16) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         uint64_t z = seed + 0x9E3779B97F4A7C15ull * (i + 1);
@@ -233,6 +244,14 @@ hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream
 hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s) {
     if (ncand <= 0 || ncand > st.cap) return hipErrorInvalidValue;
     argmax_finish_kernel<<<1, WG, 0, s>>>(st, ncand);
+    return hipGetLastError();
+}
+hipError_t launch_stream_probe(void* buf, size_t nbytes, int mode, uint32_t* sink, hipStream_t s) {
+    const size_t n = nbytes / 16;
+    if (n == 0 || (n + WG - 1) / WG > 0x7FFFFFFFu) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)((n + WG - 1) / WG);
+    if (mode == 0) stream_read_kernel<<<grid, WG, 0, s>>>(reinterpret_cast<const uint4*>(buf), n, sink);
+    else stream_write_kernel<<<grid, WG, 0, s>>>(reinterpret_cast<uint4*>(buf), n);
     return hipGetLastError();
 }
 hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s) {

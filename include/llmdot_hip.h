@@ -127,6 +127,11 @@ int32_t llmdot_hip_gemv_device(llmdot_hip_ctx* ctx, uint32_t ggml_type, const vo
 int32_t llmdot_hip_time_gemv(llmdot_hip_ctx* ctx, uint32_t ggml_type, const void* const* w_devs,
                              int32_t n_weights, const float* x_dev, float* y_dev, int32_t rows,
                              int32_t cols, int32_t iters, float* ms);
+/* Streaming probe (no reference counterpart; calibrates the HBM counters and
+ * gives the practical bandwidth ceiling): `iters` launches of a kernel that
+ * reads (mode 0) or writes (mode 1) `nbytes` of a fresh device buffer, 16 B
+ * per thread; elapsed milliseconds via HIP events. */
+int32_t llmdot_hip_stream_bench(llmdot_hip_ctx* ctx, size_t nbytes, int32_t mode, int32_t iters, float* ms);
 
 /* ---- model level: the device-resident decode step (InferenceEngine.ProcessToken,
  *      IE:134-146, LLaMA-like template IE:184-196) and greedy Generate (IE:74-132). */
@@ -178,14 +183,16 @@ int32_t llmdot_hip_kv_read(llmdot_hip_model* model, int32_t layer, int32_t posit
                            float* v);
 
 /* ---- measurement hooks for the decode step --------------------------------
- * Runs `steps` greedy decode steps from the current state (token feedback on
- * the device) and returns the elapsed milliseconds measured with HIP events on
- * the model's stream.  With per_kernel != 0 every launch of the dominant
- * quantized GEMV class is additionally bracketed with HIP events and their
- * summed duration / launch count / algorithmic bytes are reported. */
+ * per_kernel == 0: runs `steps` greedy decode steps from the current state
+ * (token feedback on the device) and returns the elapsed milliseconds measured
+ * with HIP events on the model's stream.
+ * per_kernel != 0: times the step's dominant kernel alone -- `steps` passes of
+ * every layer's FFN gate/up GEMV launched back to back between two HIP events
+ * (distinct weights per layer, so nothing is served from cache) -- and reports
+ * the launch count and their algorithmic bytes. */
 typedef struct llmdot_hip_step_timing {
     float total_ms;
-    float gemv_ms;           /* summed duration of the bracketed GEMV launches */
+    float gemv_ms;           /* per_kernel: elapsed time of the gate/up launches */
     int32_t gemv_launches;
     double gemv_bytes;       /* algorithmic bytes of those launches (weights + x + y) */
 } llmdot_hip_step_timing;
