@@ -10,14 +10,14 @@
 //
 // The reference's ExpApprox is not multiplicative, so an online (rescaling)
 // softmax cannot reproduce it; the global max must be known before any
-// exponent.  The sequence is split into chunks of 64 positions per kv head
-// (grid = chunks x kv heads; chunks past T exit), over three launches (each
-// reads what the previous wrote, so no fences or atomics are needed):
-//   scores:  RoPE + KV write + scores of the chunk + per-chunk max (per q head).
+// exponent.  The sequence is split into chunks per kv head (grid = chunks x
+// kv heads; chunks past T exit), over three launches (each reads what the
+// previous wrote, so no fences or atomics are needed):
+//   scores:  64-position chunks: RoPE + KV write + scores + chunk max (per q head).
 //            4 threads per position, each loading a quarter of the K row with
 //            16-byte loads; every K row is read once for all G q heads.
-//   pv:      global max from the chunk maxima, exponentials, chunk partial
-//            sum(e) and sum(e V) (16-byte V loads).
+//   pv:      64-position chunks: global max from the chunk maxima,
+//            exponentials, partial sum(e) and sum(e V) (16-byte V loads).
 //   combine: out = sum(eV) / sum(e) over the chunks, one q head per workgroup.
 // Loads carry no branches (positions past T read a written row and are
 // masked), so each thread's loads are all in flight together.
@@ -31,7 +31,8 @@ namespace llmdot {
 namespace {
 
 constexpr int WG = 256;
-constexpr int CH = 64;   // positions per chunk
+constexpr int CH = 64;    // positions per score chunk (scores kernel)
+constexpr int CHP = 64;   // positions per pv chunk (pv kernel; its partials feed the combine)
 
 __device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int fp16) {
     if (fp16) {
@@ -155,17 +156,19 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
 
 template <int HD, int G>
 __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
-    constexpr int DPG = HD / 16;                 // V elements per thread and position
-    constexpr int SPT = (G * CH + WG - 1) / WG;  // scores per thread
-    __shared__ float p_s[G][CH];
+    constexpr int DPG = HD / 16;                  // V elements per thread and position
+    constexpr int PPT = CHP / 16;                 // positions per thread
+    constexpr int SPT = (G * CHP + WG - 1) / WG;  // scores per thread
+    __shared__ float p_s[G][CHP];
     __shared__ float red[4][G * HD];
     __shared__ float gmax[G];
     const int T = *a.pos, n = T + 1, n8 = n & ~7;
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const int p0 = c * CH;
+    const int p0 = c * CHP;
     if (p0 >= n) return;
-    const int cnt = min(CH, n - p0);
-    const int nch = (n + CH - 1) / CH;
+    const int cnt = min(CHP, n - p0);
+    const int nch = (n + CH - 1) / CH;            // score chunks (their maxima)
+    const int cm_stride = (a.context + CH - 1) / CH;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int dg = t & 15, pg = t >> 4;
     const int64_t cache_base = (int64_t)kvh * a.context * HD;
@@ -173,26 +176,26 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     // Every global load is issued before any is used: the V rows of positions
     // pg + 16 i (rows past T read row p0), this chunk's scores, and the chunk
     // maxima of this wavefront's heads.
-    float vv[4][DPG];
+    float vv[PPT][DPG];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < PPT; i++) {
         const int p = pg + 16 * i;
         load_kv_row<DPG>(a.vcache, cache_base + (int64_t)(p0 + (p < cnt ? p : 0)) * HD + dg * DPG, a.kv_fp16, vv[i]);
     }
     float sc[SPT];
 #pragma unroll
     for (int k = 0; k < SPT; k++) {
-        const int idx = min(t + k * WG, G * CH - 1);
-        const int h = idx / CH, p = idx - h * CH;
+        const int idx = min(t + k * WG, G * CHP - 1);
+        const int h = idx / CHP, p = idx - h * CHP;
         sc[k] = a.scores[(int64_t)(kvh * G + h) * a.context + p0 + (p < cnt ? p : 0)];
     }
-    constexpr int HPW = (G + 3) / 4;             // heads per wavefront for the global max
+    constexpr int HPW = (G + 3) / 4;              // heads per wavefront for the global max
     float cm[HPW][2];
 #pragma unroll
     for (int j = 0; j < HPW; j++) {
         const int h = min(wave + 4 * j, G - 1);
-        const float* row = a.chunk_max + (int64_t)(kvh * G + h) * gridDim.x;
-        cm[j][0] = row[min(lane, nch - 1)];        // repeats of entry nch-1 do not change the max
+        const float* row = a.chunk_max + (int64_t)(kvh * G + h) * cm_stride;
+        cm[j][0] = row[min(lane, nch - 1)];       // repeats of entry nch-1 do not change the max
         cm[j][1] = row[min(lane + 64, nch - 1)];
     }
     // global max of each head's scores (Softmax's max over all n)
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     for (int j = 0; j < HPW; j++) {
         const int h = wave + 4 * j;
         float m = fmaxf(cm[j][0], cm[j][1]);
-        for (int i = lane + 128; i < nch; i += 64) m = fmaxf(m, a.chunk_max[(int64_t)(kvh * G + min(h, G - 1)) * gridDim.x + i]);
+        for (int i = lane + 128; i < nch; i += 64) m = fmaxf(m, a.chunk_max[(int64_t)(kvh * G + min(h, G - 1)) * cm_stride + i]);
         m = wave_max(m);
         if (h < G && lane == 0) gmax[h] = m;
     }
@@ -208,8 +211,8 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < SPT; k++) {
         const int idx = t + k * WG;
-        if (idx < G * CH) {
-            const int h = idx / CH, p = idx - h * CH;
+        if (idx < G * CHP) {
+            const int h = idx / CHP, p = idx - h * CHP;
             const int sidx = p0 + p;
             float e;
             {
@@ -223,7 +226,10 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     }
     __syncthreads();
     for (int h = wave; h < G; h += 4) {   // this chunk's sum of exponentials
-        const float z = wave_sum(p_s[h][lane]);
+        float z = 0.f;
+#pragma unroll
+        for (int k = 0; k < CHP / 64; k++) z += p_s[h][lane + 64 * k];
+        z = wave_sum(z);
         if (lane == 0) a.part_sum[(int64_t)c * a.heads + kvh * G + h] = z;
     }
 #pragma unroll
@@ -232,7 +238,7 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
 #pragma unroll
         for (int d = 0; d < DPG; d++) acc[d] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < PPT; i++) {
             const float pr = p_s[h][pg + 16 * i];
 #pragma unroll
             for (int d = 0; d < DPG; d++) acc[d] += pr * vv[i][d];
@@ -262,7 +268,7 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(AttnArgs a) {
     __shared__ float acc_s[NG][HD];
     __shared__ float z_s[NG];
     const int n = *a.pos + 1;
-    const int nch = (n + CH - 1) / CH;
+    const int nch = (n + CHP - 1) / CHP;
     const int hq = blockIdx.x, g = threadIdx.x / HD, d = threadIdx.x - g * HD;
     float acc = 0.f, z = 0.f;
 #pragma unroll 4
@@ -287,11 +293,10 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(AttnArgs a) {
 template <int HD, int G>
 hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
     const int nchunks = attn_max_chunks(a.heads, a.kv_heads, a.context);
-    dim3 grid(nchunks, a.kv_heads);
-    attn_scores_kernel<HD, G><<<grid, WG, 0, s>>>(a);
+    attn_scores_kernel<HD, G><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_pv_kernel<HD, G><<<grid, WG, 0, s>>>(a);
+    attn_pv_kernel<HD, G><<<dim3((a.context + CHP - 1) / CHP, a.kv_heads), WG, 0, s>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     attn_combine_kernel<HD><<<a.heads, (1024 / HD) * HD, 0, s>>>(a);

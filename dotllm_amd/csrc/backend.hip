@@ -566,6 +566,8 @@ struct llmdot_hip_model {
     std::vector<void*> owned;          // device allocations owned by the model
     // activations
     float *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    // h packed for its next RmsNorm consumer: xn = w * h, xssq[i] = sum of h^2 over h[8i .. 8i+7]
+    float *xn = nullptr, *xssq = nullptr;
     // KV cache [layer][kv_head][context][head_dim]
     uint8_t *kcache = nullptr, *vcache = nullptr;
     size_t kv_layer_bytes = 0;
@@ -643,7 +645,7 @@ hipError_t launch_gate_up(llmdot_hip_model* m, int l) {
     const LayerW& w = m->L[l];
     GemvArgs ga{};
     ga.nseg = 1; ga.seg[0] = {w.gate->dev, w.up->dev, m->act, m->d.ffn, 0};
-    ga.cols = m->d.hidden; ga.x = m->h; ga.norm_w = w.ffn_norm_f; ga.norm = 1;
+    ga.cols = m->d.hidden; ga.x = m->xn; ga.ssq = m->xssq; ga.norm = 1;
     return step_gemv(m, w.gate->type, EPI_SWIGLU, ga);
 }
 
@@ -652,7 +654,8 @@ int enqueue_step(llmdot_hip_model* m) {
     const auto& d = m->d;
     hipStream_t s = m->ctx->stream;
     const int qdim = d.heads * d.head_dim, kvdim = d.kv_heads * d.head_dim;
-    HIPCHK(launch_embed(m->embd->dev, m->embd->type, d.hidden, m_token(m), m->h, s));
+    HIPCHK(launch_embed(m->embd->dev, m->embd->type, d.hidden, m_token(m), m->h, m->L[0].attn_norm_f, m->xn,
+                        m->xssq, s));
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
         // Q, K, V projections over RmsNorm(h) (IE:185-186, IE:333-353) in one launch when the
@@ -669,7 +672,7 @@ int enqueue_step(llmdot_hip_model* m) {
         for (int i = 0; i < 3; i++) {
             if (done[i]) continue;
             GemvArgs ga{};
-            ga.cols = d.hidden; ga.x = m->h; ga.norm_w = w.attn_norm_f; ga.norm = 1;
+            ga.cols = d.hidden; ga.x = m->xn; ga.ssq = m->xssq; ga.norm = 1;
             const uint32_t lt = mixed_ok && any_q4k ? (uint32_t)GGML_Q4_K : mats[i]->type;
             for (int j = i; j < 3; j++)
                 if (!done[j] && (mats[j]->type == mats[i]->type || (mixed_ok && any_q4k))) {
@@ -688,24 +691,27 @@ int enqueue_step(llmdot_hip_model* m) {
         aa.heads = d.heads; aa.kv_heads = d.kv_heads; aa.head_dim = d.head_dim; aa.rope_half = m->rope_half;
         aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
         HIPCHK(launch_attention(aa, s));
-        {   // O projection + residual (IE:444-449, IE:189)
+        {   // O projection + residual (IE:444-449, IE:189), h packed for the FFN RmsNorm
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.o->dev, nullptr, m->h, d.hidden, 0};
             ga.cols = qdim; ga.x = m->attn;
+            ga.pack_w = w.ffn_norm_f; ga.pack_out = m->xn; ga.pack_ssq = m->xssq;
             HIPCHK(step_gemv(m, w.o->type, EPI_ADD, ga));
         }
         HIPCHK(launch_gate_up(m, l));
-        {   // down projection + residual (IE:475, IE:195)
+        {   // down projection + residual (IE:475, IE:195), h packed for the next RmsNorm
             GemvArgs ga{};
             ga.nseg = 1; ga.seg[0] = {w.down->dev, nullptr, m->h, d.hidden, 0};
             ga.cols = d.ffn; ga.x = m->act;
+            ga.pack_w = l + 1 < d.layers ? m->L[l + 1].attn_norm_f : m->out_norm_f;
+            ga.pack_out = m->xn; ga.pack_ssq = m->xssq;
             HIPCHK(step_gemv(m, w.down->type, EPI_ADD, ga));
         }
     }
     {   // final RmsNorm + LM head + greedy ArgMax (IE:575-602, Sampler.cs:26-27)
         GemvArgs ga{};
         ga.nseg = 1; ga.seg[0] = {m->out->dev, nullptr, m->logits, d.vocab, 0};
-        ga.cols = d.hidden; ga.x = m->h; ga.norm_w = m->out_norm_f; ga.norm = 1;
+        ga.cols = d.hidden; ga.x = m->xn; ga.ssq = m->xssq; ga.norm = 1;
         ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx; ga.am.cap = m->am_cap;
         ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
         ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
@@ -850,6 +856,8 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     if ((rc = A(sizeof(float) * kvdim, &p))) return bail(rc); m->v = (float*)p;
     if ((rc = A(sizeof(float) * qdim, &p))) return bail(rc); m->attn = (float*)p;
     if ((rc = A(sizeof(float) * d.ffn, &p))) return bail(rc); m->act = (float*)p;
+    if ((rc = A(sizeof(float) * d.hidden, &p))) return bail(rc); m->xn = (float*)p;
+    if ((rc = A(sizeof(float) * (d.hidden / 8), &p))) return bail(rc); m->xssq = (float*)p;
     if ((rc = A(sizeof(float) * d.vocab, &p))) return bail(rc); m->logits = (float*)p;
     const size_t elt = d.kv_fp16 ? 2 : 4;
     m->kv_layer_bytes = (size_t)d.kv_heads * d.context * d.head_dim * elt;

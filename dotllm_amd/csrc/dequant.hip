@@ -82,12 +82,44 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ src, float* __restric
     }
 }
 
-__global__ void embed_kernel(const uint8_t* __restrict__ table, uint32_t type, int hidden, int64_t row_bytes,
-                             const int32_t* __restrict__ token, float* __restrict__ out) {
-    int tok = *token;
+// One thread per element; with w set, also the packed input of the first
+// RmsNorm consumer (as pack_norm_kernel).
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ table, uint32_t type, int hidden,
+                                                    int64_t row_bytes, const int32_t* __restrict__ token,
+                                                    float* __restrict__ out, const float* __restrict__ w,
+                                                    float* __restrict__ packed, float* __restrict__ ssq) {
+    const int tok = *token;
     const uint8_t* row = table + (int64_t)tok * row_bytes;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
-        out[i] = deq_elem(type, row, i);
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const float h = i < hidden ? deq_elem(type, row, i) : 0.f;
+    if (i < hidden) out[i] = h;
+    if (w) {   // uniform
+        if (i < hidden) packed[i] = w[i] * h;
+        float q = h * h;
+        q += __shfl_xor(q, 1, 64);
+        q += __shfl_xor(q, 2, 64);
+        q += __shfl_xor(q, 4, 64);
+        if ((i & 7) == 0 && i < hidden) ssq[i >> 3] = q;
+    }
+}
+
+// One thread per element; lanes 8k..8k+7 reduce their squares for ssq[k].
+__global__ __launch_bounds__(256) void pack_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                                        float* __restrict__ packed, float* __restrict__ ssq) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const float h = i < n ? x[i] : 0.f;
+    if (i < n) packed[i] = w[i] * h;   // RmsNorm's vector lanes compute (w * x) * inv
+    float q = h * h;
+    q += __shfl_xor(q, 1, 64);
+    q += __shfl_xor(q, 2, 64);
+    q += __shfl_xor(q, 4, 64);
+    if ((i & 7) == 0 && i < n) ssq[i >> 3] = q;
+}
+
+hipError_t launch_pack_norm(const float* x, const float* w, int n, float* packed, float* ssq, hipStream_t s) {
+    if (n <= 0 || n % 8) return hipErrorInvalidValue;
+    pack_norm_kernel<<<(n + 255) / 256, 256, 0, s>>>(x, w, n, packed, ssq);
+    return hipGetLastError();
 }
 
 hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num_rows, int row_elems,
@@ -102,10 +134,11 @@ hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num
 }
 
 hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const int32_t* token_dev,
-                        float* out, hipStream_t s) {
+                        float* out, const float* w, float* packed, float* ssq, hipStream_t s) {
+    if (w && (hidden % 8 || !packed || !ssq)) return hipErrorInvalidValue;
     int64_t rb = byte_count(type, hidden);
     int grid = (hidden + 255) / 256;
-    embed_kernel<<<grid, 256, 0, s>>>(table, type, hidden, rb, token_dev, out);
+    embed_kernel<<<grid, 256, 0, s>>>(table, type, hidden, rb, token_dev, out, w, packed, ssq);
     return hipGetLastError();
 }
 

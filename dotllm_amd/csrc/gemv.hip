@@ -163,7 +163,7 @@ struct __attribute__((aligned(4))) u32x2 { uint32_t x, y; };
 
 struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
     // 4 rows per batch keep the kernel near 100 VGPRs (4 wavefronts per SIMD)
-    static constexpr int RB = 4, NS = 1, PRE = 2;
+    static constexpr int RB = 4, NS = 1, PRE = 2, DEPTH = 2;
     // dd: d | dmin << 16; f: the two header words holding sub-block g's
     // 12-bit (sc, m) field, which starts at bit 32 + 12 g of the block (the
     // 6-bit stream begins at byte 4, LSB first), i.e. at bit (12 g) mod 32 of
@@ -197,7 +197,7 @@ struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
 };
 
 struct TQ5K {   // reference Q5_K, 176 B / 256: unit = sub-block g
-    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 2;
+    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
     struct Raw { u32x4 h, q; uint32_t qh; };
     __device__ static int xoff(int u, int) { return u * 32; }
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
@@ -234,7 +234,7 @@ struct TQ5K {   // reference Q5_K, 176 B / 256: unit = sub-block g
 // n = 128 ((u >> 2) & 1), l-range l0 = 8 (u & 3) .. l0 + 7, four runs t = 0..3 of 8
 // elements at n + l0 + 32 t (the q1..q4 groups of the reference loop).
 struct TQ6K {
-    static constexpr int RB = 4, NS = 4, RUN = 8, PRE = 1;   // PRE: batches issued before the activations' arithmetic
+    static constexpr int RB = 4, NS = 4, RUN = 8, PRE = 1, DEPTH = 2;   // PRE: batches issued before the activations' arithmetic
     // A, B: ql bytes of runs 0/2 and 1/3; C: qh bytes; S: scales.  A, B, C sit
     // at multiples of 8 from the 2-aligned block start and share one shift.
     struct Raw { uint32_t A[3], B[3], C[3], S[3], d, sh; };
@@ -286,7 +286,7 @@ struct TQ6K {
 };
 
 struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block
-    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2;
+    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
     struct Raw { RawW<8> Q; uint32_t d; };
     __device__ static int xoff(int u, int) { return u * 32; }
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
@@ -310,7 +310,7 @@ struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block
 };
 
 struct TQ4_0 {   // Q4_0, 18 B / 32: unit = block; low nibbles -> j, high -> j + 16
-    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 1;
+    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 1, DEPTH = 2;
     struct Raw { RawW<4> Q; uint32_t d; };
     __device__ static int xoff(int u, int) { return u * 32; }
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
@@ -335,7 +335,7 @@ struct TQ4_0 {   // Q4_0, 18 B / 32: unit = block; low nibbles -> j, high -> j +
 };
 
 struct TF32 {
-    static constexpr int RB = 2, NS = 1, RUN = 32, PRE = 2;
+    static constexpr int RB = 2, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
     struct Raw { float4 f[8]; };
     __device__ static int xoff(int u, int) { return u * 32; }
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
@@ -356,7 +356,7 @@ struct TF32 {
 };
 
 struct TF16 {
-    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2;
+    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
     struct Raw { u32x4 q[4]; };
     __device__ static int xoff(int u, int) { return u * 32; }
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
@@ -404,45 +404,30 @@ __device__ __forceinline__ void row_sums16(float* v) {
     for (int i = 0; i < N; i++) v[i] += dpp_f32<0x121>(v[i]);   // row_ror:1
 }
 
-// Raw activations of a lane: the unit's 32 values of x (and of the norm
-// weights), in the unit's element order.
-template <bool NORM>
+// Raw activations of a lane: the unit's 32 values of x, in the unit's element
+// order.  For an RmsNorm consumer x is already w * h (packed by the producer).
 struct XRaw {
     float4 h[8];
-    float4 w[NORM ? 8 : 1];
 };
 
-template <int RUN, bool NORM, typename XOff>
-__device__ __forceinline__ void issue_x(const GemvArgs& a, XOff&& xoff, XRaw<NORM>& r) {
+template <int RUN, typename XOff>
+__device__ __forceinline__ void issue_x(const GemvArgs& a, XOff&& xoff, XRaw& r) {
 #pragma unroll
     for (int run = 0; run < 32 / RUN; run++) {
         const int off = xoff(run);
 #pragma unroll
-        for (int q = 0; q < RUN / 4; q++) {
-            r.h[run * (RUN / 4) + q] = *reinterpret_cast<const float4*>(a.x + off + 4 * q);
-            if (NORM) r.w[run * (RUN / 4) + q] = *reinterpret_cast<const float4*>(a.norm_w + off + 4 * q);
-        }
+        for (int q = 0; q < RUN / 4; q++) r.h[run * (RUN / 4) + q] = *reinterpret_cast<const float4*>(a.x + off + 4 * q);
     }
 }
 
-// v = w * h (VectorMath.RmsNorm's vector lanes compute (w * x) * inv; the
-// 1/rms factor is applied to the row sums), 0 past the row end; returns sum(h^2).
-template <bool NORM>
-__device__ __forceinline__ float finish_x(const XRaw<NORM>& r, bool has, float* v) {
-    float hsq = 0.f;
+// The lane's 32 values, 0 past the row end.
+__device__ __forceinline__ void finish_x(const XRaw& r, bool has, float* v) {
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-        float4 e = r.h[q];
-        e.x = has ? e.x : 0.f; e.y = has ? e.y : 0.f; e.z = has ? e.z : 0.f; e.w = has ? e.w : 0.f;
-        hsq += e.x * e.x + e.y * e.y + e.z * e.z + e.w * e.w;
-        if (NORM) {
-#pragma clang fp contract(off)
-            const float4 g = r.w[q];
-            e.x = g.x * e.x; e.y = g.y * e.y; e.z = g.z * e.z; e.w = g.w * e.w;
-        }
-        v[4 * q] = e.x; v[4 * q + 1] = e.y; v[4 * q + 2] = e.z; v[4 * q + 3] = e.w;
+        const float4 e = r.h[q];
+        v[4 * q] = has ? e.x : 0.f; v[4 * q + 1] = has ? e.y : 0.f;
+        v[4 * q + 2] = has ? e.z : 0.f; v[4 * q + 3] = has ? e.w : 0.f;
     }
-    return hsq;
 }
 
 template <int NS>
@@ -457,35 +442,35 @@ __device__ __forceinline__ void run_sums(XF<NS>& x) {
     }
 }
 
-// One workgroup's rows.  Issue order: the activations, then the first two
-// batches of weights (one for types with large raw blocks); a scheduling barrier keeps the activation arithmetic
-// (quantisation) after those issues, so it overlaps the weight loads.  Each
-// computed batch frees its registers for the batch two ahead.  Every lane
+// One workgroup's rows.  Issue order: the activations, then the first PRE
+// batches of weights; a scheduling barrier keeps the activation arithmetic
+// (quantisation) after those issues, so it overlaps the weight loads.  DEPTH
+// batches are in flight: each computed batch frees its registers for the
+// batch DEPTH ahead.  Every lane
 // loads (lanes past the row end read unit 0 and contribute 0): no branches,
 // so no load is serialised behind another.  Row i's per-quarter-wavefront
-// sums go to red_w[i][0..3]; returns the lane's sum(h^2).
-template <typename TT, int NB, bool NORM, typename RowPtr>
-__device__ __forceinline__ float gemv_rows(const GemvArgs& a, int uu, bool has, RowPtr&& row_ptr, float (*red_w)[4]) {
+// sums go to red_w[i][0..3].
+template <typename TT, int NB, typename RowPtr>
+__device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, RowPtr&& row_ptr, float (*red_w)[4]) {
     constexpr int RB = TT::RB;
     constexpr bool INT = std::is_same<TT, TQ4K>::value;
     const int lane = threadIdx.x & 63;
-    XRaw<NORM> xr;
-    if constexpr (INT) issue_x<32, NORM>(a, [&](int) { return uu * 32; }, xr);
-    else issue_x<TT::RUN, NORM>(a, [&](int run) { return TT::xoff(uu, run); }, xr);
-    typename TT::Raw buf[2][RB];
+    XRaw xr;
+    if constexpr (INT) issue_x<32>(a, [&](int) { return uu * 32; }, xr);
+    else issue_x<TT::RUN>(a, [&](int run) { return TT::xoff(uu, run); }, xr);
+    constexpr int D = TT::DEPTH;     // batches in flight
+    typename TT::Raw buf[D][RB];
 #pragma unroll
-    for (int i = 0; i < RB; i++) TT::load(buf[0][i], row_ptr(i), uu);
-    if (NB > 1 && TT::PRE > 1) {
+    for (int k = 0; k < TT::PRE && k < NB && k < D; k++)
 #pragma unroll
-        for (int i = 0; i < RB; i++) TT::load(buf[1][i], row_ptr(RB + i), uu);
-    }
+        for (int i = 0; i < RB; i++) TT::load(buf[k][i], row_ptr(k * RB + i), uu);
     __builtin_amdgcn_sched_barrier(0);
     float v[32];
-    const float hsq = finish_x<NORM>(xr, has, v);
-    if (NB > 1 && TT::PRE == 1) {
+    finish_x(xr, has, v);
 #pragma unroll
-        for (int i = 0; i < RB; i++) TT::load(buf[1][i], row_ptr(RB + i), uu);
-    }
+    for (int k = TT::PRE; k < NB && k < D; k++)
+#pragma unroll
+        for (int i = 0; i < RB; i++) TT::load(buf[k][i], row_ptr(k * RB + i), uu);
     typename std::conditional<INT, XQ, XF<INT ? 1 : TT::NS>>::type x;
     if constexpr (INT) {
         quantize32(v, x);
@@ -499,7 +484,7 @@ __device__ __forceinline__ float gemv_rows(const GemvArgs& a, int uu, bool has, 
         float dv[RB];
 #pragma unroll
         for (int i = 0; i < RB; i++) {
-            const float d = TT::dot(buf[b & 1][i], uu, x);
+            const float d = TT::dot(buf[b % D][i], uu, x);
             dv[i] = has ? d : 0.f;
         }
         row_sums16<RB>(dv);   // all rows level by level: no DPP hazard stalls
@@ -507,12 +492,11 @@ __device__ __forceinline__ float gemv_rows(const GemvArgs& a, int uu, bool has, 
 #pragma unroll
             for (int i = 0; i < RB; i++) red_w[b * RB + i][lane >> 4] = dv[i];
         }
-        if (b + 2 < NB) {
+        if (b + D < NB) {
 #pragma unroll
-            for (int i = 0; i < RB; i++) TT::load(buf[b & 1][i], row_ptr((b + 2) * RB + i), uu);
+            for (int i = 0; i < RB; i++) TT::load(buf[b % D][i], row_ptr((b + D) * RB + i), uu);
         }
     }
-    return hsq;
 }
 
 // ---- the kernel -------------------------------------------------------------------
@@ -561,10 +545,21 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         return base + (int64_t)(r < seg.rows ? r : 0) * rbytes;
     };
 
-    float hsq;
-    if (T2 != T && second) hsq = gemv_rows<TT2, NB, NORM>(a, uu, has, row_ptr, red[wave]);
-    else hsq = gemv_rows<TT, NB, NORM>(a, uu, has, row_ptr, red[wave]);
+    // RmsNorm: the producer's sums of h^2 over 8-element groups, K/8 <= 4 per
+    // thread (threads >= K/32), issued first and summed after the rows
+    float sq[4];
     if (NORM) {
+        const int nq = K >> 3;
+#pragma unroll
+        for (int k = 0; k < 4; k++) sq[k] = a.ssq[min((int)threadIdx.x + k * (int)blockDim.x, nq - 1)];
+    }
+    if (T2 != T && second) gemv_rows<TT2, NB>(a, uu, has, row_ptr, red[wave]);
+    else gemv_rows<TT, NB>(a, uu, has, row_ptr, red[wave]);
+    if (NORM) {
+        const int nq = K >> 3;
+        float hsq = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) hsq += (int)threadIdx.x + k * (int)blockDim.x < nq ? sq[k] : 0.f;
         const float w = wave_sum(hsq);
         if (lane == 0) ssq[wave] = w;
     }
@@ -591,7 +586,22 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     if (EPI == EPI_STORE) {
         if (valid) seg.out[row] = total(b * RB + k);
     } else if (EPI == EPI_ADD) {
-        if (valid) seg.out[row] = seg.out[row] + total(b * RB + k);
+        float hn = 0.f;
+        if (valid) {
+            hn = seg.out[row] + total(b * RB + k);   // residual: a[i] + b[i]
+            seg.out[row] = hn;
+        }
+        if (a.pack_out) {   // the updated vector packed for its RmsNorm consumer (rows come in 8s)
+            if (valid) {
+#pragma clang fp contract(off)
+                a.pack_out[row] = a.pack_w[row] * hn;
+            }
+            float q = hn * hn;
+            q += __shfl_xor(q, 1, 64);
+            q += __shfl_xor(q, 2, 64);
+            q += __shfl_xor(q, 4, 64);
+            if (valid && (t & 7) == 0) a.pack_ssq[row >> 3] = q;
+        }
     } else if (EPI == EPI_SWIGLU) {
         if (valid) {
 #pragma clang fp contract(off)
@@ -706,6 +716,8 @@ int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
     // the most rows per workgroup that still gives the target wavefront count
     int nb = 8;
     while (nb > 1 && ((rows_total + nb * opb - 1) / (nb * opb)) * nw < target_waves()) nb /= 2;
+    // the ADD epilogue packs rows in groups of 8
+    while (epi == EPI_ADD && nb < 8 && (nb * opb) % 8) nb *= 2;
     return nb;
 }
 
@@ -744,8 +756,10 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     if (epi == EPI_SWIGLU && (a.nseg != 1 || !a.seg[0].w2)) return hipErrorInvalidValue;
     if (epi == EPI_ARGMAX && (a.nseg != 1 || !a.am.cand_val || !a.am.cand_idx || !a.am.token_out))
         return hipErrorInvalidValue;
-    if (a.norm && !a.norm_w) return hipErrorInvalidValue;
+    if (a.norm && (!a.ssq || a.cols % 8)) return hipErrorInvalidValue;
     if (epi == EPI_ADD && a.norm) return hipErrorInvalidValue;
+    if (a.pack_out && (epi != EPI_ADD || !a.pack_w || !a.pack_ssq || a.nseg != 1 || a.seg[0].rows % 8))
+        return hipErrorInvalidValue;
     if ((epi == EPI_SWIGLU || epi == EPI_ARGMAX) && !a.norm) return hipErrorInvalidValue;
     int rows_total = 0;
     for (int i = 0; i < a.nseg; i++) {

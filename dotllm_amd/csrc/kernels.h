@@ -12,9 +12,13 @@ hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num
                           hipStream_t s);
 // Embedding row (InferenceEngine.GetEmbedding, IE:148-156): row *token_dev of
 // the [vocab][hidden] table, bit-exact, into out.  The token id is read on the
-// device so that a captured step can take it from the previous argmax.
+// device so that a captured step can take it from the previous argmax.  With
+// w non-null also packs out for its RmsNorm consumer (see launch_pack_norm).
 hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const int32_t* token_dev,
-                        float* out, hipStream_t s);
+                        float* out, const float* w, float* packed, float* ssq, hipStream_t s);
+// Packs x for an RmsNorm consumer: packed[i] = w[i] * x[i], ssq[i/8] = sum of x^2
+// over 8 consecutive elements (n a multiple of 8).
+hipError_t launch_pack_norm(const float* x, const float* w, int n, float* packed, float* ssq, hipStream_t s);
 
 // ---- gemv.hip ----
 enum GemvEpi : int { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
@@ -43,10 +47,15 @@ struct GemvArgs {
     GemvSeg seg[3];       // up to 3 matrices of the same type and width in one launch
     int nseg;
     int cols;             // reduction length K
-    const float* x;       // fp32 input (the unnormalised hidden state when norm != 0)
-    const float* norm_w;  // RmsNorm weights applied on the fly
-    int norm;             // apply RmsNorm to x
+    const float* x;       // fp32 input; with norm != 0 it is already w * h (RmsNorm weights applied)
+    const float* ssq;     // norm != 0: sums of h^2 over consecutive 8-element groups, K/8 of them
+    int norm;             // RmsNorm of the input: row sums are scaled by 1/sqrt(sum(h^2)/K + eps)
     float eps;
+    // EPI_ADD: also pack the updated vector for its RmsNorm consumer:
+    // pack_out[i] = pack_w[i] * out[i] and pack_ssq[i/8] = sum of out^2 over 8 rows
+    const float* pack_w;
+    float* pack_out;
+    float* pack_ssq;
     ArgmaxState am;       // EPI_ARGMAX
 };
 
