@@ -2,10 +2,12 @@
 
 One step = one greedy decode token (the whole LLaMA-like step: 32 layers +
 LM head + argmax) with weights and KV cache resident in HBM.  The prompt is
-processed first on the device (sequential steps, as the reference does), so
-the timed steps run at context position `--ctx`.  Prints one JSON line.
+processed first on the device (batched MFMA prefill: a `--prefill`-token
+prefill from position 0 is timed and reported with its MFMA utilisation, then
+the rest of the prompt), so the timed decode steps run at context position
+`--ctx`.  Prints one JSON line.
 
-  python bench.py [--steps K] [--warmup W] [--ctx T] [--config mistral7b]
+  python bench.py [--steps K] [--warmup W] [--ctx T] [--prefill P] [--config mistral7b]
 """
 from __future__ import annotations
 
@@ -57,6 +59,20 @@ def cpu_baseline(img, ctx: int, steps: int, threads: int) -> dict:
                       f"{os.cpu_count()} host cores"}
 
 
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+
+
+def prefill_flops(spec: dict, n: int) -> float:
+    """Algorithmic FLOPs of an n-token prompt: 2 x projection parameters x n,
+    causal attention 2 hd n^2 per head and layer (QK^T + PV over the lower
+    triangle), and the LM head once (the last token)."""
+    d, f, L = spec["hidden"], spec["ffn"], spec["layers"]
+    q, kv = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
+    params = L * (2 * d * q + 2 * d * kv + 3 * d * f)
+    attn = 2.0 * spec["head_dim"] * n * n * spec["heads"] * L
+    return 2.0 * params * n + attn + 2.0 * d * spec["vocab"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -69,6 +85,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
+    ap.add_argument("--prefill", type=int, default=2048,
+                    help="tokens of the timed prefill from position 0 (0: none)")
     ap.add_argument("--synthetic-kv", action="store_true",
                     help="fill the KV cache of the first --ctx positions with random values instead of "
                          "processing a --ctx-token prompt (same decode-step work; for short profiling runs)")
@@ -99,15 +117,30 @@ def main() -> int:
     eng = InferenceEngine(model, be, kv_fp16=True, context=total_ctx)
     log(f"uploaded weights + built step graph in {time.perf_counter() - t0:.1f}s on {info['name']} ({info['arch']})")
 
+    prompt = synth.prompt(spec["vocab"], max(args.ctx, args.prefill), seed=7)
+    pf = None
+    n_pf = min(args.prefill, args.ctx) if not args.synthetic_kv else args.prefill
+    if n_pf > 0:
+        eng.time_prefill(prompt[:min(256, n_pf)], 0)           # warm-up (kernel loads)
+        pf_ms = eng.time_prefill(prompt[:n_pf], 0)
+        fl = prefill_flops(spec, n_pf)
+        pf = {"tokens": n_pf, "ms": round(pf_ms, 3), "tok_s": round(n_pf / (pf_ms * 1e-3), 1),
+              "flops": fl, "tflops": round(fl / (pf_ms * 1e-3) / 1e12, 1), "peak_tflops": MFMA_PEAK_TFLOPS,
+              "mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+              "arith": "fp16 MFMA, activations as two fp16 planes (fp32-equivalent), fp32 accumulation"}
+        log(f"prefill {n_pf} tokens: {pf_ms:.2f} ms, {pf['tok_s']:.0f} tok/s, {pf['tflops']:.0f} TFLOP/s "
+            f"({100 * pf['mfma_util']:.1f}% of {MFMA_PEAK_TFLOPS:.0f})")
     if args.synthetic_kv:
         eng.kv_fill_random(args.ctx, seed=3)
         tok = 1
         log(f"filled {args.ctx} KV positions with random values")
     else:
-        prompt = synth.prompt(spec["vocab"], args.ctx, seed=7)
         t0 = time.perf_counter()
-        _, tok = eng.prefill(prompt, 0)
-        log(f"processed {args.ctx}-token prompt in {time.perf_counter() - t0:.1f}s")
+        # the timed prefill left positions 0 .. n_pf-1 in the cache; the rest of the
+        # prompt continues from there (its last token's argmax starts the decode)
+        start = n_pf if n_pf < args.ctx else args.ctx - 1
+        _, tok = eng.prefill(prompt[start:args.ctx], start)
+        log(f"processed the rest of the {args.ctx}-token prompt in {time.perf_counter() - t0:.1f}s")
     pos = args.ctx
 
     if args.warmup > 0:
@@ -155,6 +188,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.config),
                      "bytes_per_launch": per_launch_bytes, "us_per_launch": round(per_launch_ms * 1e3, 2),
                      "stream_probe_gbps": {k: round(v, 1) for k, v in stream.items()}},
+        "prefill": pf,
         "cpu_baseline": None,
     }
     eng.dispose()

@@ -113,6 +113,7 @@ SIGNATURES = {
     "llmdot_hip_generate": [_P, _PI32, _I32, _I32, _I32, _PI32, _PI32, _P],
     "llmdot_hip_kv_read": [_P, _I32, _I32, _P, _P],
     "llmdot_hip_model_time_decode": [_P, _I32, _I32, _I32, _I32, C.POINTER(StepTiming)],
+    "llmdot_hip_model_time_prefill": [_P, _PI32, _I32, _I32, C.POINTER(C.c_float)],
     "llmdot_hip_model_step_bytes": [_P, _I32, C.POINTER(C.c_double)],
     "llmdot_hip_model_kv_fill_random": [_P, _I32, _U64],
     "llmdot_hip_quantize": [_U32, _P, _I64, _I64, _P],

@@ -34,16 +34,6 @@ constexpr int WG = 256;
 constexpr int CH = 64;    // positions per score chunk (scores kernel)
 constexpr int CHP = 64;   // positions per pv chunk (pv kernel; its partials feed the combine)
 
-__device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int fp16) {
-    if (fp16) {
-        const _Float16 h = (_Float16)v;                 // round to nearest even
-        reinterpret_cast<_Float16*>(cache)[idx] = h;
-        return (float)h;
-    }
-    reinterpret_cast<float*>(cache)[idx] = v;
-    return v;
-}
-
 // N consecutive cache elements starting at element idx (16-byte aligned) as floats.
 template <int N>
 __device__ __forceinline__ void load_kv_row(const void* cache, int64_t idx, int fp16, float* out) {
@@ -81,14 +71,6 @@ __device__ __forceinline__ void load_kv_row(const void* cache, int64_t idx, int 
             for (int i = 0; i < N; i++) out[i] = p[i];
         }
     }
-}
-
-// NeoX rotation of element d of a head (pairs (i, i + half), dims >= 2*half untouched).
-__device__ __forceinline__ float rope_elem(const float* x, int d, int half, const float* cs, const float* sn) {
-#pragma clang fp contract(off)
-    if (d < half) return x[d] * cs[d] - x[d + half] * sn[d];
-    if (d < 2 * half) return x[d - half] * sn[d - half] + x[d] * cs[d - half];
-    return x[d];
 }
 
 template <int HD, int G>

@@ -86,6 +86,7 @@ struct llmdot_hip_ctx {
     hipStream_t stream = nullptr;
     std::unordered_map<std::string, Weight> weights;
     DevBuf scratch[6];
+    DevBuf planes[5];            // batched MatMul: activation planes (xh, xl, sh, sl, xinv)
     int32_t* am_ints = nullptr;  // [0] token_out
     float* am_val = nullptr;
     int32_t* am_idx = nullptr;
@@ -179,6 +180,7 @@ extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->weights) (void)hipFree(kv.second.dev);
     for (auto& b : ctx->scratch) b.release();
+    for (auto& b : ctx->planes) b.release();
     if (ctx->am_ints) (void)hipFree(ctx->am_ints);
     if (ctx->am_val) (void)hipFree(ctx->am_val);
     if (ctx->am_idx) (void)hipFree(ctx->am_idx);
@@ -249,6 +251,20 @@ int stage_in(llmdot_hip_ctx* ctx, int slot, const T* host, size_t n, T** dev) {
     return 0;
 }
 
+// Activation-plane buffers for M rows of K elements.
+int ctx_planes(llmdot_hip_ctx* ctx, int M, int K, PfPlanes* pl) {
+    const size_t n = (size_t)M * K;
+    HIPCHK(ctx->planes[0].ensure(2 * n));
+    HIPCHK(ctx->planes[1].ensure(2 * n));
+    HIPCHK(ctx->planes[2].ensure(2 * (n / 32 + 8)));
+    HIPCHK(ctx->planes[3].ensure(2 * (n / 32 + 8)));
+    HIPCHK(ctx->planes[4].ensure(4 * (size_t)M));
+    pl->xh = (_Float16*)ctx->planes[0].p; pl->xl = (_Float16*)ctx->planes[1].p;
+    pl->sh = (_Float16*)ctx->planes[2].p; pl->sl = (_Float16*)ctx->planes[3].p;
+    pl->xinv = (float*)ctx->planes[4].p;
+    return 0;
+}
+
 int copy_out(llmdot_hip_ctx* ctx, void* host, const void* dev, size_t nbytes) {
     HIPCHK(hipMemcpyAsync(host, dev, nbytes, hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
@@ -292,6 +308,14 @@ int matmul_common(llmdot_hip_ctx* ctx, const float* a, const void* b, float* res
     float *da, *dy;
     if (int rc = stage_in(ctx, 0, a, (size_t)(a_rows * a_cols), &da)) return rc;
     if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)result_len, &dy)) return rc;
+    if (a_rows > 1 && a_rows <= INT32_MAX && prefill_gemm_supported(type, a_cols)) {
+        // several activation rows (TO:92-111): one MFMA GEMM over all of them
+        PfPlanes pl;
+        if (int rc = ctx_planes(ctx, (int)a_rows, a_cols, &pl)) return rc;
+        HIPCHK(launch_prefill_planes(da, (int)a_rows, a_cols, nullptr, 0.f, pl, ctx->stream));
+        HIPCHK(launch_prefill_gemm(type, 0, pl, w->dev, nullptr, (int)a_rows, b_cols, a_cols, dy, b_cols, ctx->stream));
+        return copy_out(ctx, result, dy, sizeof(float) * (size_t)result_len);
+    }
     for (int64_t r = 0; r < a_rows; r++)
         if (int rc = ctx_gemv(ctx, type, w->dev, da + r * a_cols, dy + r * b_cols, b_cols, a_cols)) return rc;
     return copy_out(ctx, result, dy, sizeof(float) * (size_t)result_len);
@@ -583,6 +607,13 @@ struct llmdot_hip_model {
     int am_cap = 0;
     hipGraphExec_t graph = nullptr;
     bool use_graph = true;
+    // batched prefill (allocated on first use): chunk of pf_cap tokens
+    bool pf_eligible = false;
+    int pf_cap = 0;
+    float *pf_h = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_qr = nullptr, *pf_attn = nullptr,
+          *pf_act = nullptr, *pf_scores = nullptr, *pf_rowmax = nullptr;
+    PfPlanes pf_planes{};
+    int32_t* pf_tokens = nullptr;
 };
 
 namespace {
@@ -649,6 +680,20 @@ hipError_t launch_gate_up(llmdot_hip_model* m, int l) {
     return step_gemv(m, w.gate->type, EPI_SWIGLU, ga);
 }
 
+// Final RmsNorm + LM head + greedy ArgMax (IE:575-602, Sampler.cs:26-27) over the
+// packed xn / xssq; the argmax pass advances the device position and step.
+int enqueue_head(llmdot_hip_model* m) {
+    const auto& d = m->d;
+    GemvArgs ga{};
+    ga.nseg = 1; ga.seg[0] = {m->out->dev, nullptr, m->logits, d.vocab, 0};
+    ga.cols = d.hidden; ga.x = m->xn; ga.ssq = m->xssq; ga.norm = 1;
+    ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx; ga.am.cap = m->am_cap;
+    ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
+    ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
+    HIPCHK(step_gemv(m, m->out->type, EPI_ARGMAX, ga));
+    return 0;
+}
+
 // Enqueues one decode step on the model stream (token and position on the device).
 int enqueue_step(llmdot_hip_model* m) {
     const auto& d = m->d;
@@ -708,16 +753,7 @@ int enqueue_step(llmdot_hip_model* m) {
             HIPCHK(step_gemv(m, w.down->type, EPI_ADD, ga));
         }
     }
-    {   // final RmsNorm + LM head + greedy ArgMax (IE:575-602, Sampler.cs:26-27)
-        GemvArgs ga{};
-        ga.nseg = 1; ga.seg[0] = {m->out->dev, nullptr, m->logits, d.vocab, 0};
-        ga.cols = d.hidden; ga.x = m->xn; ga.ssq = m->xssq; ga.norm = 1;
-        ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx; ga.am.cap = m->am_cap;
-        ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
-        ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
-        HIPCHK(step_gemv(m, m->out->type, EPI_ARGMAX, ga));
-    }
-    return 0;
+    return enqueue_head(m);
 }
 
 int build_graph(llmdot_hip_model* m) {
@@ -747,6 +783,122 @@ int run_step(llmdot_hip_model* m) {
 int set_int(llmdot_hip_model* m, int32_t* dst, int32_t v) {
     HIPCHK(launch_set_scalar(dst, v, m->ctx->stream));
     return 0;
+}
+
+// ---- batched prefill ------------------------------------------------------
+
+// Whether every projection of every layer has a batched (MFMA) kernel.
+bool prefill_check(const llmdot_hip_model* m) {
+    const auto& d = m->d;
+    const int qdim = d.heads * d.head_dim;
+    for (const auto& w : m->L) {
+        const Weight* in_h[5] = {w.q, w.k, w.v, w.gate, w.up};
+        for (auto* x : in_h)
+            if (!prefill_gemm_supported(x->type, d.hidden)) return false;
+        if (!prefill_gemm_supported(w.o->type, qdim) || !prefill_gemm_supported(w.down->type, d.ffn)) return false;
+    }
+    return true;
+}
+
+int prefill_chunk_cap(const llmdot_hip_model* m) {
+    int cap = 2048;
+    if (const char* v = getenv("LLMDOT_HIP_PREFILL_CHUNK")) {
+        const int c = atoi(v);
+        if (c >= 16) cap = c;
+    }
+    // score scratch [heads][cap][context] fp32 within 2 GiB
+    const double per_tok = 4.0 * m->d.heads * (double)m->d.context;
+    while (cap > 64 && per_tok * cap > 2147483648.0) cap /= 2;
+    return cap;
+}
+
+int ensure_prefill_ws(llmdot_hip_model* m) {
+    if (m->pf_cap) return 0;
+    const auto& d = m->d;
+    const int cap = prefill_chunk_cap(m);
+    const size_t qdim = (size_t)d.heads * d.head_dim, kvdim = (size_t)d.kv_heads * d.head_dim;
+    const size_t kmax = std::max({(size_t)d.hidden, qdim, (size_t)d.ffn});
+    void* p;
+    auto A = [&](size_t n, void** dst) { return dalloc(m, n, dst); };
+    int rc;
+    if ((rc = A(4 * cap * (size_t)d.hidden, &p))) return rc; m->pf_h = (float*)p;
+    if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_q = (float*)p;
+    if ((rc = A(4 * cap * kvdim, &p))) return rc; m->pf_k = (float*)p;
+    if ((rc = A(4 * cap * kvdim, &p))) return rc; m->pf_v = (float*)p;
+    if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_qr = (float*)p;
+    if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_attn = (float*)p;
+    if ((rc = A(4 * cap * (size_t)d.ffn, &p))) return rc; m->pf_act = (float*)p;
+    if ((rc = A(4 * (size_t)d.heads * cap * (size_t)d.context, &p))) return rc; m->pf_scores = (float*)p;
+    if ((rc = A(4 * (size_t)d.heads * cap, &p))) return rc; m->pf_rowmax = (float*)p;
+    if ((rc = A(2 * cap * kmax, &p))) return rc; m->pf_planes.xh = (_Float16*)p;
+    if ((rc = A(2 * cap * kmax, &p))) return rc; m->pf_planes.xl = (_Float16*)p;
+    if ((rc = A(2 * cap * (kmax / 32), &p))) return rc; m->pf_planes.sh = (_Float16*)p;
+    if ((rc = A(2 * cap * (kmax / 32), &p))) return rc; m->pf_planes.sl = (_Float16*)p;
+    if ((rc = A(4 * (size_t)cap, &p))) return rc; m->pf_planes.xinv = (float*)p;
+    if ((rc = A(4 * (size_t)cap, &p))) return rc; m->pf_tokens = (int32_t*)p;
+    m->pf_cap = cap;
+    return 0;
+}
+
+// One chunk of T prompt tokens at positions pos0 .. pos0+T-1 (tokens already
+// in pf_tokens): every layer as batched GEMMs, RoPE + KV write and causal
+// attention; leaves the chunk's hidden states in pf_h.
+int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
+    const auto& d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int qdim = d.heads * d.head_dim, kvdim = d.kv_heads * d.head_dim;
+    const PfPlanes& pl = m->pf_planes;
+    HIPCHK(launch_embed_rows(m->embd->dev, m->embd->type, d.hidden, m->pf_tokens, T, m->pf_h, s));
+    for (int l = 0; l < d.layers; l++) {
+        const LayerW& w = m->L[l];
+        HIPCHK(launch_prefill_planes(m->pf_h, T, d.hidden, w.attn_norm_f, d.eps, pl, s));
+        HIPCHK(launch_prefill_gemm(w.q->type, 0, pl, w.q->dev, nullptr, T, qdim, d.hidden, m->pf_q, qdim, s));
+        HIPCHK(launch_prefill_gemm(w.k->type, 0, pl, w.k->dev, nullptr, T, kvdim, d.hidden, m->pf_k, kvdim, s));
+        HIPCHK(launch_prefill_gemm(w.v->type, 0, pl, w.v->dev, nullptr, T, kvdim, d.hidden, m->pf_v, kvdim, s));
+        PfAttnArgs aa{};
+        aa.q = m->pf_q; aa.k = m->pf_k; aa.v = m->pf_v; aa.qr = m->pf_qr;
+        aa.kcache = m->kcache + (size_t)l * m->kv_layer_bytes;
+        aa.vcache = m->vcache + (size_t)l * m->kv_layer_bytes;
+        aa.cos_tab = m->cos_tab; aa.sin_tab = m->sin_tab;
+        aa.scores = m->pf_scores; aa.rowmax = m->pf_rowmax; aa.out = m->pf_attn;
+        aa.T = T; aa.pos0 = pos0; aa.ld_scores = d.context;
+        aa.heads = d.heads; aa.kv_heads = d.kv_heads; aa.head_dim = d.head_dim; aa.rope_half = m->rope_half;
+        aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
+        HIPCHK(launch_prefill_rope_kv(aa, s));
+        HIPCHK(launch_prefill_attention(aa, s));
+        HIPCHK(launch_prefill_planes(m->pf_attn, T, qdim, nullptr, 0.f, pl, s));
+        HIPCHK(launch_prefill_gemm(w.o->type, 1, pl, w.o->dev, nullptr, T, d.hidden, qdim, m->pf_h, d.hidden, s));
+        HIPCHK(launch_prefill_planes(m->pf_h, T, d.hidden, w.ffn_norm_f, d.eps, pl, s));
+        HIPCHK(launch_prefill_gemm(w.gate->type, 2, pl, w.gate->dev, w.up->dev, T, d.ffn, d.hidden, m->pf_act, d.ffn, s));
+        HIPCHK(launch_prefill_planes(m->pf_act, T, d.ffn, nullptr, 0.f, pl, s));
+        HIPCHK(launch_prefill_gemm(w.down->type, 1, pl, w.down->dev, nullptr, T, d.hidden, d.ffn, m->pf_h, d.hidden, s));
+    }
+    return 0;
+}
+
+// Batched prompt processing of n tokens from pos0 (the sequential loop of
+// IE:84-88 in chunks), then the LM head and argmax of the last token.  The
+// device position ends at pos0 + n; with reset_step the argmax is logged as
+// token 0 of a Generate call.
+int prefill_batched(llmdot_hip_model* m, const int32_t* tokens, int n, int pos0, bool reset_step) {
+    if (int rc = ensure_prefill_ws(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    int T = 0;
+    for (int c0 = 0; c0 < n; c0 += m->pf_cap) {
+        T = std::min(m->pf_cap, n - c0);
+        HIPCHK(hipMemcpyAsync(m->pf_tokens, tokens + c0, sizeof(int32_t) * (size_t)T, hipMemcpyHostToDevice, s));
+        if (int rc = enqueue_prefill_chunk(m, T, pos0 + c0)) return rc;
+    }
+    const float* h_last = m->pf_h + (size_t)(T - 1) * m->d.hidden;
+    HIPCHK(launch_pack_norm(h_last, m->out_norm_f, m->d.hidden, m->xn, m->xssq, s));
+    if (int rc = set_int(m, m_pos(m), pos0 + n - 1)) return rc;
+    if (reset_step)
+        if (int rc = set_int(m, m_step(m), 0)) return rc;
+    return enqueue_head(m);
+}
+
+bool use_batched_prefill(const llmdot_hip_model* m, int n) {
+    return m->pf_eligible && n > 1 && !env_flag("LLMDOT_HIP_SEQ_PREFILL");
 }
 
 }  // namespace
@@ -876,6 +1028,7 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
         if ((rc = A(sizeof(float) * (size_t)g, &p))) return bail(rc); m->am_val = (float*)p;
         if ((rc = A(sizeof(int32_t) * (size_t)g, &p))) return bail(rc); m->am_idx = (int32_t*)p;
     }
+    m->pf_eligible = prefill_check(m);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return bail(fail(LLMDOT_E_DEVICE, "synchronize failed"));
     if ((rc = build_graph(m))) {
         // fall back to eager launches
@@ -931,6 +1084,10 @@ extern "C" int32_t llmdot_hip_prefill(llmdot_hip_model* m, const int32_t* tokens
     if (int rc = check_pos(m, pos0 + n - 1)) return rc;
     for (int i = 0; i < n; i++)
         if (int rc = check_token(m, tokens[i])) return rc;
+    if (use_batched_prefill(m, n)) {
+        if (int rc = prefill_batched(m, tokens, n, pos0, false)) return rc;
+        return fetch_outputs(m, logits, am);
+    }
     if (int rc = set_int(m, m_pos(m), pos0)) return rc;
     for (int i = 0; i < n; i++) {
         if (int rc = set_int(m, m_token(m), tokens[i])) return rc;
@@ -957,12 +1114,16 @@ extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* promp
     const int fit = d.context - np + 1;
     const int produce = max_tokens < fit ? max_tokens : fit;
     hipStream_t s = m->ctx->stream;
-    if (int rc = set_int(m, m_pos(m), 0)) return rc;   // KvCache.Reset (IE:79)
-    for (int i = 0; i < np; i++) {
-        if (i == np - 1)
-            if (int rc = set_int(m, m_step(m), 0)) return rc;
-        if (int rc = set_int(m, m_token(m), pr[i])) return rc;
-        if (int rc = run_step(m)) return rc;
+    if (use_batched_prefill(m, np)) {
+        if (int rc = prefill_batched(m, pr.data(), np, 0, true)) return rc;   // KvCache.Reset (IE:79) + prompt
+    } else {
+        if (int rc = set_int(m, m_pos(m), 0)) return rc;   // KvCache.Reset (IE:79)
+        for (int i = 0; i < np; i++) {
+            if (i == np - 1)
+                if (int rc = set_int(m, m_step(m), 0)) return rc;
+            if (int rc = set_int(m, m_token(m), pr[i])) return rc;
+            if (int rc = run_step(m)) return rc;
+        }
     }
     if (logits_out) HIPCHK(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
     for (int g = 1; g < produce; g++) {
@@ -1036,6 +1197,32 @@ extern "C" int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* m, int32_t 
     HIPCHK(launch_fill_random_half(m->vcache, count, seed ^ 0x5DEECE66Dull, m->d.kv_fp16, m->ctx->stream));
     HIPCHK(hipStreamSynchronize(m->ctx->stream));
     return 0;
+}
+
+extern "C" int32_t llmdot_hip_model_time_prefill(llmdot_hip_model* m, const int32_t* tokens, int32_t n, int32_t pos0,
+                                                 float* ms) {
+    if (!m || !tokens || n <= 0 || !ms) return fail(LLMDOT_E_INVALID, "bad prefill timing arguments");
+    if (!m->pf_eligible) return fail(LLMDOT_E_UNSUPPORTED, "the model's weight types have no batched prefill kernel");
+    if (int rc = check_pos(m, pos0)) return rc;
+    if (int rc = check_pos(m, pos0 + n - 1)) return rc;
+    for (int i = 0; i < n; i++)
+        if (int rc = check_token(m, tokens[i])) return rc;
+    if (int rc = ensure_prefill_ws(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    HIPCHK(hipStreamSynchronize(s));
+    HIPCHK(hipEventRecord(e0, s));
+    int rc = prefill_batched(m, tokens, n, pos0, false);
+    if (rc == 0) {
+        HIPCHK(hipEventRecord(e1, s));
+        HIPCHK(hipEventSynchronize(e1));
+        HIPCHK(hipEventElapsedTime(ms, e0, e1));
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
 }
 
 extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t first_token, int32_t position, int32_t steps,

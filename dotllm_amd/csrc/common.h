@@ -98,6 +98,27 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// NeoX rotation of element d of a head (TensorOps.ApplyRoPE, TO:679-743):
+// pairs (i, i + half) with the position's cos/sin, dims >= 2*half untouched.
+__device__ __forceinline__ float rope_elem(const float* x, int d, int half, const float* cs, const float* sn) {
+#pragma clang fp contract(off)
+    if (d < half) return x[d] * cs[d] - x[d + half] * sn[d];
+    if (d < 2 * half) return x[d - half] * sn[d - half] + x[d] * cs[d - half];
+    return x[d];
+}
+
+// Stores one KV cache element (fp16: round to nearest even) and returns the
+// value as later reads see it.
+__device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int fp16) {
+    if (fp16) {
+        const _Float16 h = (_Float16)v;
+        reinterpret_cast<_Float16*>(cache)[idx] = h;
+        return (float)h;
+    }
+    reinterpret_cast<float*>(cache)[idx] = v;
+    return v;
+}
+
 // One lane of ExpApproxVector (src/Llmdot.Core/Tensors/Numeric/VectorMath.cs:137-166),
 // bit-exact: every operation is a separately rounded fp32 op (contraction is
 // switched off in the function body; the __f*_rn spellings alone do not stop it).

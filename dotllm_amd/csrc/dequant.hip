@@ -122,6 +122,22 @@ hipError_t launch_pack_norm(const float* x, const float* w, int n, float* packed
     return hipGetLastError();
 }
 
+// Embedding rows of a token chunk: grid (hidden / 256, T).
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t* __restrict__ table, uint32_t type, int hidden,
+                                                         int64_t row_bytes, const int32_t* __restrict__ tokens,
+                                                         float* __restrict__ out) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i < hidden) out[(int64_t)t * hidden + i] = deq_elem(type, table + (int64_t)tokens[t] * row_bytes, i);
+}
+
+hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, int hidden, const int32_t* tokens, int T, float* out,
+                             hipStream_t s) {
+    if (T <= 0 || hidden <= 0) return hipErrorInvalidValue;
+    embed_rows_kernel<<<dim3((hidden + 255) / 256, T), 256, 0, s>>>(table, type, hidden, byte_count(type, hidden), tokens,
+                                                                      out);
+    return hipGetLastError();
+}
+
 hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num_rows, int row_elems,
                           hipStream_t s) {
     int64_t rb = byte_count(type, row_elems);

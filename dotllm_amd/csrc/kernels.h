@@ -110,4 +110,40 @@ int attn_max_chunks(int heads, int kv_heads, int context);
 bool attn_supported(int heads, int kv_heads, int head_dim);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
+// ---- prefill.hip (batched prompt processing) ----
+// Activation planes of a [M][K] fp32 matrix: xh/xl [M][K] fp16 (x s = xh + xl,
+// s a power of two per row), sh/sl [M][K/32] fp16 (group sums of x times s/32),
+// xinv [M] = 1/s.
+struct PfPlanes {
+    _Float16 *xh, *xl, *sh, *sl;
+    float* xinv;
+};
+struct PfAttnArgs {
+    const float* q;           // [T][heads*head_dim] projections (pre-RoPE)
+    const float* k;           // [T][kv_heads*head_dim]
+    const float* v;
+    float* qr;                // [T][heads*head_dim] rotated q
+    void* kcache;             // this layer: [kv_heads][context][head_dim]
+    void* vcache;
+    const float* cos_tab;     // [context][rope_half]
+    const float* sin_tab;
+    float* scores;            // [heads][T][ld_scores]
+    float* rowmax;            // [heads][T]
+    float* out;               // [T][heads*head_dim]
+    int T, pos0, ld_scores, heads, kv_heads, head_dim, rope_half, context, kv_fp16;
+};
+bool prefill_gemm_supported(uint32_t type, int cols);
+// Optional RmsNorm (norm_w non-null) of each row of x, then its planes.
+hipError_t launch_prefill_planes(const float* x, int M, int K, const float* norm_w, float eps, const PfPlanes& p,
+                                 hipStream_t s);
+// out[M][ldo] (=, += for epi 1, SiLU(gate) * up for epi 2 with w = gate, w2 = up)
+// of the planes times the [N][K] weight blocks, transposed.
+hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const uint8_t* w, const uint8_t* w2, int M,
+                               int N, int K, float* out, int ldo, hipStream_t s);
+hipError_t launch_prefill_rope_kv(const PfAttnArgs& a, hipStream_t s);
+hipError_t launch_prefill_attention(const PfAttnArgs& a, hipStream_t s);
+// Embedding rows tokens[0..T) (device ids) into out[T][hidden].
+hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, int hidden, const int32_t* tokens, int T, float* out,
+                             hipStream_t s);
+
 }  // namespace llmdot

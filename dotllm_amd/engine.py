@@ -222,6 +222,14 @@ class InferenceEngine:
     def kv_fill_random(self, n: int, seed: int = 1) -> None:
         _call(lib().llmdot_hip_model_kv_fill_random(self._m, int(n), int(seed)))
 
+    def time_prefill(self, tokens, pos0: int = 0) -> float:
+        """Milliseconds (HIP events) of the batched prompt path over tokens from pos0."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        ms = C.c_float(0)
+        _call(lib().llmdot_hip_model_time_prefill(self._m, t.ctypes.data_as(C.POINTER(C.c_int32)), t.size, int(pos0),
+                                                  C.byref(ms)))
+        return ms.value
+
     def time_decode(self, first_token: int, position: int, steps: int, per_kernel: bool = False) -> dict:
         t = _lib.StepTiming()
         _call(lib().llmdot_hip_model_time_decode(self._m, int(first_token), int(position), int(steps),

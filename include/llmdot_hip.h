@@ -74,7 +74,8 @@ int32_t llmdot_hip_has_weight(llmdot_hip_ctx* ctx, const char* key, int32_t* pre
 /* ICB:9  MatMul(a, b, result, bType, aCols, bCols, weightKey).
  * result_len = aRows * bCols.  When weight_key names an uploaded weight, b may
  * be NULL and the resident copy is used; otherwise b is uploaded for this call
- * (and kept under weight_key when weight_key is non-NULL). */
+ * (and kept under weight_key when weight_key is non-NULL).  With aRows > 1
+ * (TO:92-111) and a batched kernel for b_type, all rows run as one MFMA GEMM. */
 int32_t llmdot_hip_matmul(llmdot_hip_ctx* ctx, const float* a, const void* b, float* result,
                           int64_t result_len, uint32_t b_type, int32_t a_cols, int32_t b_cols,
                           const char* weight_key);
@@ -166,12 +167,17 @@ int32_t llmdot_hip_model_reset(llmdot_hip_model* model);
  * argmax_or_null receives ArgMax(logits). */
 int32_t llmdot_hip_decode_step(llmdot_hip_model* model, int32_t token, int32_t position,
                                float* logits_or_null, int32_t* argmax_or_null);
-/* Sequential prompt processing (IE:84-88): tokens[i] at position pos0 + i.
- * Outputs refer to the last token. */
+/* Prompt processing (the sequential loop of IE:84-88): tokens[i] at position
+ * pos0 + i; outputs refer to the last token.  When every projection's type has
+ * a batched kernel (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0) and n > 1 the tokens run as
+ * chunks of batched MFMA GEMMs with causal attention over the chunk and the
+ * cache; otherwise (or with LLMDOT_HIP_SEQ_PREFILL=1) one decode step per token.
+ * Either way the KV cache ends as the sequential loop leaves it. */
 int32_t llmdot_hip_prefill(llmdot_hip_model* model, const int32_t* tokens, int32_t n, int32_t pos0,
                            float* logits_or_null, int32_t* argmax_or_null);
 /* Greedy Generate (IE:74-132, Sampler.cs:26-27): resets the cache, processes the
- * prompt, then yields max_tokens tokens (stopping after eos when eos >= 0).
+ * prompt (as llmdot_hip_prefill), then yields max_tokens tokens (stopping after
+ * eos when eos >= 0).
  * The decode loop runs on the device (token feedback stays in HBM).
  * logits_out (nullable) receives [max_tokens][vocab]: the logits each token was
  * sampled from. */
@@ -196,6 +202,12 @@ typedef struct llmdot_hip_step_timing {
     int32_t gemv_launches;
     double gemv_bytes;       /* algorithmic bytes of those launches (weights + x + y) */
 } llmdot_hip_step_timing;
+/* Batched prompt processing of n tokens from pos0 (as llmdot_hip_prefill,
+ * including the last token's LM head) timed with HIP events on the model's
+ * stream; fails with LLMDOT_E_UNSUPPORTED when the model has no batched path.
+ * No reference counterpart (the reference has no batched prompt path). */
+int32_t llmdot_hip_model_time_prefill(llmdot_hip_model* model, const int32_t* tokens, int32_t n,
+                                      int32_t pos0, float* ms);
 int32_t llmdot_hip_model_time_decode(llmdot_hip_model* model, int32_t first_token, int32_t position,
                                      int32_t steps, int32_t per_kernel, llmdot_hip_step_timing* out);
 /* Algorithmic HBM bytes of one decode step at `position`: quantized weights read
