@@ -28,12 +28,17 @@
 //  rounding-level error, like the decode GEMV.
 //
 // Tiles: 128 tokens x 128 weight rows per 256-thread workgroup; wave w owns
-// tokens 64 (w & 1) .. +63 and rows 64 (w >> 1) .. +63 as 4 x 4 MFMA tiles.
-// K advances 32 per step (one MFMA K), the scale chunk is 256 (K-quants) or
-// 32 (Q8_0, Q4_0).  Global loads of step s+1 are issued before the MFMAs of
-// step s; their dequantisation follows the MFMAs so it overlaps them.
+// all 128 tokens and rows 32 w .. 32 w + 31 as 8 x 2 MFMA tiles, so each
+// wave dequantises only its own 32 rows.  K advances 32 per step (one MFMA
+// K).  Each step's activation planes and raw weight blocks are copied
+// global -> LDS by the waves (global_load_lds, no registers) two steps ahead;
+// each wave then builds its weight fragments from the raw bytes in LDS.
 #include "common.h"
 #include "kernels.h"
+
+// dma16 below names m0 (the LDS base of global_load_lds) as clobbered; nothing
+// else in this file keeps a value in m0.
+#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace llmdot {
 
@@ -148,6 +153,7 @@ struct PfGemmArgs {
     const uint8_t* w2;                   // SWIGLU: the up matrix (w = gate)
     float* out;                          // [M][ldo]
     int M, N, K, ldo;
+    int tiles_n;                         // weight-row tiles (128 rows; SWIGLU: 64 gate + 64 up)
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -175,342 +181,369 @@ __device__ __forceinline__ uint32_t k_field12(uint32_t w1, uint32_t w2, uint32_t
     return __builtin_amdgcn_alignbit(hi, lo, (uint32_t)(b & 31)) & 0xFFFu;
 }
 
-// Per-thread staging registers of one 32-K step: this thread's weight bytes
-// (one row half: 16 elements) and the row's scale fields.
-struct Stage {
-    uint32_t q[4];      // weight payload bytes (Q4_K/Q5_K: q[0..1])
-    uint32_t qh[4];     // Q6_K: high bits; Q5_K: qh[0] = 16 high bits
-    uint32_t hdr[4];    // Q4_K/Q5_K: the 16-byte block header; others: hdr[0] = fp16 d, hdr[1] = Q6_K scale byte
-};
-
-typedef __attribute__((address_space(1))) void gvoid;
-typedef __attribute__((address_space(3))) void lvoid;
-
+// Weight formats on the batched path.  Per 32-element step a row contributes
+// R 16-byte chunks of raw block bytes.  K-quants (16-byte aligned blocks) keep
+// chunk ch of all 128 rows together in LDS ([ch][row]: a fragment read of 16
+// rows touches 256 contiguous bytes); the 2-byte aligned formats copy windows
+// starting at the block address rounded down to 4 bytes ([row][ch]).
+// Every step's partial sum is scaled by the row's block scale d; NP = weight
+// planes; NS = LDS stages (prefetch distance NS - 1).
 template <uint32_t FMT>
 struct PfFmt;
 template <>
-struct PfFmt<GGML_Q4_K> { static constexpr int SB = 8, NP = 1, BSZ = 144, EPB = 256; static constexpr bool MIN = true; };
+struct PfFmt<GGML_Q4_K> { static constexpr int BSZ = 144, EPB = 256, R = 2, NP = 1, NS = 2; static constexpr bool MIN = true, KQ = true; };
 template <>
-struct PfFmt<GGML_Q5_K> { static constexpr int SB = 8, NP = 1, BSZ = 176, EPB = 256; static constexpr bool MIN = true; };
+struct PfFmt<GGML_Q5_K> { static constexpr int BSZ = 176, EPB = 256, R = 4, NP = 1, NS = 2; static constexpr bool MIN = true, KQ = true; };
 template <>
-struct PfFmt<GGML_Q6_K> { static constexpr int SB = 8, NP = 2, BSZ = 210, EPB = 256; static constexpr bool MIN = false; };
+struct PfFmt<GGML_Q6_K> { static constexpr int BSZ = 210, EPB = 256, R = 8, NP = 2, NS = 2; static constexpr bool MIN = false, KQ = false; };
 template <>
-struct PfFmt<GGML_Q8_0> { static constexpr int SB = 1, NP = 1, BSZ = 34, EPB = 32; static constexpr bool MIN = false; };
+struct PfFmt<GGML_Q8_0> { static constexpr int BSZ = 34, EPB = 32, R = 4, NP = 1, NS = 2; static constexpr bool MIN = false, KQ = false; };
 template <>
-struct PfFmt<GGML_Q4_0> { static constexpr int SB = 1, NP = 1, BSZ = 18, EPB = 32; static constexpr bool MIN = false; };
+struct PfFmt<GGML_Q4_0> { static constexpr int BSZ = 18, EPB = 32, R = 2, NP = 1, NS = 2; static constexpr bool MIN = false, KQ = false; };
 
-// Global loads of step `st` (K offset 32 st) for this thread's weight row half.
+// K-quants: byte offset of chunk ch of group g within a superblock.
 template <uint32_t FMT>
-__device__ __forceinline__ void load_w(Stage& S, const uint8_t* rowp, int st, int hf) {
+__device__ __forceinline__ int kq_chunk_off(int ch, int g) {
+    if constexpr (FMT == GGML_Q4_K) return ch == 0 ? 0 : 16 + 16 * g;                          // header | quants of g
+    else return ch == 0 ? 0 : ch == 1 ? 48 + 16 * g : 16 + 16 * (g >> 2);                   // header | low nibbles | high bits
+}
+// 2-byte aligned formats: byte offset (from the row start) of the window that
+// chunk ch of step st belongs to, and the chunk's index inside that window.
+template <uint32_t FMT>
+__device__ __forceinline__ void win_chunk(int st, int ch, int64_t* off, int* k) {
     using F = PfFmt<FMT>;
-    if constexpr (FMT == GGML_Q4_K || FMT == GGML_Q5_K) {
-        const int sb = st >> 3, g = st & 7;
-        const uint8_t* blk = rowp + (int64_t)sb * F::BSZ;
-        const u32x4 h = ld16_a4(blk);
-        S.hdr[0] = h.x; S.hdr[1] = h.y; S.hdr[2] = h.z; S.hdr[3] = h.w;
-        if constexpr (FMT == GGML_Q4_K) {
-            const uint2 v = *reinterpret_cast<const uint2*>(blk + 16 + 16 * g + 8 * hf);
-            S.q[0] = v.x; S.q[1] = v.y;
-        } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(blk + 48 + 16 * g + 8 * hf);
-            S.q[0] = v.x; S.q[1] = v.y;
-            S.qh[0] = *reinterpret_cast<const uint16_t*>(blk + 16 + 4 * g + 2 * hf);
-        }
-    } else if constexpr (FMT == GGML_Q6_K) {
-        const int sb = st >> 3, g = st & 7;
-        const uint8_t* blk = rowp + (int64_t)sb * F::BSZ;
-        const int n = 128 * (g >> 2), qq = g & 3;
-        ld_realign<4>(blk + n / 2 + (qq & 1) * 32 + 16 * hf, S.q);
-        ld_realign<4>(blk + 128 + n / 4 + 16 * hf, S.qh);
-        S.hdr[0] = *reinterpret_cast<const uint16_t*>(blk + 208);
-        S.hdr[1] = blk[192 + 2 * g + hf];   // int8 scale of elements 32 g + 16 hf .. +15
-    } else {   // Q8_0, Q4_0: one block per step
-        const uint8_t* blk = rowp + (int64_t)st * F::BSZ;
-        S.hdr[0] = *reinterpret_cast<const uint16_t*>(blk);
-        if constexpr (FMT == GGML_Q8_0) ld_realign<4>(blk + 2 + 16 * hf, S.q);
-        else ld_realign<4>(blk + 2, S.q);
+    if constexpr (FMT == GGML_Q6_K) {
+        const int g = st & 7, n = 128 * (g >> 2), qq = g & 3;
+        const int64_t blk = (int64_t)(st >> 3) * F::BSZ;
+        *off = blk + (ch < 3 ? n / 2 + (qq & 1) * 32 : ch < 6 ? 128 + n / 4 : 192);     // ql | qh | scales + d
+        *k = ch < 3 ? ch : ch < 6 ? ch - 3 : ch - 6;
+    } else {   // Q8_0, Q4_0: the block
+        *off = (int64_t)st * F::BSZ;
+        *k = ch < 2 ? ch : 2;
     }
 }
 
-// Dequantises this thread's 16 elements (plane 0, and plane 1 for Q6_K) into
-// out[plane][8] words of fp16 pairs in natural element order.
+// 8 bytes starting at byte offset o (any alignment) of an LDS array, as 2 words.
+__device__ __forceinline__ void lds_bytes8(const unsigned char* p, int o, uint32_t* w) {
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(p + (o & ~3));
+    const uint32_t sh = (uint32_t)(o & 3);
+    const uint32_t a = d[0], b = d[1], c = d[2];
+    w[0] = __builtin_amdgcn_alignbyte(b, a, sh);
+    w[1] = __builtin_amdgcn_alignbyte(c, b, sh);
+}
+
+// K-quant B fragment: elements 8 lk .. 8 lk + 7 of group g for the row whose
+// header (16 bytes) is at hdr and whose quant chunk(s) start at qs (next chunk
+// 2048 bytes further): fp16 sc * (q - 8|16), exact.
 template <uint32_t FMT>
-__device__ __forceinline__ void convert_w(const Stage& S, int st, int hf, uint32_t (*out)[8]) {
-    if constexpr (FMT == GGML_Q4_K || FMT == GGML_Q5_K) {
-        const int g = st & 7;
-        const uint32_t f = k_field12(S.hdr[1], S.hdr[2], S.hdr[3], 12 * g);
-        const _Float16 sc = (_Float16)(float)(f & 63u);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint32_t w = S.q[j];
-            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-            uint32_t n0 = perm(hi, lo, 0x05010400u);   // elements 8j+0..3 as bytes
-            uint32_t n1 = perm(hi, lo, 0x07030602u);   // elements 8j+4..7
-            if constexpr (FMT == GGML_Q5_K) {
-                const uint32_t hb = S.qh[0] >> (8 * j);
-                n0 |= ((((hb & 15u) * 0x00204081u) & 0x01010101u) << 4);
-                n1 |= (((((hb >> 4) & 15u) * 0x00204081u) & 0x01010101u) << 4);
-                bytes_to_h2(n0, (_Float16)1040.f, sc, &out[0][4 * j]);
-                bytes_to_h2(n1, (_Float16)1040.f, sc, &out[0][4 * j + 2]);
-            } else {
-                bytes_to_h2(n0, (_Float16)1032.f, sc, &out[0][4 * j]);
-                bytes_to_h2(n1, (_Float16)1032.f, sc, &out[0][4 * j + 2]);
-            }
-        }
-    } else if constexpr (FMT == GGML_Q6_K) {
-        const int g = st & 7, qq = g & 3;
-        const int scv = (int)(int8_t)(uint8_t)S.hdr[1];
+__device__ __forceinline__ h8 kq_frag(const unsigned char* hdr, const unsigned char* qs, int g, int lk) {
+    const int b = 12 * g;   // scale field bit offset in bytes 4..15 (wave-uniform)
+    const uint2 fw = *reinterpret_cast<const uint2*>(hdr + 4 + 4 * (b >> 5));
+    const _Float16 sc = (_Float16)(float)(__builtin_amdgcn_alignbit(fw.y, fw.x, (uint32_t)(b & 31)) & 63u);
+    const uint32_t w = reinterpret_cast<const uint32_t*>(qs)[lk];
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    uint32_t n0 = perm(hi, lo, 0x05010400u), n1 = perm(hi, lo, 0x07030602u);
+    uint32_t pr[4];
+    if constexpr (FMT == GGML_Q5_K) {
+        const uint32_t hb = qs[2048 + 4 * (g & 3) + lk];
+        n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
+        n1 |= ((((hb >> 4) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+        bytes_to_h2(n0, (_Float16)1040.f, sc, &pr[0]);
+        bytes_to_h2(n1, (_Float16)1040.f, sc, &pr[2]);
+    } else {
+        bytes_to_h2(n0, (_Float16)1032.f, sc, &pr[0]);
+        bytes_to_h2(n1, (_Float16)1032.f, sc, &pr[2]);
+    }
+    return __builtin_bit_cast(h8, v4u{pr[0], pr[1], pr[2], pr[3]});
+}
+
+// Windowed B fragment for the row whose R chunks start at raw; rowoff = the
+// row's byte offset in the tensor (window alignment shifts).
+template <uint32_t FMT>
+__device__ __forceinline__ void win_frag(const unsigned char* raw, int st, int lk, int64_t rowoff, h8* out, float* d) {
+    uint32_t pr[4];
+    if constexpr (FMT == GGML_Q6_K) {
+        const int g = st & 7, n = 128 * (g >> 2), qq = g & 3;
+        const int64_t blk = rowoff + (int64_t)(st >> 3) * 210;
+        const int sA = (int)((blk + n / 2 + (qq & 1) * 32) & 3), sB = (int)((blk + 128 + n / 4) & 3);
+        const int sC = (int)((blk + 192) & 3);
+        uint32_t ql[2], qh[2];
+        lds_bytes8(raw, sA + 8 * lk, ql);
+        lds_bytes8(raw + 48, sB + 8 * lk, qh);
+        const int scv = (int)(int8_t)raw[96 + sC + 2 * g + (lk >> 1)];
+        const uint32_t dw = reinterpret_cast<const uint32_t*>(raw + 96)[(sC + 16) >> 2];
+        *d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw >> (8 * ((sC + 16) & 3))));
         const h2 sc2 = {(_Float16)(float)scv, (_Float16)(float)scv};
         const h2 off = {(_Float16)1056.f, (_Float16)1056.f};
         const uint32_t nsh = 4 * (qq >> 1), qsh = 2 * qq;
+        uint32_t ph[4], pl[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t qb = ((S.q[j] >> nsh) & 0x0F0F0F0Fu) | (((S.qh[j] >> qsh) & 0x03030303u) << 4);
+        for (int j = 0; j < 2; j++) {
+            const uint32_t qb = ((ql[j] >> nsh) & 0x0F0F0F0Fu) | (((qh[j] >> qsh) & 0x03030303u) << 4);
 #pragma unroll
             for (int p = 0; p < 2; p++) {
-                const uint32_t pr = perm(0x64646464u, qb, p ? 0x04030402u : 0x04010400u);
-                const h2 qv = as_h2(pr) - off;                 // q - 32, exact
-                const h2 vh = qv * sc2;                        // rounded to fp16
-                const h2 vl = __builtin_elementwise_fma(qv, sc2, -vh);   // exact remainder
-                out[0][2 * j + p] = as_u(vh);
-                out[1][2 * j + p] = as_u(vl);
+                const h2 qv = as_h2(perm(0x64646464u, qb, p ? 0x04030402u : 0x04010400u)) - off;   // q - 32
+                const h2 vh = qv * sc2;
+                ph[2 * j + p] = as_u(vh);
+                pl[2 * j + p] = as_u(__builtin_elementwise_fma(qv, sc2, -vh));
             }
         }
-    } else if constexpr (FMT == GGML_Q8_0) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) bytes_to_h2(S.q[j] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &out[0][2 * j]);
-    } else {   // Q4_0: half 0 = low nibbles of bytes 0..15, half 1 = high nibbles
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t b = hf ? ((S.q[j] >> 4) & 0x0F0F0F0Fu) : (S.q[j] & 0x0F0F0F0Fu);
-            bytes_to_h2(b, (_Float16)1032.f, (_Float16)1.f, &out[0][2 * j]);
+        out[0] = __builtin_bit_cast(h8, v4u{ph[0], ph[1], ph[2], ph[3]});
+        out[1] = __builtin_bit_cast(h8, v4u{pl[0], pl[1], pl[2], pl[3]});
+    } else {   // Q8_0, Q4_0: window shift s = block offset & 3; d at s, payload at s + 2
+        const int sh = (int)((rowoff + (int64_t)st * PfFmt<FMT>::BSZ) & 3);
+        const uint32_t dw = reinterpret_cast<const uint32_t*>(raw)[0];
+        *d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw >> (8 * sh)));
+        uint32_t q[2];
+        if constexpr (FMT == GGML_Q8_0) {
+            lds_bytes8(raw, sh + 2 + 8 * lk, q);
+            bytes_to_h2(q[0] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &pr[0]);
+            bytes_to_h2(q[1] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &pr[2]);
+        } else {   // elements 0..15: low nibbles of bytes 0..15; 16..31: high nibbles
+            lds_bytes8(raw, sh + 2 + 8 * (lk & 1), q);
+            const uint32_t sft = lk < 2 ? 0u : 4u;
+            bytes_to_h2((q[0] >> sft) & 0x0F0F0F0Fu, (_Float16)1032.f, (_Float16)1.f, &pr[0]);
+            bytes_to_h2((q[1] >> sft) & 0x0F0F0F0Fu, (_Float16)1032.f, (_Float16)1.f, &pr[2]);
         }
+        out[0] = __builtin_bit_cast(h8, v4u{pr[0], pr[1], pr[2], pr[3]});
     }
 }
 
 enum PfEpi : int { PF_STORE = 0, PF_ADD = 1, PF_SWIGLU = 2 };
 
-// Workgroup barrier for LDS hand-offs: waits for this wave's LDS reads and
-// writes, then s_barrier.  Unlike __syncthreads() it does not wait for
-// outstanding global loads (the prefetched steps stay in flight); the
-// activation copies of the step about to be read are complete because the
-// wave has waited for the weight registers issued after them.
+// 16 bytes per lane from global memory straight into LDS: lane i reads
+// base + off_i and writes LDS bytes [lds + 16 i, lds + 16 i + 16) (base and
+// lds wave-uniform).  Issued as inline assembly so that the compiler's
+// wait-count bookkeeping does not serialise it; completion is awaited
+// explicitly with vm_wait below.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+// Waits until at most N of this wave's vector memory operations are outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+// Workgroup barrier after this wave's LDS operations (no wait on global loads).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // LDS rows of 32 halves (64 bytes) hold 4 chunks of 8; chunk c of row r sits
 // at position c ^ swz(r), which spreads the 16 rows of an MFMA fragment read
-// over distinct banks.
+// over distinct banks.  swz(16 i + l) = swz(l) ^ 2 (i & 1).
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 template <uint32_t FMT, int EPI>
 __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     using F = PfFmt<FMT>;
-    constexpr int NP = F::NP;
-    // Activation stages are copied global -> LDS by global_load_lds_dwordx4
-    // (no registers); NXB stages give a prefetch distance of NXB - 1 steps.
-    // Weight bytes travel through registers at the same distance.
-    constexpr int NXB = NP == 2 ? 2 : 3, D = NXB - 1;
-    constexpr int XS1 = 2 * BM * 64;                 // one stage: [plane][token][32 halves]
-    constexpr int XS_B = NXB * XS1;
-    constexpr int WS_B = 2 * NP * BN * 64;           // [buf][plane][row][32 halves]
-    constexpr int WD_B = 2 * BN * 4;                 // [buf][row] block scale d
-    constexpr int WM_B = F::MIN ? 2 * BN * 4 : 0;    // [sb parity][row] 32 dmin
-    constexpr int WQ_B = F::MIN ? 2 * BN * 16 : 0;   // [sb parity][row][8] m_g
+    constexpr int NP = F::NP, R = F::R, NS = F::NS;
+    constexpr int TI = BM / 16, TJ = BN / 16 / 4;    // wave w: all BM tokens x rows 16 TJ w .. +16 TJ - 1
+    constexpr int XS1 = 2 * BM * 64;                 // activation stage: [plane][token][32 halves]
+    constexpr int WS1 = BN * R * 16;                 // raw weight stage
+    constexpr int ST1 = XS1 + WS1;
     constexpr int SS_B = F::MIN ? 2 * 2 * BM * 16 : 0;   // [sb parity][plane][token][8] group sums
-    constexpr int STAGE_B = XS_B + WS_B + WD_B + WM_B + WQ_B + SS_B;
-    constexpr int EX_B = 2 * 64 * 65 * 4;            // SWIGLU exchange
+    constexpr int STAGE_B = NS * ST1 + SS_B;
+    constexpr int EX_B = 2 * BM * (16 * TJ + 1) * 4;     // SWIGLU exchange: [gate wave][token][rows + 1]
     constexpr int SMEM = STAGE_B > EX_B ? STAGE_B : EX_B;
+    constexpr int NX = 4, NW = R / 2;                // DMA instructions per wave and step
     __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-    unsigned char* const Xb = smem;
-    unsigned char* const Wb = smem + XS_B;
-    float* const Wd = reinterpret_cast<float*>(smem + XS_B + WS_B);
-    float* const Wm = reinterpret_cast<float*>(smem + XS_B + WS_B + WD_B);
-    unsigned char* const Wq = smem + XS_B + WS_B + WD_B + WM_B;
-    unsigned char* const Ss = smem + XS_B + WS_B + WD_B + WM_B + WQ_B;
-    auto xaddr = [&](int buf, int pl, int r, int c) { return Xb + buf * XS1 + (pl * BM + r) * 64 + ((c ^ swz(r)) << 4); };
-    auto waddr = [&](int buf, int pl, int r, int c) { return Wb + ((buf * NP + pl) * BN + r) * 64 + ((c ^ swz(r)) << 4); };
+    const uint32_t sm = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    unsigned char* const Ss = smem + NS * ST1;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1, lr = lane & 15, lk = lane >> 4;
-    const int m0 = blockIdx.y * BM;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lk = lane >> 4;
+    // XCD-aware tile order: workgroup L runs on XCD L % 8, which takes the
+    // contiguous tile range [xcd * per, (xcd + 1) * per) in token-tile-major
+    // order, so the workgroups resident on one XCD share a token tile and its
+    // activation stream stays in that XCD's L2.
+    const int ntm = (a.M + BM - 1) / BM, ntn = a.tiles_n, per = (ntm * ntn + 7) / 8;
+    const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (tile >= ntm * ntn) return;
+    const int tn = tile % ntn, m0 = (tile / ntn) * BM;
     const int K = a.K, nsteps = K / 32;
-
-    // weight row staged by this thread: rows 0..127 of the tile, two threads per row
-    const int srow = tid >> 1, hf = tid & 1;
-    int grow;
-    const uint8_t* wbase = a.w;
-    if (EPI == PF_SWIGLU) {
-        grow = blockIdx.x * 64 + (srow & 63);
-        if (srow >= 64) wbase = a.w2;
-    } else {
-        grow = blockIdx.x * BN + srow;
-    }
-    grow = min(grow, a.N - 1);
     const int64_t rbytes = (int64_t)(K / F::EPB) * F::BSZ;
-    const uint8_t* rowp = wbase + (int64_t)grow * rbytes;
+    auto grow_of = [&](int r) {   // tile row -> weight row (SWIGLU: rows 0..63 gate, 64..127 up)
+        const int g = EPI == PF_SWIGLU ? tn * 64 + (r & 63) : tn * BN + r;
+        return min(g, a.N - 1);
+    };
+    auto wsel = [&](int r) -> const uint8_t* { return EPI == PF_SWIGLU && r >= 64 ? a.w2 : a.w; };
 
-    // Activation stage st: wave w's instruction i fills LDS slots (4w + i) * 64 + lane
-    // (16 bytes each) of the stage; slot q holds plane q >> 9, token (q >> 2) & 127,
-    // position q & 3, i.e. chunk (q & 3) ^ swz(token) of the token's 32 elements.
-    auto load_x = [&](int st) __attribute__((always_inline)) {
-        unsigned char* base = Xb + (st % NXB) * XS1;
+    // DMA sources.  Activations: instruction i of wave wv covers stage slots
+    // q = (NX wv + i) 64 + lane: plane q >> 9, token (q >> 2) & 127, position
+    // q & 3 holding chunk (q & 3) ^ swz(token).
+    uint32_t xoff[NX];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int q = (4 * wave + i) * 64 + lane;
-            const int pl = q >> 9, tk = (q >> 2) & 127, c = (q & 3) ^ swz(tk);
-            const int tg = min(m0 + tk, a.M - 1);
-            const _Float16* src = (pl ? a.xl : a.xh) + (int64_t)tg * K + 32 * st + 8 * c;
-            __builtin_amdgcn_global_load_lds((gvoid*)src, (lvoid*)(base + (4 * wave + i) * 1024), 16, 0, 0);
-        }
-        if (F::MIN && (st & 7) == 0) {   // group sums of the superblock: [plane][token] 16-byte rows
-            const int q = wave * 64 + lane;
-            const int pl = q >> 7, tk = q & 127;
-            const int tg = min(m0 + tk, a.M - 1);
-            const _Float16* src = (pl ? a.sl : a.sh) + (int64_t)tg * (K / 32) + 8 * (st >> 3);
-            __builtin_amdgcn_global_load_lds((gvoid*)src, (lvoid*)(Ss + ((st >> 3) & 1) * (2 * BM * 16) + wave * 1024),
-                                             16, 0, 0);
-        }
-    };
-    // Issues step st's loads: the activation copies first, then the weight
-    // registers.  Loads return in issue order, so once a wave has the weight
-    // registers of step st its activation copies of step st are in LDS too.
-    auto load = [&](Stage& S, int st) __attribute__((always_inline)) {
-        load_x(st);
-        __builtin_amdgcn_sched_barrier(0);
-        load_w<FMT>(S, rowp, st, hf);
-    };
-    auto store_w = [&](const Stage& S, int st) __attribute__((always_inline)) {
-        const int buf = st & 1;
-        uint32_t wv[2][8];
-        convert_w<FMT>(S, st, hf, wv);
+    for (int i = 0; i < NX; i++) {
+        const int q = (NX * wv + i) * 64 + lane;
+        const int tk = (q >> 2) & 127, c = (q & 3) ^ swz(tk);
+        xoff[i] = (uint32_t)(((int64_t)min(m0 + tk, a.M - 1) * K + 8 * c) * 2);
+    }
+    // Weights: K-quants: slot q = ch * 128 + row (ch uniform per instruction);
+    // others: slot q = row * R + ch.
+    uint32_t woff[NW];
+    int64_t wrow[NW];
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-            *reinterpret_cast<v4u*>(waddr(buf, p, srow, 2 * hf)) = v4u{wv[p][0], wv[p][1], wv[p][2], wv[p][3]};
-            *reinterpret_cast<v4u*>(waddr(buf, p, srow, 2 * hf + 1)) = v4u{wv[p][4], wv[p][5], wv[p][6], wv[p][7]};
-        }
-        if (hf == 0) Wd[buf * BN + srow] = (float)__builtin_bit_cast(_Float16, (uint16_t)(S.hdr[0] & 0xFFFFu));
-        if constexpr (F::MIN) {
-            if ((st & 7) == 0 && hf == 0) {
-                const int sp = (st >> 3) & 1;
-                Wm[sp * BN + srow] = 32.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(S.hdr[0] >> 16));
-                h8 mv;
+    for (int j = 0; j < NW; j++) {
+        const int q = (NW * wv + j) * 64 + lane;
+        const int r = F::KQ ? (q & 127) : q / R;
+        wrow[j] = (int64_t)grow_of(r) * rbytes;
+        woff[j] = (uint32_t)wrow[j];
+    }
+    uint32_t soff = 0;
+    if (F::MIN) soff = (uint32_t)((int64_t)min(m0 + ((wv * 64 + lane) & 127), a.M - 1) * (K / 32) * 2);
+
+    auto issue = [&](int st) __attribute__((always_inline)) {
+        const uint32_t lb = sm + (uint32_t)((st % NS) * ST1);
 #pragma unroll
-                for (int gg = 0; gg < 8; gg++)
-                    mv[gg] = (_Float16)(float)(k_field12(S.hdr[1], S.hdr[2], S.hdr[3], 12 * gg) >> 6);
-                *reinterpret_cast<h8*>(Wq + (sp * BN + srow) * 16) = mv;
+        for (int i = 0; i < NX; i++) {
+            const char* xb = reinterpret_cast<const char*>(((NX * wv + i) >> 3) ? a.xl : a.xh) + 64 * st;
+            dma16(xb, xoff[i], lb + (NX * wv + i) * 1024);
+        }
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+            const int q0 = (NW * wv + j) * 64;
+            if constexpr (F::KQ) {
+                const uint8_t* wb = wsel(q0 & 127) + (int64_t)(st >> 3) * F::BSZ + kq_chunk_off<FMT>(q0 >> 7, st & 7);
+                dma16(wb, woff[j], lb + XS1 + (NW * wv + j) * 1024);
+            } else {
+                int64_t off;
+                int k;
+                win_chunk<FMT>(st, (q0 + lane) % R, &off, &k);
+                const uint32_t o = (uint32_t)(((wrow[j] + off) & ~int64_t(3)) + 16 * k);
+                dma16(wsel(q0 / R), o, lb + XS1 + (NW * wv + j) * 1024);
             }
         }
-    };
-
-    f4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-    // One step: issue step st + D's loads, MFMAs on step st, then step st + 1's
-    // weights into LDS.  With D == 2, cur (step st, already in LDS) takes step
-    // st + 2 and nxt holds step st + 1; with D == 1, nxt takes step st + 1.
-    auto step = [&](int st, Stage& cur, Stage& nxt) __attribute__((always_inline)) {
-        const int xb = st % NXB, wbuf = st & 1;
-        if (st + D < nsteps) load(D == 2 ? cur : nxt, st + D);
-        h8 wb[NP][4];
-        float d[4];
-#pragma unroll
-        for (int tj = 0; tj < 4; tj++) {
-            const int r = wn * 64 + tj * 16 + lr;
-#pragma unroll
-            for (int p = 0; p < NP; p++) wb[p][tj] = *reinterpret_cast<const h8*>(waddr(wbuf, p, r, lk));
-            d[tj] = Wd[wbuf * BN + r];
+        if (F::MIN && (st & 7) == 0) {
+            const char* sbase = reinterpret_cast<const char*>((wv >> 1) ? a.sl : a.sh) + 16 * (st >> 3);
+            dma16(sbase, soff, sm + (uint32_t)(NS * ST1 + ((st >> 3) & 1) * (2 * BM * 16) + wv * 1024));
         }
+    };
+    // fragment addresses: activation rows ti * 16 + lr (two swizzle patterns),
+    // weight rows rw[tj]
+    const int xo0 = lr * 64 + ((lk ^ swz(lr)) << 4), xo1 = lr * 64 + ((lk ^ swz(lr) ^ 2) << 4);
+    int rw[TJ];
+    int64_t frow[TJ];
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-            const int r = wm * 64 + ti * 16 + lr;
-            const h8 x0 = *reinterpret_cast<const h8*>(xaddr(xb, 0, r, lk));
-            const h8 x1 = *reinterpret_cast<const h8*>(xaddr(xb, 1, r, lk));
+    for (int tj = 0; tj < TJ; tj++) {
+        rw[tj] = wv * 16 * TJ + tj * 16 + lr;
+        frow[tj] = (int64_t)grow_of(rw[tj]) * rbytes;
+    }
+
+    f4 acc[TI][TJ];
 #pragma unroll
-            for (int tj = 0; tj < 4; tj++) {
-                f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wb[0][tj], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, wb[0][tj], c, 0, 0, 0);
-                if constexpr (NP == 2) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wb[1][tj], c, 0, 0, 0);
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    issue(0);
+    if (NS == 3 && nsteps > 1) issue(1);
+    for (int st = 0; st < nsteps; st++) {
+        // step st's copies are complete once at most the later step's remain
+        if (NS == 3 && st + 1 < nsteps) {
+            if (F::MIN && ((st + 1) & 7) == 0) vm_wait<NX + NW + 1>();
+            else vm_wait<NX + NW>();
+        } else {
+            vm_wait<0>();
+        }
+        lds_barrier();   // every wave's copies of step st landed; step st - 1's buffers are free
+        if (st + NS - 1 < nsteps) issue(st + NS - 1);
+        const unsigned char* sb = smem + (st % NS) * ST1;
+        const unsigned char* raw = sb + XS1;
+        h8 wf[TJ][NP];
+        float d[TJ];
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) {
+            if constexpr (F::KQ) {
+                wf[tj][0] = kq_frag<FMT>(raw + rw[tj] * 16, raw + 2048 + rw[tj] * 16, st & 7, lk);
+                d[tj] = (float)*reinterpret_cast<const _Float16*>(raw + rw[tj] * 16);
+            } else {
+                win_frag<FMT>(raw + rw[tj] * R * 16, st, lk, frow[tj], wf[tj], &d[tj]);
+            }
+        }
+        // activation fragments of tile ti + 1 are read while tile ti's MFMAs issue
+        h8 xn0 = *reinterpret_cast<const h8*>(sb + xo0), xn1 = *reinterpret_cast<const h8*>(sb + xo0 + BM * 64);
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) {
+            const h8 x0 = xn0, x1 = xn1;
+            if (ti + 1 < TI) {
+                const unsigned char* xr = sb + (ti + 1) * 1024 + (((ti + 1) & 1) ? xo1 : xo0);
+                xn0 = *reinterpret_cast<const h8*>(xr);
+                xn1 = *reinterpret_cast<const h8*>(xr + BM * 64);
+            }
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++) {
+                f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wf[tj][0], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, wf[tj][0], c, 0, 0, 0);
+                if constexpr (NP == 2) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wf[tj][1], c, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[ti][tj][e] += d[tj] * c[e];
             }
         }
         if constexpr (F::MIN) {
-            if ((st & 7) == 7) {   // superblock end: acc -= 32 dmin (sum_g m_g S_g) / 32
+            if ((st & 7) == 7) {   // superblock end: acc -= 32 dmin * (sum_g m_g S_g) / 32
                 const int sp = (st >> 3) & 1;
 #pragma unroll
-                for (int tj = 0; tj < 4; tj++) {
-                    const int rl = wn * 64 + tj * 16 + lr;
-                    const float dm = Wm[sp * BN + rl];
+                for (int tj = 0; tj < TJ; tj++) {
+                    const uint32_t* hw = reinterpret_cast<const uint32_t*>(raw + rw[tj] * 16);
+                    const float dm = 32.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(hw[0] >> 16));
                     h4 mq = h4{0, 0, 0, 0};
-                    if (lk < 2) mq = *reinterpret_cast<const h4*>(Wq + (sp * BN + rl) * 16 + 8 * lk);
+                    if (lk < 2) {
+                        const uint32_t h1 = hw[1], h2w = hw[2], h3 = hw[3];
 #pragma unroll
-                    for (int ti = 0; ti < 4; ti++) {
-                        const int tl = wm * 64 + ti * 16 + lr;
+                        for (int gg = 0; gg < 4; gg++)
+                            mq[gg] = (_Float16)(float)(k_field12(h1, h2w, h3, 12 * (4 * lk + gg)) >> 6);
+                    }
+#pragma unroll
+                    for (int ti = 0; ti < TI; ti++) {
+                        const int tl = ti * 16 + lr;
                         h4 s0 = h4{0, 0, 0, 0}, s1 = h4{0, 0, 0, 0};
                         if (lk < 2) {
                             s0 = *reinterpret_cast<const h4*>(Ss + ((sp * 2 + 0) * BM + tl) * 16 + 8 * lk);
                             s1 = *reinterpret_cast<const h4*>(Ss + ((sp * 2 + 1) * BM + tl) * 16 + 8 * lk);
                         }
-                        f4 r = __builtin_amdgcn_mfma_f32_16x16x16f16(s0, mq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        r = __builtin_amdgcn_mfma_f32_16x16x16f16(s1, mq, r, 0, 0, 0);
+                        f4 rr = __builtin_amdgcn_mfma_f32_16x16x16f16(s0, mq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        rr = __builtin_amdgcn_mfma_f32_16x16x16f16(s1, mq, rr, 0, 0, 0);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) acc[ti][tj][e] -= dm * r[e];
+                        for (int e = 0; e < 4; e++) acc[ti][tj][e] -= dm * rr[e];
                     }
                 }
             }
         }
-        if (st + 1 < nsteps) store_w(nxt, st + 1);
-        lds_barrier();
-    };
-
-    Stage S0, S1;
-    S0.qh[0] = S0.qh[1] = S0.qh[2] = S0.qh[3] = 0u;
-    S1.qh[0] = S1.qh[1] = S1.qh[2] = S1.qh[3] = 0u;
-    S0.hdr[1] = S0.hdr[2] = S0.hdr[3] = 0u;
-    S1.hdr[1] = S1.hdr[2] = S1.hdr[3] = 0u;
-    load(S0, 0);
-    if (D == 2 && nsteps > 1) load(S1, 1);
-    store_w(S0, 0);
-    lds_barrier();
-    for (int st = 0; st < nsteps; st += 2) {
-        step(st, S0, S1);
-        if (st + 1 < nsteps) step(st + 1, S1, S0);
     }
+    lds_barrier();   // all waves are done with the stage buffers (SWIGLU reuses them)
+    const int wn = wv;
 
     // epilogue: y = acc / s for token rows; lane holds tokens 4 lk + e of tile ti, row lr of tile tj
-    float xi[4][4];
+    float xi[TI][4];
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++)
+    for (int ti = 0; ti < TI; ti++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) xi[ti][e] = a.xinv[min(m0 + wm * 64 + ti * 16 + 4 * lk + e, a.M - 1)];
+        for (int e = 0; e < 4; e++) xi[ti][e] = a.xinv[min(m0 + ti * 16 + 4 * lk + e, a.M - 1)];
     if (EPI == PF_SWIGLU) {
-        float (*E)[64][65] = reinterpret_cast<float (*)[64][65]>(smem);
-        if (wn == 1) {
+        // waves 2, 3 hold the up rows matching the gate rows of waves 0, 1
+        float (*E)[BM][16 * TJ + 1] = reinterpret_cast<float (*)[BM][16 * TJ + 1]>(smem);
+        if (wn >= 2) {
 #pragma unroll
-            for (int ti = 0; ti < 4; ti++)
+            for (int ti = 0; ti < TI; ti++)
 #pragma unroll
-                for (int tj = 0; tj < 4; tj++)
+                for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) E[wm][ti * 16 + 4 * lk + e][tj * 16 + lr] = acc[ti][tj][e] * xi[ti][e];
+                    for (int e = 0; e < 4; e++) E[wn - 2][ti * 16 + 4 * lk + e][tj * 16 + lr] = acc[ti][tj][e] * xi[ti][e];
         }
         __syncthreads();
-        if (wn == 0) {
+        if (wn < 2) {
             const int n8 = a.N & ~7;
 #pragma unroll
-            for (int ti = 0; ti < 4; ti++)
+            for (int ti = 0; ti < TI; ti++)
 #pragma unroll
-                for (int tj = 0; tj < 4; tj++)
+                for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        const int t = m0 + wm * 64 + ti * 16 + 4 * lk + e;
-                        const int row = blockIdx.x * 64 + tj * 16 + lr;
+                        const int t = m0 + ti * 16 + 4 * lk + e;
+                        const int row = tn * 64 + wn * 16 * TJ + tj * 16 + lr;
                         if (t < a.M && row < a.N) {
 #pragma clang fp contract(off)
                             const float g = acc[ti][tj][e] * xi[ti][e];
-                            const float u = E[wm][ti * 16 + 4 * lk + e][tj * 16 + lr];
+                            const float u = E[wn][ti * 16 + 4 * lk + e][tj * 16 + lr];
                             // SiluInPlace then Mul (IE:463-474): ExpApprox on the vector lanes
                             const float sg = row < n8 ? silu_ref(g) : g / (1.0f + expf(-g));
                             a.out[(int64_t)t * a.ldo + row] = sg * u;
@@ -519,13 +552,13 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         }
     } else {
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++)
+        for (int ti = 0; ti < TI; ti++)
 #pragma unroll
-            for (int tj = 0; tj < 4; tj++)
+            for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int t = m0 + wm * 64 + ti * 16 + 4 * lk + e;
-                    const int row = blockIdx.x * BN + wn * 64 + tj * 16 + lr;
+                    const int t = m0 + ti * 16 + 4 * lk + e;
+                    const int row = tn * BN + wn * 16 * TJ + tj * 16 + lr;
                     if (t < a.M && row < a.N) {
                         const float y = acc[ti][tj][e] * xi[ti][e];
                         float* o = a.out + (int64_t)t * a.ldo + row;
@@ -910,8 +943,10 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
 }
 
 template <uint32_t FMT>
-hipError_t launch_gemm_fmt(int epi, const PfGemmArgs& a, hipStream_t s) {
-    const dim3 grid(epi == PF_SWIGLU ? (a.N + 63) / 64 : (a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+hipError_t launch_gemm_fmt(int epi, PfGemmArgs a, hipStream_t s) {
+    a.tiles_n = epi == PF_SWIGLU ? (a.N + 63) / 64 : (a.N + BN - 1) / BN;
+    const int tiles = a.tiles_n * ((a.M + BM - 1) / BM);
+    const dim3 grid(8 * ((tiles + 7) / 8));
     switch (epi) {
     case PF_STORE: pf_gemm_kernel<FMT, PF_STORE><<<grid, WG, 0, s>>>(a); break;
     case PF_ADD: pf_gemm_kernel<FMT, PF_ADD><<<grid, WG, 0, s>>>(a); break;
@@ -955,7 +990,10 @@ hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const 
                                int N, int K, float* out, int ldo, hipStream_t s) {
     if (M <= 0 || N <= 0 || !prefill_gemm_supported(type, K) || (epi == PF_SWIGLU && !w2) || ldo < N)
         return hipErrorInvalidValue;
-    PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, w2, out, M, N, K, ldo};
+    // the kernel addresses activations and weight rows with 32-bit byte offsets
+    if ((int64_t)M * K * 2 >= (int64_t)1 << 31 || (int64_t)N * byte_count(type, K) >= ((int64_t)1 << 31) - 65536)
+        return hipErrorInvalidValue;
+    PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, w2, out, M, N, K, ldo, 0};
     switch (type) {
     case GGML_Q4_K: return launch_gemm_fmt<GGML_Q4_K>(epi, a, s);
     case GGML_Q5_K: return launch_gemm_fmt<GGML_Q5_K>(epi, a, s);
