@@ -6,6 +6,8 @@ counter calibration run.
   python3 -m dotllm_amd.measure peak        # streaming read / write bandwidth
   python3 -m dotllm_amd.measure gemv        # isolated Q4_K / Q6_K GEMVs at the 7B shapes,
                                             # weights cycled through >= 396 MB of copies
+  python3 -m dotllm_amd.measure prefill-gemm   # batched Q4_K GEMM 2048 x 14336 x 4096 (MatMul
+                                               # with 2048 activation rows), 3 calls
 """
 from __future__ import annotations
 
@@ -91,6 +93,18 @@ def main(argv) -> int:
             for r in gemv_bench(be):
                 print(f"{r['type']} {r['rows']}x{r['cols']}: {r['us']:.2f} us/launch, {r['bytes'] / 1e6:.2f} MB, "
                       f"{r['gbps']:.0f} GB/s ({100 * r['gbps'] / 8000:.1f}% of 8 TB/s)")
+        elif cmd == "prefill-gemm":
+            import numpy as np
+            from . import Q4_K, synth
+            m, n, k = 2048, 14336, 4096
+            rng = np.random.default_rng(0)
+            w = synth.quantize(Q4_K, rng.normal(0, 0.02, size=(n, k)).astype(np.float32))
+            a = rng.normal(0, 1, size=(m, k)).astype(np.float32)
+            y = np.zeros(m * n, dtype=np.float32)
+            for _ in range(3):
+                be.mat_mul(a.reshape(-1), w, y, Q4_K, k, n, weight_key="measure.prefill_gemm")
+            be.release_weight("measure.prefill_gemm")
+            print(f"Q4_K GEMM {m}x{n}x{k}: 3 calls, {2.0 * m * n * k / 1e12:.3f} TFLOP each")
         elif cmd == "peak":
             for k, v in stream_peak_gbps(be).items():
                 print(f"stream {k}: {v:.0f} GB/s")
