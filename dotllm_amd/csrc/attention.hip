@@ -121,8 +121,7 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
         float s = 0.f;
 #pragma unroll
         for (int d = 0; d < DPT; d++) s += qv[d] * kv[d];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
+        s = sum4(s);
         const float score = s * inv_sqrt;
         if (live && sub == 0) a.scores[(int64_t)(kvh * G + h) * a.context + pos] = score;
         float m = live ? score : -INFINITY;
@@ -227,9 +226,7 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int d = 0; d < DPG; d++) {
-            float v = acc[d];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
+            const float v = xor32_add(xor16_add(acc[d]));
             if (lane < 16) red[wave][h * HD + dg * DPG + d] = v;
         }
     }

@@ -87,15 +87,77 @@ __device__ __forceinline__ void ld_realign(const uint8_t* p, uint32_t* out) {
     for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
 }
 
+// ---- lane exchanges without the LDS --------------------------------------
+// __shfl_xor compiles to ds_bpermute (an LDS round trip per step); these use
+// DPP (within 16-lane rows) and gfx950's row-swap permutes (across rows).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t lane_xor1(uint32_t x) { return dpp_u32<0xB1>(x); }   // quad_perm [1,0,3,2]
+__device__ __forceinline__ uint32_t lane_xor2(uint32_t x) { return dpp_u32<0x4E>(x); }   // quad_perm [2,3,0,1]
+// lane ^ 7 within 8 lanes (row_half_mirror) and lane ^ 15 within 16 (row_mirror):
+// once every lane of a quad (of 8 lanes) holds the same value, these act as
+// lane ^ 4 (lane ^ 8).
+__device__ __forceinline__ uint32_t lane_mirror8(uint32_t x) { return dpp_u32<0x141>(x); }
+__device__ __forceinline__ uint32_t lane_mirror16(uint32_t x) { return dpp_u32<0x140>(x); }
+// lane ^ 16 / lane ^ 32: the swap leaves each lane's own value in one result
+// and its partner's in the other.
+__device__ __forceinline__ uint32_t lane_xor16(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ float fx(uint32_t (*f)(uint32_t), float v) { return __uint_as_float(f(__float_as_uint(v))); }
+
+// Sums over each 4 / 8 consecutive lanes (every lane receives its group's sum).
+__device__ __forceinline__ float sum4(float v) {
+    v += fx(lane_xor1, v);
+    return v + fx(lane_xor2, v);
+}
+__device__ __forceinline__ float sum8(float v) {
+    v = sum4(v);
+    return v + fx(lane_mirror8, v);
+}
+__device__ __forceinline__ float sum16(float v) {
+    v = sum8(v);
+    return v + fx(lane_mirror16, v);
+}
+__device__ __forceinline__ float max16(float v) {
+    v = fmaxf(v, fx(lane_xor1, v));
+    v = fmaxf(v, fx(lane_xor2, v));
+    v = fmaxf(v, fx(lane_mirror8, v));
+    return fmaxf(v, fx(lane_mirror16, v));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v = sum16(v);
+    v += fx(lane_xor16, v);
+    return v + fx(lane_xor32, v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = max16(v);
+    v = fmaxf(v, fx(lane_xor16, v));
+    return fmaxf(v, fx(lane_xor32, v));
+}
+__device__ __forceinline__ float xor16_add(float v) { return v + fx(lane_xor16, v); }
+__device__ __forceinline__ float xor32_add(float v) { return v + fx(lane_xor32, v); }
+
+// (value, index) argmax over the wavefront: the larger value, or equal value
+// and smaller index (VectorMath.ArgMax keeps the first strict maximum; NaN
+// never wins).  Every lane receives the result.
+__device__ __forceinline__ void am_pick(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+    am_pick(v, i, fx(lane_xor1, v), (int)lane_xor1((uint32_t)i));
+    am_pick(v, i, fx(lane_xor2, v), (int)lane_xor2((uint32_t)i));
+    am_pick(v, i, fx(lane_mirror8, v), (int)lane_mirror8((uint32_t)i));
+    am_pick(v, i, fx(lane_mirror16, v), (int)lane_mirror16((uint32_t)i));
+    am_pick(v, i, fx(lane_xor16, v), (int)lane_xor16((uint32_t)i));
+    am_pick(v, i, fx(lane_xor32, v), (int)lane_xor32((uint32_t)i));
 }
 
 // NeoX rotation of element d of a head (TensorOps.ApplyRoPE, TO:679-743):

@@ -96,9 +96,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
     if (w) {   // uniform
         if (i < hidden) packed[i] = w[i] * h;
         float q = h * h;
-        q += __shfl_xor(q, 1, 64);
-        q += __shfl_xor(q, 2, 64);
-        q += __shfl_xor(q, 4, 64);
+        q = sum8(q);
         if ((i & 7) == 0 && i < hidden) ssq[i >> 3] = q;
     }
 }
@@ -110,9 +108,7 @@ __global__ __launch_bounds__(256) void pack_norm_kernel(const float* __restrict_
     const float h = i < n ? x[i] : 0.f;
     if (i < n) packed[i] = w[i] * h;   // RmsNorm's vector lanes compute (w * x) * inv
     float q = h * h;
-    q += __shfl_xor(q, 1, 64);
-    q += __shfl_xor(q, 2, 64);
-    q += __shfl_xor(q, 4, 64);
+    q = sum8(q);
     if ((i & 7) == 0 && i < n) ssq[i >> 3] = q;
 }
 

@@ -597,9 +597,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
                 a.pack_out[row] = a.pack_w[row] * hn;
             }
             float q = hn * hn;
-            q += __shfl_xor(q, 1, 64);
-            q += __shfl_xor(q, 2, 64);
-            q += __shfl_xor(q, 4, 64);
+            q = sum8(q);
             if (valid && (t & 7) == 0) a.pack_ssq[row >> 3] = q;
         }
     } else if (EPI == EPI_SWIGLU) {
@@ -615,12 +613,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         if (valid) seg.out[row] = y;
         float bv = y;
         int bi = valid ? row : 0x7FFFFFFF;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        wave_argmax(bv, bi);
         if (t == 0) {   // one candidate per workgroup; launch_argmax_finish reduces them
             a.am.cand_val[blockIdx.x] = bv;
             a.am.cand_idx[blockIdx.x] = bi;

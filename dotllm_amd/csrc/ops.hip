@@ -119,12 +119,6 @@ __global__ void scale_kernel(const float* in, float sc, float* out, int n) {
 
 constexpr int AM_PER_WG = 4096;
 
-// (v, i) beats (bv, bi): larger value, or equal value and smaller index
-// (VectorMath.ArgMax keeps the first strict maximum; NaN never wins).
-__device__ __forceinline__ void am_combine(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-}
-
 // VectorMath.ArgMax, VM:412-425, first pass: each workgroup reduces
 // AM_PER_WG elements to one candidate.
 __global__ __launch_bounds__(WG) void argmax_kernel(const float* x, int n, ArgmaxState st) {
@@ -136,11 +130,11 @@ __global__ __launch_bounds__(WG) void argmax_kernel(const float* x, int n, Argma
     const int beg = blockIdx.x * AM_PER_WG, end = min(n, beg + AM_PER_WG);
     for (int i = beg + threadIdx.x; i < end; i += WG)
         if (x[i] > v) { v = x[i]; idx = i; }   // ascending i per thread: first max wins
-    for (int o = 32; o >= 1; o >>= 1) am_combine(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    wave_argmax(v, idx);
     if (lane == 0) { sv[wave] = v; si[wave] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) am_combine(v, idx, sv[w], si[w]);
+        for (int w = 1; w < 4; w++) am_pick(v, idx, sv[w], si[w]);
         st.cand_val[blockIdx.x] = v;
         st.cand_idx[blockIdx.x] = idx;
     }
@@ -155,12 +149,12 @@ __global__ __launch_bounds__(WG) void argmax_finish_kernel(ArgmaxState st, int n
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int c = threadIdx.x; c < ncand; c += WG) am_combine(v, idx, st.cand_val[c], st.cand_idx[c]);
-    for (int o = 32; o >= 1; o >>= 1) am_combine(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    for (int c = threadIdx.x; c < ncand; c += WG) am_pick(v, idx, st.cand_val[c], st.cand_idx[c]);
+    wave_argmax(v, idx);
     if (lane == 0) { sv[wave] = v; si[wave] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) am_combine(v, idx, sv[w], si[w]);
+        for (int w = 1; w < 4; w++) am_pick(v, idx, sv[w], si[w]);
         if (idx == 0x7FFFFFFF) idx = 0;   // all NaN: ArgMax returns 0
         *st.token_out = idx;
         if (st.step) {

@@ -120,9 +120,7 @@ __global__ __launch_bounds__(WG) void pf_planes_kernel(const float* __restrict__
             y[j] = ok ? yval(base + j) : 0.f;
             g += y[j];
         }
-        g += __shfl_xor(g, 1, 64);
-        g += __shfl_xor(g, 2, 64);
-        g += __shfl_xor(g, 4, 64);
+        g = sum8(g);
         if (ok) {
             h4 hv, lv;
 #pragma unroll
@@ -684,10 +682,7 @@ __global__ __launch_bounds__(WG) void pf_attn_scores_kernel(PfAttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         float m = rmax[i];
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        m = fmaxf(m, __shfl_xor(m, 8, 64));
+        m = max16(m);
         const int t = t0 + 4 * tq + i;
         if (tk == 0 && t < a.T) a.rowmax[(int64_t)h * a.T + t] = m;
     }
@@ -751,10 +746,7 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_kernel(PfAttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         float zz = z[i];
-        zz += __shfl_xor(zz, 1, 64);
-        zz += __shfl_xor(zz, 2, 64);
-        zz += __shfl_xor(zz, 4, 64);
-        zz += __shfl_xor(zz, 8, 64);
+        zz = sum16(zz);
         const int t = t0 + 4 * tq + i;
         if (t < a.T) {
             const float inv = 1.0f / zz;
@@ -796,8 +788,8 @@ __global__ __launch_bounds__(WG) void pf_attn_scores_mfma(PfAttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(qv[ks][i]));
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = fmaxf(amax, fx(lane_xor16, amax));
+    amax = fmaxf(amax, fx(lane_xor32, amax));
     int e = 0;
     if (amax > 0.f) {
         (void)frexpf(amax, &e);
@@ -857,10 +849,7 @@ __global__ __launch_bounds__(WG) void pf_attn_scores_mfma(PfAttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         float m = rmax[r];
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        m = fmaxf(m, __shfl_xor(m, 8, 64));
+        m = max16(m);
         const int t = t0 + 16 * wave + 4 * lk + r;
         if (lr == 0 && t < a.T) a.rowmax[(int64_t)h * a.T + t] = m;
     }
@@ -926,8 +915,7 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
             }
         }
     }
-    z += __shfl_xor(z, 16, 64);
-    z += __shfl_xor(z, 32, 64);   // lanes lr, lr+16, ... hold query lr's sum
+    z = xor32_add(xor16_add(z));   // lanes lr, lr+16, ... hold query lr's sum
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int ql = 4 * lk + r;
