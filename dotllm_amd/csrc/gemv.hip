@@ -4,7 +4,8 @@
 // src/Llmdot.Core/Tensors/TensorOps.cs:60-90, fused per-type kernels TO:118-431).
 // The weight blocks are read once from HBM in their GGUF layout.
 //
-// Decomposition.  A workgroup owns a few consecutive output rows and the whole
+// Decomposition.  A workgroup owns a few output rows (slabs of 2 to 8
+// consecutive rows, interleaved across the workgroups) and the whole
 // reduction dimension.  It has ceil(U/64) wavefronts, U being the number of
 // 32-element "units" of a row, and lane L of wavefront w owns unit 64w + L in
 // every row, so a lane's activations are loaded once and stay in registers
@@ -159,22 +160,17 @@ struct XF {
 // ---- per-type row units -----------------------------------------------------------
 // RUN: contiguous elements per run of a unit; xoff(u, run) its first element.
 
-struct __attribute__((aligned(4))) u32x2 { uint32_t x, y; };
-
 struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
     // 4 rows per batch keep the kernel near 100 VGPRs (4 wavefronts per SIMD)
     static constexpr int RB = 4, NS = 1, PRE = 2, DEPTH = 2;
-    // dd: d | dmin << 16; f: the two header words holding sub-block g's
-    // 12-bit (sc, m) field, which starts at bit 32 + 12 g of the block (the
-    // 6-bit stream begins at byte 4, LSB first), i.e. at bit (12 g) mod 32 of
-    // word 1 + 12 g / 32; q: the sub-block's 16 nibble bytes.
-    struct Raw { uint32_t dd; u32x2 f; u32x4 q; };
+    // h: the 16-byte block header (d | dmin << 16, then the 96-bit 6-bit
+    // (sc, m) stream), one load shared by the block's 8 lanes; q: the
+    // sub-block's 16 nibble bytes.
+    struct Raw { u32x4 h; u32x4 q; };
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
         const uint8_t* blk = row + (u >> 3) * 144;
-        const int g = u & 7;
-        r.dd = ld4_a4(blk);
-        r.f = *reinterpret_cast<const u32x2*>(blk + 4 + 4 * ((12 * g) >> 5));
-        r.q = ld16_a4(blk + 16 + 16 * g);
+        r.h = ld16_a4(blk);
+        r.q = ld16_a4(blk + 16 + 16 * (u & 7));
     }
     __device__ static float dot(const Raw& r, int u, const XQ& x) {
         const uint32_t w[4] = {r.q.x ^ 0x88888888u, r.q.y ^ 0x88888888u, r.q.z ^ 0x88888888u, r.q.w ^ 0x88888888u};
@@ -189,9 +185,9 @@ struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
             for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_sdot8((int)w[j], (int)x.pl[4 * p + j], acc, false);
         }
         const float S = (float)acc;
-        const uint32_t fld = __builtin_amdgcn_alignbit(r.f.y, r.f.x, (uint32_t)((12 * (u & 7)) & 31));
-        const float sc = (float)(fld & 63u), m = (float)((fld >> 6) & 63u);
-        const float d = h16(r.dd & 0xFFFFu), dm = h16(r.dd >> 16);
+        float sc, m;
+        kscale(r.h.y, r.h.z, r.h.w, u & 7, sc, m);
+        const float d = h16(r.h.x & 0xFFFFu), dm = h16(r.h.x >> 16);
         return (d * sc) * (x.s * S) - (dm * m) * x.sum;
     }
 };
@@ -523,7 +519,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         blk -= a.seg[si].wgs;
     }
     const GemvSeg seg = a.seg[si];
-    const int row0 = blk * ROWS_WG;
+    // Output rows in slabs of SLAB: slab j of this workgroup is rows
+    // (j * wgs + blk) * SLAB ..., so at any moment the workgroups of a
+    // segment stream through one contiguous stretch of each matrix.  The ADD
+    // epilogue packs rows in aligned 8s.
+    constexpr int SLAB = EPI == EPI_ADD ? (ROWS_WG % 8 == 0 ? 8 : ROWS_WG) : OPB;
+    auto out_row = [&](int o) { return ((o / SLAB) * seg.wgs + blk) * SLAB + o % SLAB; };
     const int K = a.cols;
     const int u = wave * 64 + lane;
     const bool has = u < K / 32;
@@ -537,10 +538,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         const uint8_t* base = seg.w;
         int r;
         if (SW) {
-            r = row0 + b * OPB + (k % OPB);
+            r = out_row(b * OPB + (k % OPB));
             if (k >= OPB) base = seg.w2;
         } else {
-            r = row0 + i;
+            r = out_row(i);
         }
         return base + (int64_t)(r < seg.rows ? r : 0) * rbytes;
     };
@@ -552,6 +553,16 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         const int nq = K >> 3;
 #pragma unroll
         for (int k = 0; k < 4; k++) sq[k] = a.ssq[min((int)threadIdx.x + k * (int)blockDim.x, nq - 1)];
+    }
+    // ADD: the residual and norm weight of this lane's output row, loaded
+    // before the rows so the epilogue does not wait on them
+    float res = 0.f, pw = 0.f;
+    if (EPI == EPI_ADD && threadIdx.x < ROWS_WG) {
+        const int r = out_row(threadIdx.x);
+        if (r < seg.rows) {
+            res = seg.out[r];
+            if (a.pack_out) pw = a.pack_w[r];
+        }
     }
     if (T2 != T && second) gemv_rows<TT2, NB>(a, uu, has, row_ptr, red[wave]);
     else gemv_rows<TT, NB>(a, uu, has, row_ptr, red[wave]);
@@ -566,7 +577,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     __syncthreads();
     if (threadIdx.x >= 64) return;
 
-    // epilogue (wavefront 0): lane t < ROWS_WG owns output row row0 + t
+    // epilogue (wavefront 0): lane t < ROWS_WG owns output row out_row(t)
     const int t = threadIdx.x;
     float inv = 1.f;
     if (NORM) {
@@ -580,7 +591,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         for (int w = 0; w < nw; w++) s += (red[w][i][0] + red[w][i][1]) + (red[w][i][2] + red[w][i][3]);
         return s * inv;
     };
-    const int row = row0 + t;
+    const int row = out_row(t);
     const bool valid = t < ROWS_WG && row < seg.rows;
     const int b = t / OPB, k = t % OPB;
     if (EPI == EPI_STORE) {
@@ -588,13 +599,13 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     } else if (EPI == EPI_ADD) {
         float hn = 0.f;
         if (valid) {
-            hn = seg.out[row] + total(b * RB + k);   // residual: a[i] + b[i]
+            hn = res + total(b * RB + k);   // residual: a[i] + b[i]
             seg.out[row] = hn;
         }
         if (a.pack_out) {   // the updated vector packed for its RmsNorm consumer (rows come in 8s)
             if (valid) {
 #pragma clang fp contract(off)
-                a.pack_out[row] = a.pack_w[row] * hn;
+                a.pack_out[row] = pw * hn;
             }
             float q = hn * hn;
             q = sum8(q);
@@ -656,6 +667,7 @@ hipError_t launch_te(const GemvArgs& a, int nb, int grid, int threads, hipStream
     case 2: gemv_kernel<T, EPI, 2, NORM><<<grid, threads, 0, s>>>(a); break;
     case 4: gemv_kernel<T, EPI, 4, NORM><<<grid, threads, 0, s>>>(a); break;
     case 8: gemv_kernel<T, EPI, 8, NORM><<<grid, threads, 0, s>>>(a); break;
+    case 7: gemv_kernel<T, EPI, 7, NORM><<<grid, threads, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -707,6 +719,9 @@ int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
     const int nw = (cols / 32 + 63) / 64;
     const int opb = epi == EPI_SWIGLU ? type_rb(type) / 2 : type_rb(type);
     // the most rows per workgroup that still gives the target wavefront count
+    // SwiGLU: 7 batches when that gives a whole number of workgroups per CU
+    // (14336 rows: 1024 workgroups, 4 per CU, instead of 896)
+    if (epi == EPI_SWIGLU && rows_total % (7 * opb) == 0 && (rows_total / (7 * opb)) % 256 == 0) return 7;
     int nb = 8;
     while (nb > 1 && ((rows_total + nb * opb - 1) / (nb * opb)) * nw < target_waves()) nb /= 2;
     // the ADD epilogue packs rows in groups of 8
