@@ -497,7 +497,8 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, R
 
 // ---- the kernel -------------------------------------------------------------------
 // NB batches of RB dot rows; SwiGLU batches hold RB/2 gate then RB/2 up rows.
-template <uint32_t T, int EPI, int NB, bool NORM, uint32_t T2 = T>
+// Segments of the second type T2 take NB2 <= NB batches per workgroup.
+template <uint32_t T, int EPI, int NB, bool NORM, uint32_t T2 = T, int NB2 = NB>
 __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     using TT = typename TypeOf<T>::type;
     using TT2 = typename TypeOf<T2>::type;
@@ -530,6 +531,8 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     const bool has = u < K / 32;
     const int uu = has ? u : 0;
     const bool second = T2 != T && seg.type == T2;   // uniform per workgroup
+    static_assert(NB2 <= NB, "second-type segments take at most NB batches");
+    const int rows_wg = second ? NB2 * OPB : ROWS_WG;
     const int64_t rbytes = second ? (int64_t)(K / block_elems(T2)) * block_bytes(T2)
                                   : (int64_t)(K / block_elems(T)) * block_bytes(T);
 
@@ -557,14 +560,14 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     // ADD: the residual and norm weight of this lane's output row, loaded
     // before the rows so the epilogue does not wait on them
     float res = 0.f, pw = 0.f;
-    if (EPI == EPI_ADD && threadIdx.x < ROWS_WG) {
+    if (EPI == EPI_ADD && (int)threadIdx.x < rows_wg) {
         const int r = out_row(threadIdx.x);
         if (r < seg.rows) {
             res = seg.out[r];
             if (a.pack_out) pw = a.pack_w[r];
         }
     }
-    if (T2 != T && second) gemv_rows<TT2, NB>(a, uu, has, row_ptr, red[wave]);
+    if (T2 != T && second) gemv_rows<TT2, NB2>(a, uu, has, row_ptr, red[wave]);
     else gemv_rows<TT, NB>(a, uu, has, row_ptr, red[wave]);
     if (NORM) {
         const int nq = K >> 3;
@@ -577,7 +580,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     __syncthreads();
     if (threadIdx.x >= 64) return;
 
-    // epilogue (wavefront 0): lane t < ROWS_WG owns output row out_row(t)
+    // epilogue (wavefront 0): lane t < rows_wg owns output row out_row(t)
     const int t = threadIdx.x;
     float inv = 1.f;
     if (NORM) {
@@ -592,7 +595,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         return s * inv;
     };
     const int row = out_row(t);
-    const bool valid = t < ROWS_WG && row < seg.rows;
+    const bool valid = t < rows_wg && row < seg.rows;
     const int b = t / OPB, k = t % OPB;
     if (EPI == EPI_STORE) {
         if (valid) seg.out[row] = total(b * RB + k);
@@ -776,9 +779,14 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     }
     const int nb = gemv_plan(type, epi, rows_total, a.cols);
     const int rwg = gemv_rows_per_wg(type, epi, nb);
+    // Q6_K segments of a mixed launch: half the batches per workgroup (a Q6_K
+    // row costs about twice a Q4_K row), so their workgroups end with the rest
+    const int nb2 = nb > 1 ? nb / 2 : 1;
+    const int rwg2 = gemv_rows_per_wg(t2, epi, nb2);
     int grid = 0;
     for (int i = 0; i < a.nseg; i++) {
-        a.seg[i].wgs = (a.seg[i].rows + rwg - 1) / rwg;
+        const int r = (t2 != type && a.seg[i].type == t2) ? rwg2 : rwg;
+        a.seg[i].wgs = (a.seg[i].rows + r - 1) / r;
         grid += a.seg[i].wgs;
     }
     if (grid <= 0) return hipSuccess;
@@ -787,10 +795,10 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     hipError_t e;
     if (t2 != type) {   // Q4_K with Q6_K segments (Q/K/V of the Q4_K_M mix)
         switch (nb) {
-        case 1: gemv_kernel<GGML_Q4_K, EPI_STORE, 1, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
-        case 2: gemv_kernel<GGML_Q4_K, EPI_STORE, 2, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
-        case 4: gemv_kernel<GGML_Q4_K, EPI_STORE, 4, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
-        case 8: gemv_kernel<GGML_Q4_K, EPI_STORE, 8, true, GGML_Q6_K><<<grid, threads, 0, s>>>(a); break;
+        case 1: gemv_kernel<GGML_Q4_K, EPI_STORE, 1, true, GGML_Q6_K, 1><<<grid, threads, 0, s>>>(a); break;
+        case 2: gemv_kernel<GGML_Q4_K, EPI_STORE, 2, true, GGML_Q6_K, 1><<<grid, threads, 0, s>>>(a); break;
+        case 4: gemv_kernel<GGML_Q4_K, EPI_STORE, 4, true, GGML_Q6_K, 2><<<grid, threads, 0, s>>>(a); break;
+        case 8: gemv_kernel<GGML_Q4_K, EPI_STORE, 8, true, GGML_Q6_K, 4><<<grid, threads, 0, s>>>(a); break;
         default: return hipErrorInvalidValue;
         }
         return hipGetLastError();
