@@ -61,6 +61,12 @@ class DeviceInfo(C.Structure):
                 ("clock_mhz", C.c_int32), ("hbm_bytes", C.c_uint64)]
 
 
+class Sampling(C.Structure):
+    """llmdot_hip_sampling: SamplingOptions (SamplingOptions.cs:7-15) without the seed."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("repeat_window", C.c_int32)]
+
+
 class StepTiming(C.Structure):
     _fields_ = [("total_ms", C.c_float), ("gemv_ms", C.c_float), ("gemv_launches", C.c_int32),
                 ("gemv_bytes", C.c_double)]
@@ -97,6 +103,7 @@ SIGNATURES = {
     "llmdot_hip_mul": [_P, _P, _P, _P, _I32],
     "llmdot_hip_dequantize": [_P, _P, _P, _U32, _I32, _I32],
     "llmdot_hip_argmax": [_P, _P, _I32, _PI32],
+    "llmdot_hip_sample": [_P, _P, _I32, C.POINTER(Sampling), _PI32, _I32, _F, _PI32],
     "llmdot_hip_device_alloc": [_P, C.c_size_t, _PP],
     "llmdot_hip_device_free": [_P, _P],
     "llmdot_hip_memcpy_h2d": [_P, _P, _P, C.c_size_t],
@@ -111,6 +118,8 @@ SIGNATURES = {
     "llmdot_hip_decode_step": [_P, _I32, _I32, _P, _PI32],
     "llmdot_hip_prefill": [_P, _PI32, _I32, _I32, _P, _PI32],
     "llmdot_hip_generate": [_P, _PI32, _I32, _I32, _I32, _PI32, _PI32, _P],
+    "llmdot_hip_generate_sampled": [_P, _PI32, _I32, _I32, _I32, C.POINTER(Sampling), C.POINTER(C.c_float), _PI32,
+                                    _PI32, _P],
     "llmdot_hip_kv_read": [_P, _I32, _I32, _P, _P],
     "llmdot_hip_model_time_decode": [_P, _I32, _I32, _I32, _I32, C.POINTER(StepTiming)],
     "llmdot_hip_model_time_prefill": [_P, _PI32, _I32, _I32, C.POINTER(C.c_float)],

@@ -49,6 +49,13 @@ def device_count() -> int:
     return n.value if rc == 0 else 0
 
 
+def sampling_struct(options) -> "_lib.Sampling":
+    """SamplingOptions fields as the C struct."""
+    from ._lib import Sampling
+    return Sampling(float(options.temperature), int(options.top_k), float(options.top_p),
+                    float(options.repeat_penalty), int(options.repeat_penalty_window_size))
+
+
 class HipBackend:
     """IComputeBackend over one MI355X device (context + stream + weight cache)."""
 
@@ -182,6 +189,20 @@ class HipBackend:
         idx = C.c_int32(0)
         _call(lib().llmdot_hip_argmax(self._ctx, ptr(inp), inp.size, C.byref(idx)))
         return idx.value
+
+    def sample(self, logits, options, recent_tokens, r: float) -> int:
+        """Sampler.Sample (Sampler.cs:24-62) on the device.  options: an object
+        with temperature, top_k, top_p, repeat_penalty and
+        repeat_penalty_window_size (SamplingOptions); recent_tokens: the
+        recent-token list; r: the uniform draw (Random.NextSingle())."""
+        x = _f32(logits, "logits")
+        rec = np.ascontiguousarray(np.asarray(list(recent_tokens) or [0], dtype=np.int32))
+        opt = sampling_struct(options)
+        tok = C.c_int32(0)
+        _call(lib().llmdot_hip_sample(self._ctx, ptr(x), x.size, C.byref(opt),
+                                      rec.ctypes.data_as(C.POINTER(C.c_int32)), len(recent_tokens), float(r),
+                                      C.byref(tok)))
+        return tok.value
 
     # Members off the LLaMA decode path (ICB:12, 18, 19, 25, 26).
     def layer_norm(self, *args, **kw):

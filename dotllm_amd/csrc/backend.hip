@@ -476,6 +476,31 @@ extern "C" int32_t llmdot_hip_argmax(llmdot_hip_ctx* ctx, const float* input, in
     return copy_out(ctx, index, ctx->am_ints, sizeof(int32_t));
 }
 
+extern "C" int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, int32_t n, const llmdot_hip_sampling* opt,
+                                     const int32_t* recent, int32_t n_recent, float r, int32_t* token) {
+    if (!ctx || !logits || !opt || !token || n <= 0 || n_recent < 0 || (n_recent > 0 && !recent))
+        return fail(LLMDOT_E_INVALID, "bad Sample arguments");
+    if (opt->temperature <= 0.f) return llmdot_hip_argmax(ctx, logits, n, token);   // Sampler.cs:26-27
+    if (!sample_supported(n, opt->top_k))
+        return fail(LLMDOT_E_UNSUPPORTED, "TopK between " + std::to_string(SAMPLE_MAX_K) + " and the vocabulary size is not supported");
+    if (int rc = ensure_device(ctx)) return rc;
+    if (int rc = ensure_argmax(ctx, 1)) return rc;
+    float *dl, *dr;
+    int32_t* dh;
+    if (int rc = stage_in(ctx, 0, logits, (size_t)n, &dl)) return rc;
+    HIPCHK(ctx->scratch[1].ensure(sizeof(float) * (size_t)n));
+    if (int rc = stage_in(ctx, 2, recent, (size_t)n_recent, &dh)) return rc;
+    if (int rc = stage_in(ctx, 3, &r, 1, &dr)) return rc;
+    HIPCHK(launch_set_scalar(ctx->am_ints + 1, 1, ctx->stream));   // draw 0
+    SampleArgs sa{};
+    sa.logits = dl; sa.n = n; sa.inv_temp = 1.0f / opt->temperature;
+    sa.top_k = opt->top_k; sa.top_p = opt->top_p; sa.penalty = opt->repeat_penalty; sa.window = opt->repeat_window;
+    sa.hist = dh; sa.hist_base = n_recent; sa.step = ctx->am_ints + 1; sa.rvals = dr;
+    sa.work = (float*)ctx->scratch[1].p; sa.token_out = ctx->am_ints;
+    HIPCHK(launch_sample(sa, ctx->stream));
+    return copy_out(ctx, token, ctx->am_ints, sizeof(int32_t));
+}
+
 // ========================================================= device pointers ==
 
 extern "C" int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, void** dptr) {
@@ -614,6 +639,11 @@ struct llmdot_hip_model {
           *pf_act = nullptr, *pf_scores = nullptr, *pf_rowmax = nullptr;
     PfPlanes pf_planes{};
     int32_t* pf_tokens = nullptr;
+    // sampled generation (allocated on first use): recent-token history
+    // [context + 1], uniform draws [context + 1], sampler scratch [vocab]
+    int32_t* s_hist = nullptr;
+    float* s_draws = nullptr;
+    float* s_work = nullptr;
 };
 
 namespace {
@@ -1096,12 +1126,32 @@ extern "C" int32_t llmdot_hip_prefill(llmdot_hip_model* m, const int32_t* tokens
     return fetch_outputs(m, logits, am);
 }
 
-extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
-                                       int32_t eos, int32_t* tokens_out, int32_t* n_out, float* logits_out) {
+namespace {
+
+// Draw the token from the logits the head just wrote (after its argmax pass
+// advanced the step), replacing the argmax in the token slot and log.
+int enqueue_sample(llmdot_hip_model* m, const llmdot_hip_sampling* opt, int hist_base) {
+    SampleArgs sa{};
+    sa.logits = m->logits; sa.n = m->d.vocab; sa.inv_temp = 1.0f / opt->temperature;
+    sa.top_k = opt->top_k; sa.top_p = opt->top_p; sa.penalty = opt->repeat_penalty; sa.window = opt->repeat_window;
+    sa.hist = m->s_hist; sa.hist_base = hist_base; sa.step = m_step(m); sa.rvals = m->s_draws;
+    sa.work = m->s_work; sa.token_out = m_token(m);
+    sa.token_log = m->token_log; sa.log_cap = m->d.context + 1; sa.hist_out = m->s_hist;
+    HIPCHK(launch_sample(sa, m->ctx->stream));
+    return 0;
+}
+
+int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens, int32_t eos,
+                  const llmdot_hip_sampling* opt, const float* draws, int32_t* tokens_out, int32_t* n_out,
+                  float* logits_out) {
     if (!m || (!prompt && n_prompt > 0) || n_prompt < 0 || max_tokens < 0 || (!tokens_out && max_tokens > 0) || !n_out)
         return fail(LLMDOT_E_INVALID, "bad Generate arguments");
     *n_out = 0;
     const auto& d = m->d;
+    const bool sampled = opt && opt->temperature > 0.f;   // Sampler.cs:26-27: greedy otherwise
+    if (sampled && !draws && max_tokens > 0) return fail(LLMDOT_E_INVALID, "sampled Generate needs the uniform draws");
+    if (sampled && !sample_supported(d.vocab, opt->top_k))
+        return fail(LLMDOT_E_UNSUPPORTED, "TopK between " + std::to_string(SAMPLE_MAX_K) + " and the vocabulary size is not supported");
     std::vector<int32_t> pr(prompt, prompt + n_prompt);
     if (pr.empty()) pr.push_back(d.bos > 0 ? d.bos : 0);   // IE:90-95
     const int np = (int)pr.size();
@@ -1114,6 +1164,19 @@ extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* promp
     const int fit = d.context - np + 1;
     const int produce = max_tokens < fit ? max_tokens : fit;
     hipStream_t s = m->ctx->stream;
+    if (sampled) {
+        // recentTokens starts as the prompt (IE:101); draws on the device
+        if (!m->s_hist) {
+            void *h, *r, *w;
+            if (int rc = dalloc(m, sizeof(int32_t) * (size_t)(d.context + 1), &h)) return rc;
+            if (int rc = dalloc(m, sizeof(float) * (size_t)(d.context + 1), &r)) return rc;
+            if (int rc = dalloc(m, sizeof(float) * (size_t)d.vocab, &w)) return rc;
+            m->s_hist = (int32_t*)h; m->s_draws = (float*)r; m->s_work = (float*)w;
+        }
+        if (n_prompt > 0)
+            HIPCHK(hipMemcpyAsync(m->s_hist, prompt, sizeof(int32_t) * (size_t)n_prompt, hipMemcpyHostToDevice, s));
+        HIPCHK(hipMemcpyAsync(m->s_draws, draws, sizeof(float) * (size_t)produce, hipMemcpyHostToDevice, s));
+    }
     if (use_batched_prefill(m, np)) {
         if (int rc = prefill_batched(m, pr.data(), np, 0, true)) return rc;   // KvCache.Reset (IE:79) + prompt
     } else {
@@ -1125,9 +1188,13 @@ extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* promp
             if (int rc = run_step(m)) return rc;
         }
     }
+    if (sampled)
+        if (int rc = enqueue_sample(m, opt, n_prompt)) return rc;
     if (logits_out) HIPCHK(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
     for (int g = 1; g < produce; g++) {
         if (int rc = run_step(m)) return rc;   // consumes the token the previous head wrote
+        if (sampled)
+            if (int rc = enqueue_sample(m, opt, n_prompt)) return rc;
         if (logits_out)
             HIPCHK(hipMemcpyAsync(logits_out + (size_t)g * d.vocab, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
     }
@@ -1141,6 +1208,21 @@ extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* promp
     if (produce < max_tokens && n == produce)
         return fail(LLMDOT_E_RANGE, "generation reached the end of the KV cache");
     return 0;
+}
+
+}  // namespace
+
+extern "C" int32_t llmdot_hip_generate(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
+                                       int32_t eos, int32_t* tokens_out, int32_t* n_out, float* logits_out) {
+    return generate_impl(m, prompt, n_prompt, max_tokens, eos, nullptr, nullptr, tokens_out, n_out, logits_out);
+}
+
+extern "C" int32_t llmdot_hip_generate_sampled(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt,
+                                               int32_t max_tokens, int32_t eos, const llmdot_hip_sampling* opt,
+                                               const float* draws, int32_t* tokens_out, int32_t* n_out,
+                                               float* logits_out) {
+    if (!opt) return fail(LLMDOT_E_INVALID, "null sampling options");
+    return generate_impl(m, prompt, n_prompt, max_tokens, eos, opt, draws, tokens_out, n_out, logits_out);
 }
 
 extern "C" int32_t llmdot_hip_kv_read(llmdot_hip_model* m, int32_t layer, int32_t position, float* k, float* v) {

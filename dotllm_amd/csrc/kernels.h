@@ -110,6 +110,29 @@ int attn_max_chunks(int heads, int kv_heads, int context);
 bool attn_supported(int heads, int kv_heads, int head_dim);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
+// ---- sample.hip (Sampler.Sample on the device) ----
+constexpr int SAMPLE_MAX_K = 4096;   // largest top-k handled (TopK >= n takes the top-p path)
+struct SampleArgs {
+    const float* logits;      // [n]
+    int n;
+    float inv_temp;           // 1f / Temperature (> 0)
+    int top_k;                // 0 < top_k < n: top-k path
+    float top_p;              // < 1: nucleus (top-p path only)
+    float penalty;            // RepeatPenalty
+    int window;               // RepeatPenaltyWindowSize
+    const int32_t* hist;      // tokens so far; the draw sees hist[0, hist_base + *step - 1)
+    int hist_base;
+    const int32_t* step;      // this is draw *step - 1 (the argmax pass has advanced it)
+    const float* rvals;       // uniform draws: draw s uses rvals[s]
+    float* work;              // [n] scratch
+    int32_t* token_out;       // the sampled token
+    int32_t* token_log;       // optional: token_log[draw] = token while draw < log_cap
+    int32_t log_cap;
+    int32_t* hist_out;        // optional: hist_out[hist_base + draw] = token
+};
+bool sample_supported(int n, int top_k);
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
+
 // ---- prefill.hip (batched prompt processing) ----
 // Activation planes of a [M][K] fp32 matrix: xh/xl [M][K] fp16 (x s = xh + xl,
 // s a power of two per row), sh/sl [M][K/32] fp16 (group sums of x times s/32),

@@ -163,13 +163,24 @@ class InferenceEngine:
 
     # -- Generate ------------------------------------------------------------
     def generate(self, prompt_tokens, options: GenerationOptions | None = None):
-        """InferenceEngine.Generate: yields sampled token ids (greedy only)."""
+        """InferenceEngine.Generate (IE:74-132): yields the token ids."""
         tokens, _ = self.generate_all(prompt_tokens, options or GenerationOptions())
         yield from tokens
 
-    def generate_all(self, prompt_tokens, options: GenerationOptions, return_logits: bool = False):
-        if options.sampling.temperature > 0:
-            raise NotImplementedError("only greedy decoding (Temperature <= 0) runs on the device")
+    @staticmethod
+    def draws_for(sampling: SamplingOptions, n: int) -> np.ndarray:
+        """Uniform draws for n tokens.  The reference builds new Random(Seed) for
+        every draw when Seed >= 0 (Sampler.cs:160), so every token uses the same
+        value; this host uses numpy's generator for that value (System.Random's
+        sequence is not reproduced: a C# caller passes its own NextSingle())."""
+        if sampling.seed >= 0:
+            r = np.random.default_rng(sampling.seed).random(dtype=np.float32)
+            return np.full(max(n, 1), r, dtype=np.float32)
+        return np.random.default_rng().random(max(n, 1), dtype=np.float32)
+
+    def generate_all(self, prompt_tokens, options: GenerationOptions, return_logits: bool = False, draws=None):
+        """Greedy when Temperature <= 0 (Sampler.cs:26-27), else the device sampler
+        with the given uniform draws (draws_for(options.sampling) by default)."""
         if options.stop_sequences:
             raise NotImplementedError("stop sequences need the tokenizer")
         prompt = np.ascontiguousarray(np.asarray(prompt_tokens, dtype=np.int32))
@@ -177,10 +188,22 @@ class InferenceEngine:
         out = np.zeros(max(n, 1), dtype=np.int32)
         logits = np.zeros((max(n, 1), self.vocab), dtype=np.float32) if return_logits else None
         n_out = C.c_int32(0)
-        rc = lib().llmdot_hip_generate(self._m, prompt.ctypes.data_as(C.POINTER(C.c_int32)), prompt.size, n,
-                                       int(self.model.config.eos_token_id),
-                                       out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(n_out),
-                                       _lib.ptr(logits) if logits is not None else None)
+        pp = prompt.ctypes.data_as(C.POINTER(C.c_int32))
+        eos = int(self.model.config.eos_token_id)
+        lp = _lib.ptr(logits) if logits is not None else None
+        if options.sampling.temperature > 0:
+            from .backend import sampling_struct
+            d = np.ascontiguousarray(draws if draws is not None else self.draws_for(options.sampling, n),
+                                     dtype=np.float32)
+            if d.size < n:
+                raise ValueError("one uniform draw per generated token is needed")
+            opt = sampling_struct(options.sampling)
+            rc = lib().llmdot_hip_generate_sampled(self._m, pp, prompt.size, n, eos, C.byref(opt),
+                                                   d.ctypes.data_as(C.POINTER(C.c_float)),
+                                                   out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(n_out), lp)
+        else:
+            rc = lib().llmdot_hip_generate(self._m, pp, prompt.size, n, eos,
+                                           out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(n_out), lp)
         k = n_out.value
         if rc == _lib.E_RANGE and k > 0:
             return out[:k].tolist(), (logits[:k] if logits is not None else None)

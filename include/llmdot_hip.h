@@ -112,6 +112,25 @@ int32_t llmdot_hip_dequantize(llmdot_hip_ctx* ctx, const void* src, float* dst, 
 /* ICB:28 ArgMax(input): first index of the strict maximum. */
 int32_t llmdot_hip_argmax(llmdot_hip_ctx* ctx, const float* input, int32_t n, int32_t* index);
 
+/* SamplingOptions (src/Llmdot.Core/Sampling/SamplingOptions.cs:7-15) without
+ * the seed: the caller draws the uniform values (Random.NextSingle()). */
+typedef struct llmdot_hip_sampling {
+    float temperature;       /* <= 0: greedy ArgMax */
+    int32_t top_k;           /* 0 < top_k < n: top-k path (top_k <= 4096) */
+    float top_p;             /* < 1: nucleus, when the top-k path is not taken */
+    float repeat_penalty;
+    int32_t repeat_window;   /* RepeatPenaltyWindowSize */
+} llmdot_hip_sampling;
+/* Sampler.Sample(logits, options, ..., recentTokens) (Sampler.cs:24-62) on the
+ * device.  recent: the recent-token list (the last repeat_window entries are
+ * penalised); r: the uniform draw SampleFromProbabilities makes
+ * (Sampler.cs:160-161).  The top-k path reproduces the reference's arithmetic
+ * (ties between equal values go to the smaller index); the top-p path matches
+ * it except where r or top_p falls within float rounding of a cumulative
+ * boundary.  LLMDOT_E_UNSUPPORTED for 4096 < top_k < n. */
+int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, int32_t n, const llmdot_hip_sampling* opt,
+                          const int32_t* recent, int32_t n_recent, float r, int32_t* token);
+
 /* ---- device-pointer variants (inputs already resident in HBM; used by
  *      harnesses that time kernels without PCIe traffic). ------------------- */
 int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, void** dptr);
@@ -184,6 +203,15 @@ int32_t llmdot_hip_prefill(llmdot_hip_model* model, const int32_t* tokens, int32
 int32_t llmdot_hip_generate(llmdot_hip_model* model, const int32_t* prompt, int32_t n_prompt,
                             int32_t max_tokens, int32_t eos, int32_t* tokens_out, int32_t* n_out,
                             float* logits_out);
+/* Generate with SamplingOptions (IE:100-130, Sampler.cs:24-170): as
+ * llmdot_hip_generate, each token drawn on the device by llmdot_hip_sample's
+ * kernels from the logits in HBM, with the recent-token list kept on the device
+ * (the prompt, then the generated tokens).  draws[i] is the uniform value token
+ * i uses (max_tokens entries; for a seeded reference run, new
+ * Random(seed).NextSingle() for every i). */
+int32_t llmdot_hip_generate_sampled(llmdot_hip_model* model, const int32_t* prompt, int32_t n_prompt,
+                                    int32_t max_tokens, int32_t eos, const llmdot_hip_sampling* opt,
+                                    const float* draws, int32_t* tokens_out, int32_t* n_out, float* logits_out);
 /* Reads KV slot (layer, position) as fp32, kv_heads*head_dim floats each. */
 int32_t llmdot_hip_kv_read(llmdot_hip_model* model, int32_t layer, int32_t position, float* k,
                            float* v);

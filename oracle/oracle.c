@@ -808,6 +808,110 @@ int orc_argmax(const float* x, int n) {
     return maxIdx;
 }
 
+/* ========================================================= Sampler ====== */
+
+/* Sampler.ApplyRepeatPenalty, Sampler.cs:64-81 (every occurrence in the
+ * window applies once). */
+static void apply_repeat_penalty(float* logits, int n, float penalty, int window, const int* recent, int n_recent) {
+    if (penalty == 1.0f || n_recent == 0 || window <= 0) return;
+    int start = n_recent - window > 0 ? n_recent - window : 0;
+    for (int i = start; i < n_recent; i++) {
+        int t = recent[i];
+        if (t >= 0 && t < n) {
+            if (logits[t] > 0) logits[t] = logits[t] / penalty;
+            else logits[t] = logits[t] * penalty;
+        }
+    }
+}
+
+/* Sampler.FindTopK, Sampler.cs:83-127: the first k as the running set, each
+ * later value replaces the (first) smallest when strictly larger, then a
+ * descending insertion sort. */
+static void find_top_k(const float* logits, int k, int n, int* idx, float* val) {
+    for (int i = 0; i < k; i++) { idx[i] = i; val[i] = logits[i]; }
+    for (int i = k; i < n; i++) {
+        int minIdx = 0;
+        for (int j = 1; j < k; j++) if (val[j] < val[minIdx]) minIdx = j;
+        if (logits[i] > val[minIdx]) { idx[minIdx] = i; val[minIdx] = logits[i]; }
+    }
+    for (int i = 1; i < k; i++) {
+        int ki = idx[i];
+        float kv = val[i];
+        int j = i - 1;
+        while (j >= 0 && val[j] < kv) { idx[j + 1] = idx[j]; val[j + 1] = val[j]; j--; }
+        idx[j + 1] = ki;
+        val[j + 1] = kv;
+    }
+}
+
+/* Sampler.FindNucleus, Sampler.cs:129-156: selection sort of the indices by
+ * probability (descending), then the shortest prefix whose running sum
+ * reaches topP. */
+static int find_nucleus(const float* p, int n, float topP, int* idx, float* val) {
+    for (int i = 0; i < n; i++) idx[i] = i;
+    for (int i = 0; i < n - 1; i++) {
+        int maxIdx = i;
+        for (int j = i + 1; j < n; j++) if (p[idx[j]] > p[idx[maxIdx]]) maxIdx = j;
+        if (maxIdx != i) { int tmp = idx[i]; idx[i] = idx[maxIdx]; idx[maxIdx] = tmp; }
+    }
+    float cumulative = 0.0f;
+    int count = 0;
+    for (int i = 0; i < n; i++) {
+        val[i] = p[idx[i]];
+        cumulative += val[i];
+        count++;
+        if (cumulative >= topP) break;
+    }
+    return count;
+}
+
+/* Sampler.SampleFromProbabilities, Sampler.cs:158-170, with the draw r given
+ * (Random.NextSingle(), Sampler.cs:160-161). */
+static int sample_from(const float* p, int n, float r) {
+    float cumulative = 0.0f;
+    for (int i = 0; i < n; i++) {
+        cumulative += p[i];
+        if (r <= cumulative) return i;
+    }
+    return n - 1;
+}
+
+/* Sampler.Sample, Sampler.cs:24-62.  recent = the recent-token list, r = the
+ * uniform draw. */
+int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, float penalty, int window,
+               const int* recent, int n_recent, float r) {
+    if (temperature <= 0.0f) return orc_argmax(logits, n);
+    float* scaled = (float*)malloc(sizeof(float) * (size_t)n);
+    float* buf = (float*)malloc(sizeof(float) * (size_t)n);
+    int* ibuf = (int*)malloc(sizeof(int) * (size_t)n);
+    memcpy(scaled, logits, sizeof(float) * (size_t)n);
+    apply_repeat_penalty(scaled, n, penalty, window, recent, n_recent);
+    orc_scale(scaled, 1.0f / temperature, scaled, n);
+    int result;
+    if (top_k > 0 && top_k < n) {
+        find_top_k(scaled, top_k, n, ibuf, buf);
+        orc_softmax(buf, top_k, 0, 0.0f);
+        result = ibuf[sample_from(buf, top_k, r)];
+    } else {
+        orc_softmax(scaled, n, 0, 0.0f);
+        result = -1;
+        if (top_p < 1.0f) {
+            int m = find_nucleus(scaled, n, top_p, ibuf, buf);
+            if (m < n) {
+                float sum = 0.0f;
+                for (int i = 0; i < m; i++) sum += buf[i];
+                orc_scale(buf, 1.0f / sum, buf, m);
+                result = ibuf[sample_from(buf, m, r)];
+            }
+        }
+        if (result < 0) result = sample_from(scaled, n, r);
+    }
+    free(scaled);
+    free(buf);
+    free(ibuf);
+    return result;
+}
+
 /* ============================================================ GGUF ====== */
 
 enum { GV_U8 = 0, GV_I8, GV_U16, GV_I16, GV_U32, GV_I32, GV_F32, GV_BOOL, GV_STR,

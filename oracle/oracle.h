@@ -72,6 +72,9 @@ void orc_rope_table(float* q, float* k, int head_dim, int position,
 void orc_rope_base(float* q, float* k, int head_dim, int position,
                    float freq_base, int rotary_dim, int same_span);   /* TO:658-677 */
 int  orc_argmax(const float* x, int n);                       /* VM:412-425 */
+/* Sampler.Sample (Sampler.cs:24-62) with the uniform draw r given. */
+int  orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, float penalty, int window,
+                const int* recent, int n_recent, float r);
 
 void orc_set_threads(int n);   /* row-parallel GEMV/attention; results are bitwise identical */
 int  orc_get_threads(void);

@@ -51,6 +51,7 @@ _SIG = {
     "orc_rope_table": ([_P, _P, _I, _I, _P, _I, _I], None),
     "orc_rope_base": ([_P, _P, _I, _I, _F, _I, _I], None),
     "orc_argmax": ([_P, _I], _I),
+    "orc_sample": ([_P, _I, _F, _I, _F, _F, _I, _P, _I, _F], _I),
     "orc_set_threads": ([_I], None),
     "orc_get_threads": ([], _I),
     "orc_model_open_buffer": ([_P, C.c_size_t, _I, C.c_char_p, _I], _P),
@@ -188,6 +189,14 @@ def rope_base(q, k, head_dim, position, freq_base, rotary_dim, same=False):
 def argmax(x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     return lib().orc_argmax(_p(x), x.size)
+
+
+def sample(logits, temperature, top_k, top_p, repeat_penalty, window, recent, r):
+    """Sampler.Sample (Sampler.cs:24-62) with the uniform draw r given."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    rec = np.ascontiguousarray(list(recent) if len(recent) else [0], dtype=np.int32)
+    return lib().orc_sample(_p(x), x.size, float(temperature), int(top_k), float(top_p), float(repeat_penalty),
+                            int(window), _p(rec), len(recent), float(r))
 
 
 class Model:
