@@ -149,3 +149,78 @@ def quantize(ggml_type: int, x: np.ndarray) -> np.ndarray:
     out = np.zeros(rows * byte_count(ggml_type, cols), dtype=np.uint8)
     check(lib().llmdot_hip_quantize(ggml_type, _lib.ptr(x), rows, cols, _lib.ptr(out)))
     return out
+
+
+# ------------------------------------------------------------ command line --
+
+QUANT_NAMES = {"f32": F32, "q8_0": Q8_0, "q4_0": _lib.Q4_0, "q4_k": Q4_K, "q5_k": _lib.Q5_K, "q6_k": Q6_K}
+
+
+def write_model(name: str, path: str, seed: int = 1234, context: int | None = None, sigma: float = 0.02) -> int:
+    """Writes the seeded synthetic model `name` (SPECS) as a GGUF file; returns its size."""
+    img = build_image(name, seed=seed, sigma=sigma, context=context)
+    with open(path, "wb") as f:
+        f.write(img.tobytes())
+    return int(img.size)
+
+
+def quantize_tensors(tensors: dict, ggml_type: int, path: str, metadata_items: list | None = None) -> int:
+    """Writes fp32 tensors (name -> 1-D or [rows, cols] array) as a GGUF file:
+    2-D tensors quantized to ggml_type, 1-D tensors kept F32 (norm weights).
+    GGUF dims are [cols, rows] (Tensor.cs:12-13).  Returns the file size."""
+    infos, blobs = [], []
+    for n, a in tensors.items():
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        if a.ndim == 1 or ggml_type == F32:
+            q = a.reshape(-1).view(np.uint8)
+            dims = (a.shape[-1],) if a.ndim == 1 else (a.shape[1], a.shape[0])
+            t = F32
+        elif a.ndim == 2:
+            if a.shape[1] % _lib.BLOCK[ggml_type][0]:
+                raise ValueError(f"{n}: width {a.shape[1]} is not a multiple of the block size")
+            q, dims, t = quantize(ggml_type, a), (a.shape[1], a.shape[0]), ggml_type
+        else:
+            raise ValueError(f"{n}: only 1-D and 2-D tensors")
+        infos.append((n, dims, t, int(q.size)))
+        blobs.append(q)
+    md = [("general.alignment", gguf.U32, 32)] + list(metadata_items or [])
+    hdr, offsets, total = gguf.header_bytes(md, infos)
+    img = np.zeros(total, dtype=np.uint8)
+    img[:len(hdr)] = np.frombuffer(hdr, dtype=np.uint8)
+    for off, q in zip(offsets, blobs):
+        img[len(hdr) + off: len(hdr) + off + q.size] = q
+    with open(path, "wb") as f:
+        f.write(img.tobytes())
+    return int(total)
+
+
+def main(argv=None) -> int:
+    """python -m dotllm_amd.synth model NAME OUT.gguf [--seed S] [--context N] [--sigma X]
+    python -m dotllm_amd.synth quantize IN.npz OUT.gguf --type q4_k|q5_k|q6_k|q8_0|q4_0|f32"""
+    import argparse
+    ap = argparse.ArgumentParser(prog="python -m dotllm_amd.synth",
+                                 description="GGUF writer: seeded synthetic models and reference-layout quantization")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    m = sub.add_parser("model", help="write a seeded synthetic model")
+    m.add_argument("name", choices=sorted(SPECS))
+    m.add_argument("out")
+    m.add_argument("--seed", type=int, default=1234)
+    m.add_argument("--context", type=int, default=None)
+    m.add_argument("--sigma", type=float, default=0.02)
+    q = sub.add_parser("quantize", help="quantize the fp32 arrays of an .npz file into a GGUF file")
+    q.add_argument("inp")
+    q.add_argument("out")
+    q.add_argument("--type", required=True, choices=sorted(QUANT_NAMES))
+    args = ap.parse_args(argv)
+    if args.cmd == "model":
+        n = write_model(args.name, args.out, args.seed, args.context, args.sigma)
+    else:
+        with np.load(args.inp, allow_pickle=False) as z:
+            tensors = {k: z[k] for k in z.files}
+        n = quantize_tensors(tensors, QUANT_NAMES[args.type], args.out)
+    print(f"wrote {args.out}: {n} bytes")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -92,3 +92,33 @@ def test_model_mix_types():
 def test_device_count_without_gpu_is_not_an_exception():
     from dotllm_amd.backend import device_count
     assert device_count() >= 0
+
+
+def test_gguf_tool_roundtrip(tmp_path):
+    """The shipped GGUF writer: a quantized file reads back with the reader the
+    engine uses, and the oracle decodes its blocks to the quantizer's output."""
+    rng = np.random.default_rng(2)
+    w = rng.normal(0, 0.02, size=(64, 512)).astype(np.float32)
+    norm = np.ones(512, np.float32)
+    np.savez(tmp_path / "t.npz", **{"blk.0.attn_q.weight": w, "blk.0.attn_norm.weight": norm})
+    for name, t in (("q4_k", Q4_K), ("q6_k", Q6_K), ("q8_0", Q8_0)):
+        out = tmp_path / f"t_{name}.gguf"
+        assert synth.main(["quantize", str(tmp_path / "t.npz"), str(out), "--type", name]) == 0
+        m = gguf.read(str(out))
+        ti = m.tensor("blk.0.attn_q.weight")
+        assert (ti.ggml_type, ti.rows, ti.cols) == (t, 64, 512)
+        assert m.tensor("blk.0.attn_norm.weight").ggml_type == F32
+        blocks = np.asarray(ti.data)
+        assert blocks.size == byte_count(t, 64 * 512)
+        assert np.array_equal(blocks, synth.quantize(t, w))
+        y = O.dequantize(blocks, t, 64, 512).reshape(64, 512)
+        assert np.max(np.abs(y - w)) < 0.02
+
+
+def test_gguf_tool_writes_loadable_model(tmp_path):
+    out = tmp_path / "tiny.gguf"
+    assert synth.main(["model", "tiny", str(out), "--context", "64"]) == 0
+    raw = np.fromfile(out, dtype=np.uint8)
+    assert np.array_equal(raw, synth.build_image("tiny", context=64))
+    cfg = gguf.resolve(gguf.read(str(out)))
+    assert (cfg.hidden_size, cfg.layer_count, cfg.vocab_size) == (512, 4, 32000)
