@@ -85,6 +85,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
+    ap.add_argument("--contexts", default="512,2048",
+                    help="extra decode contexts timed after the main run (decode_by_context)")
     ap.add_argument("--prefill", type=int, default=2048,
                     help="tokens of the timed prefill from position 0 (0: none)")
     ap.add_argument("--synthetic-kv", action="store_true",
@@ -152,6 +154,15 @@ def main() -> int:
     step_bytes = eng.step_bytes(pos + args.warmup + args.steps // 2)
     log(f"decode: {ms_step:.3f} ms/token, {value:.1f} tok/s, {step_bytes / ms_step / 1e6:.1f} GB/s step-level")
 
+    # the same loop at shorter contexts (the cost depends on the position only)
+    by_ctx = {}
+    for c in sorted({int(v) for v in args.contexts.split(",") if v.strip()}):
+        if 0 < c < pos:
+            r = eng.time_decode(tok, c, args.steps)
+            by_ctx[str(c)] = round(1000.0 * args.steps / r["total_ms"], 2)
+    by_ctx[str(args.ctx)] = round(value, 2)
+    log("decode by context: " + ", ".join(f"{c}: {v:.1f} tok/s" for c, v in by_ctx.items()))
+
     # dominant kernel: the fused gate/up SwiGLU GEMV, bracketed with HIP events
     kr = eng.time_decode(tok, pos + args.warmup + args.steps, args.kernel_steps, per_kernel=True)
     from dotllm_amd.measure import stream_peak_gbps
@@ -188,6 +199,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.config),
                      "bytes_per_launch": per_launch_bytes, "us_per_launch": round(per_launch_ms * 1e3, 2),
                      "stream_probe_gbps": {k: round(v, 1) for k, v in stream.items()}},
+        "decode_by_context": by_ctx,
         "prefill": pf,
         "cpu_baseline": None,
     }
