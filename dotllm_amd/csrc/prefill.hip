@@ -426,11 +426,14 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         frow[tj] = (int64_t)grow_of(rw[tj]) * rbytes;
     }
 
-    f4 acc[TI][TJ];
+    // K-quants carry one scale d per 256-element superblock: their MFMA sums run
+    // over the superblock's 8 steps in cs and are scaled into acc once, at its end
+    constexpr bool SBD = F::EPB == 256;
+    f4 acc[TI][TJ], cs[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < TJ; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TJ; j++) acc[i][j] = cs[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
     issue(0);
     if (NS == 3 && nsteps > 1) issue(1);
@@ -469,12 +472,26 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
             }
 #pragma unroll
             for (int tj = 0; tj < TJ; tj++) {
-                f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wf[tj][0], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wf[tj][0], SBD ? cs[ti][tj] : f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, wf[tj][0], c, 0, 0, 0);
                 if constexpr (NP == 2) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, wf[tj][1], c, 0, 0, 0);
+                if constexpr (SBD) {
+                    cs[ti][tj] = c;
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc[ti][tj][e] += d[tj] * c[e];
+                    for (int e = 0; e < 4; e++) acc[ti][tj][e] += d[tj] * c[e];
+                }
             }
+        }
+        if (SBD && (st & 7) == 7) {   // superblock end: acc += d * (its 8 steps' sums)
+#pragma unroll
+            for (int ti = 0; ti < TI; ti++)
+#pragma unroll
+                for (int tj = 0; tj < TJ; tj++) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[ti][tj][e] += d[tj] * cs[ti][tj][e];
+                    cs[ti][tj] = f4{0.f, 0.f, 0.f, 0.f};
+                }
         }
         if constexpr (F::MIN) {
             if ((st & 7) == 7) {   // superblock end: acc -= 32 dmin * (sum_g m_g S_g) / 32
