@@ -787,7 +787,8 @@ constexpr int KPAD = 8;   // halves of row padding in the K / V^T tiles
 template <int HD>
 __global__ __launch_bounds__(WG) void pf_attn_scores_mfma(PfAttnArgs a) {
     constexpr int KS = HD / 32;   // MFMA k-steps over the head dimension
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[AK][HD + KPAD];
+    constexpr int KCH = AK * HD / 8 / WG;   // 16-byte K chunks per thread and tile
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][AK][HD + KPAD];
     const int t0 = blockIdx.x * AQ, h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
     const int qdim = a.heads * HD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lk = lane >> 4;
@@ -834,20 +835,33 @@ __global__ __launch_bounds__(WG) void pf_attn_scores_mfma(PfAttnArgs a) {
     const int64_t kbase = (int64_t)kvh * a.context * HD;
     const _Float16* kc = reinterpret_cast<const _Float16*>(a.kcache);
     float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    for (int j0 = 0; j0 < nkeys; j0 += AK) {
-        __syncthreads();
-        for (int c = tid; c < AK * HD / 8; c += WG) {   // 16-byte chunks of the K tile
-            const int r = c / (HD / 8), q = c - r * (HD / 8);
-            const int j = min(j0 + r, nkeys - 1);
-            *reinterpret_cast<v4u*>(&Ks[r][8 * q]) = *reinterpret_cast<const v4u*>(kc + kbase + (int64_t)j * HD + 8 * q);
+    // The next tile's K rows are loaded into registers while this tile's
+    // MFMAs run; tiles alternate between two LDS buffers.
+    v4u kr[KCH];
+    auto load_k = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < KCH; k++) {
+            const int c = tid + k * WG, r = c / (HD / 8), q = c - r * (HD / 8);
+            kr[k] = *reinterpret_cast<const v4u*>(kc + kbase + (int64_t)min(j0 + r, nkeys - 1) * HD + 8 * q);
+        }
+    };
+    load_k(0);
+    int it = 0;
+    for (int j0 = 0; j0 < nkeys; j0 += AK, it++) {
+        const int buf = it & 1;
+#pragma unroll
+        for (int k = 0; k < KCH; k++) {   // this tile's K rows into LDS (buffer last read two tiles ago)
+            const int c = tid + k * WG, r = c / (HD / 8), q = c - r * (HD / 8);
+            *reinterpret_cast<v4u*>(&Ks[buf][r][8 * q]) = kr[k];
         }
         __syncthreads();
+        if (j0 + AK < nkeys) load_k(j0 + AK);
 #pragma unroll
         for (int kt = 0; kt < AK / 16; kt++) {
             f4 c = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
-                const h8 kf = *reinterpret_cast<const h8*>(&Ks[kt * 16 + lr][32 * ks + 8 * lk]);
+                const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][kt * 16 + lr][32 * ks + 8 * lk]);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kf, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], kf, c, 0, 0, 0);
             }
@@ -877,7 +891,9 @@ __global__ __launch_bounds__(WG) void pf_attn_scores_mfma(PfAttnArgs a) {
 template <int HD>
 __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
     constexpr int DT = HD / 16;   // 16-wide output tiles over the head dimension
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[HD][AK + KPAD];   // V^T tile
+    constexpr int VCH = AK * HD / 8 / WG;   // 16-byte V chunks per thread and tile
+    constexpr int SPL = AK / 32 * 8;        // scores per lane and tile
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][HD][AK + KPAD];   // V^T tiles
     const int t0 = blockIdx.x * AQ, h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
     const int qdim = a.heads * HD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lk = lane >> 4;
@@ -895,16 +911,34 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
 #pragma unroll
     for (int i = 0; i < DT; i++) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
     float z = 0.f;
-    for (int j0 = 0; j0 < nkeys; j0 += AK) {
-        __syncthreads();
-        for (int c = tid; c < AK * HD / 8; c += WG) {   // V rows -> V^T; a wave writes 64 consecutive keys
-            const int r = c & (AK - 1), q = c / AK;
-            const int j = min(j0 + r, nkeys - 1);
-            const h8 v = *reinterpret_cast<const h8*>(vc + vbase + (int64_t)j * HD + 8 * q);
+    // The next tile's V rows and this lane's scores are loaded into registers
+    // while this tile computes; V^T tiles alternate between two LDS buffers.
+    h8 vr[VCH];
+    float sr[SPL], sn[SPL];
+    auto load_tile = [&](int j0, float* so) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) Vt[8 * q + i][r] = v[i];
+        for (int k = 0; k < VCH; k++) {
+            const int c = tid + k * WG, r = c & (AK - 1), q = c / AK;
+            vr[k] = *reinterpret_cast<const h8*>(vc + vbase + (int64_t)min(j0 + r, nkeys - 1) * HD + 8 * q);
+        }
+#pragma unroll
+        for (int kk = 0; kk < AK / 32; kk++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) so[8 * kk + i] = srow[min(j0 + kk * 32 + 8 * lk + i, nA - 1)];
+    };
+    load_tile(0, sr);
+    int it = 0;
+    for (int j0 = 0; j0 < nkeys; j0 += AK, it++) {
+        const int buf = it & 1;
+#pragma unroll
+        for (int k = 0; k < VCH; k++) {   // V rows -> V^T (buffer last read two tiles ago); a wave writes 64 consecutive keys
+            const int c = tid + k * WG, r = c & (AK - 1), q = c / AK;
+#pragma unroll
+            for (int i = 0; i < 8; i++) Vt[buf][8 * q + i][r] = vr[k][i];
         }
         __syncthreads();
+        const bool more = j0 + AK < nkeys;
+        if (more) load_tile(j0 + AK, sn);
 #pragma unroll
         for (int kk = 0; kk < AK / 32; kk++) {
             const int kb = j0 + kk * 32 + 8 * lk;   // this lane's 8 keys
@@ -915,7 +949,7 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
                 float ev = 0.f;
                 if (liveA && key < nA) {
 #pragma clang fp contract(off)
-                    const float x = srow[key] - mA;
+                    const float x = sr[8 * kk + i] - mA;
                     ev = key < n8A ? exp_approx(x) : expf(x);
                 }
                 z += ev;
@@ -926,10 +960,14 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
             }
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
-                const h8 vf = *reinterpret_cast<const h8*>(&Vt[dt * 16 + lr][kk * 32 + 8 * lk]);
+                const h8 vf = *reinterpret_cast<const h8*>(&Vt[buf][dt * 16 + lr][kk * 32 + 8 * lk]);
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(eh, vf, acc[dt], 0, 0, 0);
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(el, vf, acc[dt], 0, 0, 0);
             }
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < SPL; i++) sr[i] = sn[i];
         }
     }
     z = xor32_add(xor16_add(z));   // lanes lr, lr+16, ... hold query lr's sum
