@@ -91,6 +91,10 @@ struct llmdot_hip_ctx {
     float* am_val = nullptr;
     int32_t* am_idx = nullptr;
     int am_cap = 0;
+    // two more streams (default priority) for independent prompt GEMMs, forked
+    // from and joined back into `stream` with events
+    hipStream_t side[2] = {nullptr, nullptr};
+    hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -184,6 +188,14 @@ extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
     if (ctx->am_ints) (void)hipFree(ctx->am_ints);
     if (ctx->am_val) (void)hipFree(ctx->am_val);
     if (ctx->am_idx) (void)hipFree(ctx->am_idx);
+    for (int i = 0; i < 2; i++) {
+        if (ctx->side[i]) {
+            (void)hipStreamSynchronize(ctx->side[i]);
+            (void)hipStreamDestroy(ctx->side[i]);
+        }
+        if (ctx->join[i]) (void)hipEventDestroy(ctx->join[i]);
+    }
+    if (ctx->fork) (void)hipEventDestroy(ctx->fork);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;
@@ -842,8 +854,19 @@ int prefill_chunk_cap(const llmdot_hip_model* m) {
     return cap;
 }
 
+int ensure_side_streams(llmdot_hip_ctx* ctx) {
+    if (ctx->fork) return 0;
+    for (int i = 0; i < 2; i++) {
+        HIPCHK(hipStreamCreateWithFlags(&ctx->side[i], hipStreamNonBlocking));
+        HIPCHK(hipEventCreateWithFlags(&ctx->join[i], hipEventDisableTiming));
+    }
+    HIPCHK(hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming));
+    return 0;
+}
+
 int ensure_prefill_ws(llmdot_hip_model* m) {
     if (m->pf_cap) return 0;
+    if (int rc = ensure_side_streams(m->ctx)) return rc;
     const auto& d = m->d;
     const int cap = prefill_chunk_cap(m);
     const size_t qdim = (size_t)d.heads * d.head_dim, kvdim = (size_t)d.kv_heads * d.head_dim;
@@ -882,9 +905,19 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
         HIPCHK(launch_prefill_planes(m->pf_h, T, d.hidden, w.attn_norm_f, d.eps, pl, s));
+        // Q, K and V read the same planes and write separate buffers: K and V
+        // run on the side streams beside Q (K and V alone fill half the CUs)
+        llmdot_hip_ctx* c = m->ctx;
+        HIPCHK(hipEventRecord(c->fork, s));
+        HIPCHK(hipStreamWaitEvent(c->side[0], c->fork, 0));
+        HIPCHK(hipStreamWaitEvent(c->side[1], c->fork, 0));
+        HIPCHK(launch_prefill_gemm(w.k->type, 0, pl, w.k->dev, nullptr, T, kvdim, d.hidden, m->pf_k, kvdim, c->side[0]));
+        HIPCHK(launch_prefill_gemm(w.v->type, 0, pl, w.v->dev, nullptr, T, kvdim, d.hidden, m->pf_v, kvdim, c->side[1]));
+        HIPCHK(hipEventRecord(c->join[0], c->side[0]));
+        HIPCHK(hipEventRecord(c->join[1], c->side[1]));
         HIPCHK(launch_prefill_gemm(w.q->type, 0, pl, w.q->dev, nullptr, T, qdim, d.hidden, m->pf_q, qdim, s));
-        HIPCHK(launch_prefill_gemm(w.k->type, 0, pl, w.k->dev, nullptr, T, kvdim, d.hidden, m->pf_k, kvdim, s));
-        HIPCHK(launch_prefill_gemm(w.v->type, 0, pl, w.v->dev, nullptr, T, kvdim, d.hidden, m->pf_v, kvdim, s));
+        HIPCHK(hipStreamWaitEvent(s, c->join[0], 0));
+        HIPCHK(hipStreamWaitEvent(s, c->join[1], 0));
         PfAttnArgs aa{};
         aa.q = m->pf_q; aa.k = m->pf_k; aa.v = m->pf_v; aa.qr = m->pf_qr;
         aa.kcache = m->kcache + (size_t)l * m->kv_layer_bytes;
