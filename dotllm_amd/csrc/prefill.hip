@@ -780,194 +780,230 @@ __global__ __launch_bounds__(WG) void pf_attn_pv_kernel(PfAttnArgs a) {
 // fp16 planes each (22-bit significands), with fp32 accumulation, so scores
 // and outputs carry fp32-level rounding only.  Wave w of a workgroup owns
 // queries t0 + 16 w .. + 15 of one q head; keys advance 64 per tile.
+//
+// Scores are computed transposed, S^T = K q^T (MFMA A = K rows, B = the
+// query planes), so a lane holds keys 4 (l >> 4) .. + 3 of each 16-key
+// sub-tile for query l & 15: exactly the row layout the e V product needs as
+// its A operand (with the keys of a 32-key step taken in the order 4 lk .. +3,
+// 16 + 4 lk .. +3, matched in the V^T fragment).  Two passes over the keys:
+// the first finds each query's maximum (VectorMath.Softmax needs the exact
+// maximum before any ExpApprox, VM:215-258), the second recomputes the same
+// scores bit for bit and accumulates e and e V; no score leaves registers.
 
 constexpr int KPAD = 8;   // halves of row padding in the K / V^T tiles
 
-// Scores (q . K_j) / sqrt(hd) into the score scratch plus each query's maximum.
+// The lane's query planes (query l & 15 of the wave, dims 32 ks + 8 lk .. +7,
+// scaled by a power of two) and the factor that turns an MFMA sum into the
+// score (q . K_j) / sqrt(hd).
 template <int HD>
-__global__ __launch_bounds__(WG) void pf_attn_scores_mfma(PfAttnArgs a) {
-    constexpr int KS = HD / 32;   // MFMA k-steps over the head dimension
-    constexpr int KCH = AK * HD / 8 / WG;   // 16-byte K chunks per thread and tile
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][AK][HD + KPAD];
-    const int t0 = blockIdx.x * AQ, h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
-    const int qdim = a.heads * HD;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lk = lane >> 4;
-    // this lane's q elements (query lr of the wave, dims 32 ks + 8 lk .. +7) as two planes
-    const int tq = min(t0 + 16 * wave + lr, a.T - 1);
-    const float* qrow = a.qr + (int64_t)tq * qdim + h * HD;
-    float qv[KS][8];
-    float amax = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
-        const float4 u = *reinterpret_cast<const float4*>(qrow + 32 * ks + 8 * lk);
-        const float4 v = *reinterpret_cast<const float4*>(qrow + 32 * ks + 8 * lk + 4);
-        qv[ks][0] = u.x; qv[ks][1] = u.y; qv[ks][2] = u.z; qv[ks][3] = u.w;
-        qv[ks][4] = v.x; qv[ks][5] = v.y; qv[ks][6] = v.z; qv[ks][7] = v.w;
-#pragma unroll
-        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(qv[ks][i]));
-    }
-    amax = fmaxf(amax, fx(lane_xor16, amax));
-    amax = fmaxf(amax, fx(lane_xor32, amax));
-    int e = 0;
-    if (amax > 0.f) {
-        (void)frexpf(amax, &e);
-        e = 15 - e;
-        e = e > 126 ? 126 : (e < -126 ? -126 : e);
-    }
-    const float sq = ldexpf(1.0f, e);
+struct QFrag {
+    static constexpr int KS = HD / 32;
     h8 qh[KS], ql[KS];
+    float oscale;
+    __device__ void load(const PfAttnArgs& a, int tq, int h, int lk) {
+        const float* qrow = a.qr + (int64_t)tq * (a.heads * HD) + h * HD;
+        float qv[KS][8];
+        float amax = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
+        for (int ks = 0; ks < KS; ks++) {
+            const float4 u = *reinterpret_cast<const float4*>(qrow + 32 * ks + 8 * lk);
+            const float4 v = *reinterpret_cast<const float4*>(qrow + 32 * ks + 8 * lk + 4);
+            qv[ks][0] = u.x; qv[ks][1] = u.y; qv[ks][2] = u.z; qv[ks][3] = u.w;
+            qv[ks][4] = v.x; qv[ks][5] = v.y; qv[ks][6] = v.z; qv[ks][7] = v.w;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float x = qv[ks][i] * sq;
-            const _Float16 hi = (_Float16)x;
-            qh[ks][i] = hi;
-            ql[ks][i] = (_Float16)(x - (float)hi);
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(qv[ks][i]));
         }
-    // output rows are queries 4 lk + r: their scale factors (held by lanes 4 lk + r)
-    const float inv_sqrt = 1.0f / sqrtf((float)HD);
-    float oscale[4];
+        amax = fmaxf(amax, fx(lane_xor16, amax));
+        amax = fmaxf(amax, fx(lane_xor32, amax));
+        int e = 0;
+        if (amax > 0.f) {
+            (void)frexpf(amax, &e);
+            e = 15 - e;
+            e = e > 126 ? 126 : (e < -126 ? -126 : e);
+        }
+        const float sq = ldexpf(1.0f, e);
 #pragma unroll
-    for (int r = 0; r < 4; r++) oscale[r] = inv_sqrt * ldexpf(1.0f, -__shfl(e, 4 * lk + r, 64));
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = qv[ks][i] * sq;
+                const _Float16 hi = (_Float16)x;
+                qh[ks][i] = hi;
+                ql[ks][i] = (_Float16)(x - (float)hi);
+            }
+        oscale = (1.0f / sqrtf((float)HD)) * ldexpf(1.0f, -e);
+    }
+    // scores of keys kt * 16 + 4 lk + r (r = 0..3) of the LDS K tile for this lane's query
+    __device__ f4 scores(const _Float16 (*Ks)[HD + KPAD], int kt, int lr, int lk) const {
+        f4 c = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const h8 kf = *reinterpret_cast<const h8*>(&Ks[kt * 16 + lr][32 * ks + 8 * lk]);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], c, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) c[r] = c[r] * oscale;
+        return c;
+    }
+};
 
+// 16-byte chunks of a K tile (rows j0 .. j0 + AK - 1, clamped to the last key)
+// through registers into LDS.
+template <int HD>
+struct KTile {
+    static constexpr int CH = AK * HD / 8 / WG;
+    v4u r[CH];
+    __device__ void load(const _Float16* kc, int64_t base, int j0, int nkeys, int tid) {
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int c = tid + k * WG, row = c / (HD / 8), q = c - row * (HD / 8);
+            r[k] = *reinterpret_cast<const v4u*>(kc + base + (int64_t)min(j0 + row, nkeys - 1) * HD + 8 * q);
+        }
+    }
+    __device__ void store(_Float16 (*Ks)[HD + KPAD], int tid) const {
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int c = tid + k * WG, row = c / (HD / 8), q = c - row * (HD / 8);
+            *reinterpret_cast<v4u*>(&Ks[row][8 * q]) = r[k];
+        }
+    }
+};
+
+// Query block and head of this workgroup: the causal work grows with the
+// block, so the last (heaviest) blocks are dispatched first and the light
+// ones fill the CUs as they free up.
+__device__ __forceinline__ void attn_block(const PfAttnArgs& a, int& t0, int& h) {
+    const int nqb = (a.T + AQ - 1) / AQ;
+    const int L = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    h = L % a.heads;
+    t0 = (nqb - 1 - L / a.heads) * AQ;
+}
+
+// Pass 1: each query's maximum score over keys 0 .. pos0 + t.
+template <int HD>
+__global__ __launch_bounds__(WG) void pf_attn_max_mfma(PfAttnArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][AK][HD + KPAD];
+    int t0, h;
+    attn_block(a, t0, h);
+    const int kvh = h / (a.heads / a.kv_heads);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lk = lane >> 4;
+    const int tq = t0 + 16 * wave + lr;
+    QFrag<HD> qf;
+    qf.load(a, min(tq, a.T - 1), h, lk);
+    const int last = tq < a.T ? a.pos0 + tq : -1;      // the query's last key
     const int nkeys = a.pos0 + min(t0 + AQ, a.T);
     const int64_t kbase = (int64_t)kvh * a.context * HD;
     const _Float16* kc = reinterpret_cast<const _Float16*>(a.kcache);
-    float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    // The next tile's K rows are loaded into registers while this tile's
-    // MFMAs run; tiles alternate between two LDS buffers.
-    v4u kr[KCH];
-    auto load_k = [&](int j0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < KCH; k++) {
-            const int c = tid + k * WG, r = c / (HD / 8), q = c - r * (HD / 8);
-            kr[k] = *reinterpret_cast<const v4u*>(kc + kbase + (int64_t)min(j0 + r, nkeys - 1) * HD + 8 * q);
-        }
-    };
-    load_k(0);
+    float m = -INFINITY;
+    KTile<HD> kt_regs;
+    kt_regs.load(kc, kbase, 0, nkeys, tid);
     int it = 0;
     for (int j0 = 0; j0 < nkeys; j0 += AK, it++) {
         const int buf = it & 1;
-#pragma unroll
-        for (int k = 0; k < KCH; k++) {   // this tile's K rows into LDS (buffer last read two tiles ago)
-            const int c = tid + k * WG, r = c / (HD / 8), q = c - r * (HD / 8);
-            *reinterpret_cast<v4u*>(&Ks[buf][r][8 * q]) = kr[k];
-        }
+        kt_regs.store(Ks[buf], tid);   // buffer last read two tiles ago
         __syncthreads();
-        if (j0 + AK < nkeys) load_k(j0 + AK);
+        if (j0 + AK < nkeys) kt_regs.load(kc, kbase, j0 + AK, nkeys, tid);
 #pragma unroll
         for (int kt = 0; kt < AK / 16; kt++) {
-            f4 c = f4{0.f, 0.f, 0.f, 0.f};
+            const f4 c = qf.scores(Ks[buf], kt, lr, lk);
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const h8 kf = *reinterpret_cast<const h8*>(&Ks[buf][kt * 16 + lr][32 * ks + 8 * lk]);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kf, c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], kf, c, 0, 0, 0);
-            }
-            const int key = j0 + kt * 16 + lr;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = t0 + 16 * wave + 4 * lk + r;
-                if (t < a.T && key <= a.pos0 + t) {
-                    const float sc = c[r] * oscale[r];
-                    a.scores[((int64_t)h * a.T + t) * a.ld_scores + key] = sc;
-                    rmax[r] = fmaxf(rmax[r], sc);
-                }
-            }
+            for (int r = 0; r < 4; r++)
+                if (j0 + kt * 16 + 4 * lk + r <= last) m = fmaxf(m, c[r]);
         }
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        float m = rmax[r];
-        m = max16(m);
-        const int t = t0 + 16 * wave + 4 * lk + r;
-        if (lr == 0 && t < a.T) a.rowmax[(int64_t)h * a.T + t] = m;
-    }
+    m = fmaxf(m, fx(lane_xor16, m));
+    m = fmaxf(m, fx(lane_xor32, m));
+    if (lk == 0 && tq < a.T) a.rowmax[(int64_t)h * a.T + tq] = m;
 }
 
-// Softmax numerators (ExpApprox on the first 8 floor(n/8) keys, expf on the
-// tail, VM:215-258) and out = sum_j e_j V_j / sum_j e_j.
+// Pass 2: the same scores, softmax numerators (ExpApprox on the first
+// 8 floor(n/8) keys, expf on the tail, VM:215-258) and out = sum_j e_j V_j /
+// sum_j e_j.
 template <int HD>
 __global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
-    constexpr int DT = HD / 16;   // 16-wide output tiles over the head dimension
-    constexpr int VCH = AK * HD / 8 / WG;   // 16-byte V chunks per thread and tile
-    constexpr int SPL = AK / 32 * 8;        // scores per lane and tile
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][HD][AK + KPAD];   // V^T tiles
-    const int t0 = blockIdx.x * AQ, h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
+    constexpr int DT = HD / 16;              // 16-wide output tiles over the head dimension
+    constexpr int VCH = AK * HD / 8 / WG;    // 16-byte V chunks per thread and tile
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[AK][HD + KPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[HD][AK + KPAD];   // V^T tile
+    int t0, h;
+    attn_block(a, t0, h);
+    const int kvh = h / (a.heads / a.kv_heads);
     const int qdim = a.heads * HD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lk = lane >> 4;
-    const int tA = t0 + 16 * wave + lr;                 // this lane's A-operand query
-    const bool liveA = tA < a.T;
-    const int tAc = min(tA, a.T - 1);
-    const int nA = a.pos0 + tAc + 1, n8A = nA & ~7;     // keys of that query, vector-lane part
-    const float mA = a.rowmax[(int64_t)h * a.T + tAc];
-    const float* srow = a.scores + ((int64_t)h * a.T + tAc) * a.ld_scores;
+    const int tq = t0 + 16 * wave + lr;
+    const int tqc = min(tq, a.T - 1);
+    QFrag<HD> qf;
+    qf.load(a, tqc, h, lk);
+    const int last = tq < a.T ? a.pos0 + tq : -1;
+    const int n8 = (a.pos0 + tqc + 1) & ~7;            // keys of the query on the vector lanes
+    const float mq = a.rowmax[(int64_t)h * a.T + tqc];
     const int nkeys = a.pos0 + min(t0 + AQ, a.T);
-    const int64_t vbase = (int64_t)kvh * a.context * HD;
+    const int64_t base = (int64_t)kvh * a.context * HD;
+    const _Float16* kc = reinterpret_cast<const _Float16*>(a.kcache);
     const _Float16* vc = reinterpret_cast<const _Float16*>(a.vcache);
     const float P14 = 16384.0f;
     f4 acc[DT];
 #pragma unroll
     for (int i = 0; i < DT; i++) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
     float z = 0.f;
-    // The next tile's V rows and this lane's scores are loaded into registers
-    // while this tile computes; V^T tiles alternate between two LDS buffers.
+    KTile<HD> kr;
     h8 vr[VCH];
-    float sr[SPL], sn[SPL];
-    auto load_tile = [&](int j0, float* so) __attribute__((always_inline)) {
+    auto load_v = [&](int j0) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < VCH; k++) {
             const int c = tid + k * WG, r = c & (AK - 1), q = c / AK;
-            vr[k] = *reinterpret_cast<const h8*>(vc + vbase + (int64_t)min(j0 + r, nkeys - 1) * HD + 8 * q);
+            vr[k] = *reinterpret_cast<const h8*>(vc + base + (int64_t)min(j0 + r, nkeys - 1) * HD + 8 * q);
         }
-#pragma unroll
-        for (int kk = 0; kk < AK / 32; kk++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) so[8 * kk + i] = srow[min(j0 + kk * 32 + 8 * lk + i, nA - 1)];
     };
-    load_tile(0, sr);
-    int it = 0;
-    for (int j0 = 0; j0 < nkeys; j0 += AK, it++) {
-        const int buf = it & 1;
+    kr.load(kc, base, 0, nkeys, tid);
+    load_v(0);
+    for (int j0 = 0; j0 < nkeys; j0 += AK) {
+        __syncthreads();   // the previous tile's LDS reads are done
+        kr.store(Ks, tid);
 #pragma unroll
-        for (int k = 0; k < VCH; k++) {   // V rows -> V^T (buffer last read two tiles ago); a wave writes 64 consecutive keys
+        for (int k = 0; k < VCH; k++) {   // V rows -> V^T; a wave writes 64 consecutive keys
             const int c = tid + k * WG, r = c & (AK - 1), q = c / AK;
 #pragma unroll
-            for (int i = 0; i < 8; i++) Vt[buf][8 * q + i][r] = vr[k][i];
+            for (int i = 0; i < 8; i++) Vt[8 * q + i][r] = vr[k][i];
         }
         __syncthreads();
-        const bool more = j0 + AK < nkeys;
-        if (more) load_tile(j0 + AK, sn);
+        if (j0 + AK < nkeys) {
+            kr.load(kc, base, j0 + AK, nkeys, tid);
+            load_v(j0 + AK);
+        }
 #pragma unroll
-        for (int kk = 0; kk < AK / 32; kk++) {
-            const int kb = j0 + kk * 32 + 8 * lk;   // this lane's 8 keys
+        for (int p = 0; p < AK / 32; p++) {
             h8 eh, el;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int key = kb + i;
-                float ev = 0.f;
-                if (liveA && key < nA) {
+            for (int half = 0; half < 2; half++) {
+                const int kt = 2 * p + half;
+                const f4 c = qf.scores(Ks, kt, lr, lk);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = j0 + kt * 16 + 4 * lk + r;
+                    float ev = 0.f;
+                    if (key <= last) {
 #pragma clang fp contract(off)
-                    const float x = sr[8 * kk + i] - mA;
-                    ev = key < n8A ? exp_approx(x) : expf(x);
+                        const float x = c[r] - mq;
+                        ev = key < n8 ? exp_approx(x) : expf(x);
+                    }
+                    z += ev;
+                    const float xs = ev * P14;
+                    const _Float16 hi = (_Float16)xs;
+                    eh[4 * half + r] = hi;
+                    el[4 * half + r] = (_Float16)(xs - (float)hi);
                 }
-                z += ev;
-                const float xs = ev * P14;
-                const _Float16 hi = (_Float16)xs;
-                eh[i] = hi;
-                el[i] = (_Float16)(xs - (float)hi);
             }
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
-                const h8 vf = *reinterpret_cast<const h8*>(&Vt[buf][dt * 16 + lr][kk * 32 + 8 * lk]);
+                // keys 32 p + 4 lk .. +3 and 32 p + 16 + 4 lk .. +3, as in eh / el
+                const uint2 v0 = *reinterpret_cast<const uint2*>(&Vt[dt * 16 + lr][32 * p + 4 * lk]);
+                const uint2 v1 = *reinterpret_cast<const uint2*>(&Vt[dt * 16 + lr][32 * p + 16 + 4 * lk]);
+                const h8 vf = __builtin_bit_cast(h8, v4u{v0.x, v0.y, v1.x, v1.y});
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(eh, vf, acc[dt], 0, 0, 0);
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(el, vf, acc[dt], 0, 0, 0);
             }
-        }
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < SPL; i++) sr[i] = sn[i];
         }
     }
     z = xor32_add(xor16_add(z));   // lanes lr, lr+16, ... hold query lr's sum
@@ -1002,7 +1038,7 @@ hipError_t launch_gemm_fmt(int epi, PfGemmArgs a, hipStream_t s) {
 template <int HD>
 hipError_t launch_attn_hd(const PfAttnArgs& a, hipStream_t s) {
     const dim3 grid((a.T + AQ - 1) / AQ, a.heads);
-    if (a.kv_fp16) pf_attn_scores_mfma<HD><<<grid, WG, 0, s>>>(a);
+    if (a.kv_fp16) pf_attn_max_mfma<HD><<<grid, WG, 0, s>>>(a);
     else pf_attn_scores_kernel<HD><<<grid, WG, 0, s>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
