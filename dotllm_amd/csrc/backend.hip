@@ -848,9 +848,12 @@ int prefill_chunk_cap(const llmdot_hip_model* m) {
         const int c = atoi(v);
         if (c >= 16) cap = c;
     }
-    // score scratch [heads][cap][context] fp32 within 2 GiB
-    const double per_tok = 4.0 * m->d.heads * (double)m->d.context;
-    while (cap > 64 && per_tok * cap > 2147483648.0) cap /= 2;
+    // fp32 KV: score scratch [heads][cap][context] fp32 within 2 GiB (the
+    // fp16-KV attention keeps its scores in registers)
+    if (!m->d.kv_fp16) {
+        const double per_tok = 4.0 * m->d.heads * (double)m->d.context;
+        while (cap > 64 && per_tok * cap > 2147483648.0) cap /= 2;
+    }
     return cap;
 }
 
@@ -881,7 +884,10 @@ int ensure_prefill_ws(llmdot_hip_model* m) {
     if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_qr = (float*)p;
     if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_attn = (float*)p;
     if ((rc = A(4 * cap * (size_t)d.ffn, &p))) return rc; m->pf_act = (float*)p;
-    if ((rc = A(4 * (size_t)d.heads * cap * (size_t)d.context, &p))) return rc; m->pf_scores = (float*)p;
+    if (!d.kv_fp16) {
+        if ((rc = A(4 * (size_t)d.heads * cap * (size_t)d.context, &p))) return rc;
+        m->pf_scores = (float*)p;
+    }
     if ((rc = A(4 * (size_t)d.heads * cap, &p))) return rc; m->pf_rowmax = (float*)p;
     if ((rc = A(2 * cap * kmax, &p))) return rc; m->pf_planes.xh = (_Float16*)p;
     if ((rc = A(2 * cap * kmax, &p))) return rc; m->pf_planes.xl = (_Float16*)p;

@@ -921,7 +921,7 @@ __global__ __launch_bounds__(WG) void pf_attn_max_mfma(PfAttnArgs a) {
 // 8 floor(n/8) keys, expf on the tail, VM:215-258) and out = sum_j e_j V_j /
 // sum_j e_j.
 template <int HD>
-__global__ __launch_bounds__(WG) void pf_attn_pv_mfma(PfAttnArgs a) {
+__global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
     constexpr int DT = HD / 16;              // 16-wide output tiles over the head dimension
     constexpr int VCH = AK * HD / 8 / WG;    // 16-byte V chunks per thread and tile
     __shared__ __attribute__((aligned(16))) _Float16 Ks[AK][HD + KPAD];
