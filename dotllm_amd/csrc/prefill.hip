@@ -325,9 +325,10 @@ __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" :
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // LDS rows of 32 halves (64 bytes) hold 4 chunks of 8; chunk c of row r sits
-// at position c ^ swz(r), which spreads the 16 rows of an MFMA fragment read
-// over distinct banks.  swz(16 i + l) = swz(l) ^ 2 (i & 1).
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// at position c ^ swz(r), which spreads an MFMA fragment read (16 rows x 4
+// chunks) over distinct banks whether the LDS serves 16 or 32 lanes of a
+// 16-byte read per cycle.  swz(16 i + l) = swz(l) ^ 2 (i & 1).
+__device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ r ^ ((r >> 3) & 2)) & 3; }
 
 template <uint32_t FMT, int EPI>
 __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
