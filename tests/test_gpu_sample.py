@@ -55,7 +55,7 @@ def test_greedy_is_argmax(hip):
 
 
 TOPK_CASES = [(100, 1, 0.8), (100, 3, 1.0), (100, 40, 0.7), (1000, 999, 1.3), (32000, 40, 0.8),
-              (32000, 4096, 1.1), (128256, 40, 0.8), (128256, 4096, 0.6)]
+              (32000, 4096, 1.1), (128256, 40, 0.8), (128256, 4096, 0.6), (13, 12, 0.9), (37, 11, 2.0)]
 
 
 @pytest.mark.parametrize("n,k,temp", TOPK_CASES)
@@ -81,7 +81,7 @@ def test_top_k_with_repeat_penalty(hip):
 
 
 TOPP_CASES = [(100, 0, 0.5), (100, 100, 0.9), (4096, 0, 0.95), (4096, 0, 0.5), (4096, 0, 1.0), (32000, 0, 0.9),
-              (32000, 32000, 0.95)]
+              (32000, 32000, 0.95), (37, 0, 0.9), (1000, 0, 0.01), (13, 0, 1.0)]
 
 
 @pytest.mark.parametrize("n,k,top_p", TOPP_CASES)
