@@ -295,8 +295,6 @@ hipError_t launch_hd(const AttnArgs& a, hipStream_t s) {
 
 }  // namespace
 
-int attn_chunk(int, int) { return CH; }
-
 int attn_max_chunks(int heads, int kv_heads, int context) {
     (void)heads; (void)kv_heads;
     return (context + CH - 1) / CH;

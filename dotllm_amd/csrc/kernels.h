@@ -105,7 +105,6 @@ struct AttnArgs {
     float* out;             // [heads][head_dim]
     int heads, kv_heads, head_dim, rope_half, context, kv_fp16;
 };
-int attn_chunk(int heads, int kv_heads);
 int attn_max_chunks(int heads, int kv_heads, int context);
 bool attn_supported(int heads, int kv_heads, int head_dim);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
