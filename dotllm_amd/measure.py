@@ -5,7 +5,7 @@ counter calibration run.
                                             # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
   python3 -m dotllm_amd.measure peak        # streaming read / write bandwidth
   python3 -m dotllm_amd.measure gemv        # isolated Q4_K / Q6_K GEMVs at the 7B shapes,
-                                            # weights cycled through >= 396 MB of copies
+                                            # weights cycled through >= 512 MB of copies
   python3 -m dotllm_amd.measure prefill-gemm   # batched Q4_K GEMM 2048 x 14336 x 4096 (MatMul
                                                # with 2048 activation rows), 3 calls
 """
@@ -36,9 +36,10 @@ def stream_peak_gbps(backend: HipBackend, nbytes: int = 1 << 30, iters: int = 10
 
 # (type, rows, cols, copies): Q4_K 4096x4096, 14336x4096, 4096x14336, the
 # 7B gate+up pair as one 28672x4096 matrix, Q+K (5120x4096), and the Q6_K
-# LM head and attn_v; copies chosen so every pass reads >= 396 MB.
-GEMV_SHAPES = [(12, 4096, 4096, 48), (12, 14336, 4096, 14), (12, 4096, 14336, 14), (12, 28672, 4096, 6),
-               (12, 5120, 4096, 36), (14, 32000, 4096, 4), (14, 1024, 4096, 120)]
+# LM head and attn_v; copies chosen so every pass reads >= 512 MB (twice the
+# 256 MB MALL, so no launch finds its weights there).
+GEMV_SHAPES = [(12, 4096, 4096, 55), (12, 14336, 4096, 16), (12, 4096, 14336, 16), (12, 28672, 4096, 8),
+               (12, 5120, 4096, 44), (14, 32000, 4096, 5), (14, 1024, 4096, 150)]
 
 
 def gemv_bench(backend: HipBackend, iters: int = 200) -> list:
