@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of the llmdot ("dotllm") managed decode path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * TEST INFRASTRUCTURE ONLY.  This library computes the expected values for the HIP
  * implementation in dotllm_amd/.  Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load it, and only to compute expected
  * values or to time the reference algorithm on the host.  The product never

@@ -2,8 +2,8 @@
 
 The oracle is the CPU restatement of the reference's managed decode path
 (see oracle.h).  Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg may import this module, and only as the checker or the timed
-CPU baseline.  Build it with ``make -C oracle`` (gcc, -ffp-contract=off).
+cpu_baseline leg may import this module, and only to compute expected values
+or as the timed CPU baseline.  Build it with ``make -C oracle`` (gcc, -ffp-contract=off).
 """
 from __future__ import annotations
 

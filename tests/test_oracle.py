@@ -1,5 +1,5 @@
 """Pins the oracle (oracle/oracle.c, the CPU restatement of the reference's
-managed decode path) before it is trusted as the GPU path's checker.
+managed decode path) before it is trusted as the GPU path's reference.
 
 Sources of truth, in order: the reference's own known-answer tests (cited by
 file:line under tests/Llmdot.Core.Tests), blocks built field by field with an
