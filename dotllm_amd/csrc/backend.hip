@@ -1312,10 +1312,9 @@ extern "C" int32_t llmdot_hip_model_step_bytes(llmdot_hip_model* m, int32_t posi
 extern "C" int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* m, int32_t n, uint64_t seed) {
     if (!m) return fail(LLMDOT_E_INVALID, "null model");
     if (n < 0 || n > m->d.context) return fail(LLMDOT_E_RANGE, "fill length outside the KV cache");
-    const size_t elt = m->d.kv_fp16 ? 2 : 4;
-    const size_t count = m->kv_layer_bytes * m->d.layers / elt;
-    HIPCHK(launch_fill_random_half(m->kcache, count, seed, m->d.kv_fp16, m->ctx->stream));
-    HIPCHK(launch_fill_random_half(m->vcache, count, seed ^ 0x5DEECE66Dull, m->d.kv_fp16, m->ctx->stream));
+    const auto& d = m->d;
+    HIPCHK(launch_kv_fill(m->kcache, 0, d.layers, d.kv_heads, d.context, d.head_dim, n, seed, d.kv_fp16, m->ctx->stream));
+    HIPCHK(launch_kv_fill(m->vcache, 1, d.layers, d.kv_heads, d.context, d.head_dim, n, seed, d.kv_fp16, m->ctx->stream));
     HIPCHK(hipStreamSynchronize(m->ctx->stream));
     return 0;
 }

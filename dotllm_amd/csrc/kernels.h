@@ -86,7 +86,10 @@ hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s)
 hipError_t launch_stream_probe(void* buf, size_t nbytes, int mode, uint32_t* sink, hipStream_t s);
 // Position bookkeeping for a captured decode step.
 hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s);
-hipError_t launch_fill_random_half(void* dst, size_t n, uint64_t seed, int fp16, hipStream_t s);
+// Seeded KV contents at positions [0, n) of one cache (kind 0 = K, 1 = V); the values
+// depend only on (seed, layer, kind, position, element).
+hipError_t launch_kv_fill(uint8_t* cache, int kind, int layers, int kv_heads, int context, int hd, int n,
+                          uint64_t seed, int fp16, hipStream_t s);
 
 // ---- attention.hip ----
 struct AttnArgs {

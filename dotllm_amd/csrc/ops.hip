@@ -179,15 +179,34 @@ __global__ __launch_bounds__(WG) void stream_write_kernel(uint4* __restrict__ p,
     if (i < n) p[i] = make_uint4((uint32_t)i, 1u, 2u, 3u);
 }
 
-__global__ void fill_random_kernel(void* dst, size_t n, uint64_t seed, int fp16) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        uint64_t z = seed + 0x9E3779B97F4A7C15ull * (i + 1);
-        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-        z ^= z >> 31;
-        const float u = ((float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f) - 0.5f) * 3.0f;
-        if (fp16) reinterpret_cast<_Float16*>(dst)[i] = (_Float16)u;
-        else reinterpret_cast<float*>(dst)[i] = u;
+// Seeded KV contents: element e (= kv head * head_dim + d) of the K (kind 0) or
+// V (kind 1) row of (layer, pos) is a function of (seed, layer, kind, pos, e)
+// alone (a SplitMix64 finaliser over the packed key, 24 bits scaled to
+// [-1.5, 1.5)), so any cache layout or capacity holds the same values.
+__device__ __forceinline__ float kv_fill_value(uint64_t seed, int layer, int kind, int pos, int e) {
+#pragma clang fp contract(off)
+    const uint64_t key = ((uint64_t)(2 * layer + kind) << 44) | ((uint64_t)pos << 20) | (uint64_t)e;
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (key + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return ((float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f) - 0.5f) * 3.0f;
+}
+
+// Positions [0, n) of a [layer][kv head][context][head_dim] cache.
+__global__ void kv_fill_kernel(uint8_t* cache, int kind, int layers, int kv_heads, int context, int hd, int n,
+                               uint64_t seed, int fp16) {
+    const size_t total = (size_t)layers * kv_heads * n * hd;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int d = (int)(i % hd);
+        size_t r = i / hd;
+        const int pos = (int)(r % n);
+        r /= n;
+        const int kvh = (int)(r % kv_heads), layer = (int)(r / kv_heads);
+        const float u = kv_fill_value(seed, layer, kind, pos, kvh * hd + d);
+        const size_t off = (((size_t)layer * kv_heads + kvh) * context + pos) * hd + d;
+        if (fp16) reinterpret_cast<_Float16*>(cache)[off] = (_Float16)u;
+        else reinterpret_cast<float*>(cache)[off] = u;
     }
 }
 
@@ -252,10 +271,13 @@ hipError_t launch_set_scalar(int32_t* dst, int32_t v, hipStream_t s) {
     set_scalar_kernel<<<1, 1, 0, s>>>(dst, v);
     return hipGetLastError();
 }
-hipError_t launch_fill_random_half(void* dst, size_t n, uint64_t seed, int fp16, hipStream_t s) {
-    if (n == 0) return hipSuccess;
-    size_t g = (n + WG - 1) / WG;
-    fill_random_kernel<<<(unsigned)(g > 65536 ? 65536 : g), WG, 0, s>>>(dst, n, seed, fp16);
+hipError_t launch_kv_fill(uint8_t* cache, int kind, int layers, int kv_heads, int context, int hd, int n,
+                          uint64_t seed, int fp16, hipStream_t s) {
+    if (layers <= 0 || kv_heads <= 0 || hd <= 0 || n <= 0 || n > context) return n == 0 ? hipSuccess : hipErrorInvalidValue;
+    const size_t total = (size_t)layers * kv_heads * n * hd;
+    const size_t g = (total + WG - 1) / WG;
+    kv_fill_kernel<<<(unsigned)(g > 65536 ? 65536 : g), WG, 0, s>>>(cache, kind, layers, kv_heads, context, hd, n, seed,
+                                                                     fp16);
     return hipGetLastError();
 }
 

@@ -241,8 +241,13 @@ int32_t llmdot_hip_model_time_decode(llmdot_hip_model* model, int32_t first_toke
 /* Algorithmic HBM bytes of one decode step at `position`: quantized weights read
  * once + the KV rows read + one embedding row. */
 int32_t llmdot_hip_model_step_bytes(llmdot_hip_model* model, int32_t position, double* bytes);
-/* Fills KV positions [0, n) with seeded values (timing at a given context without
- * running the prompt). */
+/* Fills KV positions [0, n) with seeded values (timing and parity at a given
+ * context without running the prompt).  Element e (kv head * head_dim + d) of
+ * the K (kind 0) or V (kind 1) row of (layer, pos) is
+ *   key = (2 layer + kind) << 44 | pos << 20 | e,  z = SplitMix64 finaliser of
+ *   seed + 0x9E3779B97F4A7C15 (key + 1),  value = ((z >> 40) / 2^24 - 0.5) * 3,
+ * stored in the cache's element type (fp16: round to nearest even).  No
+ * reference counterpart: a test and timing aid. */
 int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* model, int32_t n, uint64_t seed);
 
 /* ---- GGUF tooling: reference-layout quantizers and seeded synthetic weights

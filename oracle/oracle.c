@@ -1436,20 +1436,28 @@ int orc_generate(orc_model* m, const int* prompt, int n_prompt, int max_tokens, 
     return 0;
 }
 
+/* Seeded KV contents (no reference counterpart; timing and long-context
+ * parity): element e of the K (kind 0) or V (kind 1) row of (layer, pos) is a
+ * SplitMix64 finaliser of the packed key, 24 bits scaled to [-1.5, 1.5) -- the
+ * same values llmdot_hip_model_kv_fill_random writes. */
+static float kv_fill_value(uint64_t seed, int layer, int kind, int pos, int e) {
+    uint64_t key = ((uint64_t)(2 * layer + kind) << 44) | ((uint64_t)pos << 20) | (uint64_t)e;
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (key + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return ((float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f) - 0.5f) * 3.0f;
+}
+
 int orc_kv_fill_random(orc_model* m, int n, uint64_t seed) {
-    if (n > m->cache_ctx) return -2;
+    if (n < 0 || n > m->cache_ctx) return -2;
     int kvdim = m->cfg.kv_heads * m->cfg.head_dim;
-    uint64_t s = seed ? seed : 0x9E3779B97F4A7C15ull;
     for (int l = 0; l < m->cfg.layers; l++)
         for (int p = 0; p < n; p++)
-            for (int d = 0; d < kvdim; d++) {
-                size_t i = ((size_t)l * m->cache_ctx + p) * kvdim + d;
-                s ^= s << 13; s ^= s >> 7; s ^= s << 17;
-                float u = (float)((s >> 40) & 0xFFFFFF) / 16777216.0f - 0.5f;
-                m->kcache[i] = kv_store(m, u * 3.0f);
-                s ^= s << 13; s ^= s >> 7; s ^= s << 17;
-                u = (float)((s >> 40) & 0xFFFFFF) / 16777216.0f - 0.5f;
-                m->vcache[i] = kv_store(m, u * 3.0f);
+            for (int e = 0; e < kvdim; e++) {
+                size_t i = ((size_t)l * m->cache_ctx + p) * kvdim + e;
+                m->kcache[i] = kv_store(m, kv_fill_value(seed, l, 0, p, e));
+                m->vcache[i] = kv_store(m, kv_fill_value(seed, l, 1, p, e));
             }
     return 0;
 }

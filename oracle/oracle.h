@@ -109,7 +109,8 @@ int orc_process_token(orc_model* m, int token, int position, float* logits);
  * sampled token was taken from.  eos < 0 disables the EOS stop. */
 int orc_generate(orc_model* m, const int* prompt, int n_prompt, int max_tokens,
                  int eos, int* tokens_out, int* n_out, float* logits_out);
-/* Fills KV positions [0, n) with N(0,1)-ish values (timing only). */
+/* Fills KV positions [0, n) with the seeded values llmdot_hip_model_kv_fill_random
+ * writes (timing and long-context parity). */
 int orc_kv_fill_random(orc_model* m, int n, uint64_t seed);
 /* Copies one KV slot (kvDim floats each). */
 int orc_kv_read(const orc_model* m, int layer, int position, float* k, float* v);

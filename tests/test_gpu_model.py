@@ -170,3 +170,53 @@ def test_mistral7b_steps(hip, oracle_threads):
 def test_phi3mini_steps(hip, oracle_threads):
     """Phi-3-mini shape, MHA head_dim 96, Q6_K/Q8_0 mix."""
     _big_model_check(hip, "phi3mini", 4, 4, 16, DEEP_LOGIT_TOL)
+
+
+@pytest.mark.parametrize("kv_fp16", [False, True])
+def test_kv_fill_matches_oracle(hip, tiny_image, kv_fp16):
+    """The seeded KV fill writes the oracle's values bit for bit (fp16: the
+    same round-to-nearest-even), at positions [0, n) only."""
+    ref = O.Model(tiny_image, kv_fp16=kv_fp16, context=96)
+    ref.kv_fill_random(80, seed=5)
+    eng = _engine(hip, tiny_image, kv_fp16, context=96)
+    eng.kv_fill_random(80, seed=5)
+    for layer, pos in ((0, 0), (1, 41), (3, 79)):
+        gk, gv = eng.kv_read(layer, pos)
+        rk, rv = ref.kv_read(layer, pos)
+        assert np.array_equal(gk, rk) and np.array_equal(gv, rv), (layer, pos)
+    ref.close()
+    eng.dispose()
+
+
+@pytest.fixture(scope="module")
+def mistral7b_long_image():
+    return synth.build_image("mistral7b", seed=1234, context=4200)
+
+
+@pytest.mark.parametrize("ctx,kv_fp16", [(512, True), (2048, True), (4096, True), (4096, False)])
+def test_mistral7b_long_context(hip, oracle_threads, mistral7b_long_image, ctx, kv_fp16):
+    """The headline decode workload at its contexts: 7B shape, KV positions
+    [0, ctx) filled with the same seeded values on both sides, then 3 steps
+    from position ctx, teacher-forced on the oracle's greedy tokens.  Logits
+    within the 32-layer bound at every step; the same argmax wherever the
+    oracle's top-2 gap is at least NEAR_TIE."""
+    img = mistral7b_long_image
+    cap = ctx + 8
+    ref = O.Model(img, kv_fp16=kv_fp16, context=cap)
+    ref.kv_fill_random(ctx, seed=11)
+    eng = _engine(hip, img, kv_fp16, context=cap)
+    eng.kv_fill_random(ctx, seed=11)
+    tol = max(FP16_KV_LOGIT_TOL, DEEP_LOGIT_TOL) if kv_fp16 else DEEP_LOGIT_TOL
+    tok, errs = 1, []
+    for pos in range(ctx, ctx + 3):
+        rl = ref.process_token(tok, pos)
+        gl = eng.process_token(tok, pos)
+        errs.append(float(np.max(np.abs(gl - rl))))
+        top2 = np.sort(rl)[-2:]
+        if top2[1] - top2[0] >= NEAR_TIE:
+            assert int(np.argmax(gl)) == int(np.argmax(rl)), (ctx, pos)
+        tok = int(np.argmax(rl))
+    ref.close()
+    eng.dispose()
+    print(f"mistral7b ctx {ctx} kv_fp16={kv_fp16}: max |dlogit| per step {['%.3e' % e for e in errs]}")
+    assert max(errs) <= tol, errs

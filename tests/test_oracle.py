@@ -12,7 +12,7 @@ import math
 import numpy as np
 import pytest
 
-from dotllm_amd import BF16, F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0
+from dotllm_amd import BF16, F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, synth
 from oracle import oracle as O
 
 
@@ -348,3 +348,36 @@ def test_rope_is_a_rotation():
         assert abs(abs(a) - abs(b)) < 1e-5
         ang = pos / base ** (2 * i / hd)
         assert abs(b - a * complex(math.cos(ang), math.sin(ang))) < 2e-4 * max(1, abs(a))
+
+
+def _kv_fill_closed_form(seed, layer, kind, pos, e):
+    """The documented seeded KV value (llmdot_hip.h, llmdot_hip_model_kv_fill_random)."""
+    mask = (1 << 64) - 1
+    key = ((2 * layer + kind) << 44) | (pos << 20) | e
+    z = (seed + 0x9E3779B97F4A7C15 * (key + 1)) & mask
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+    z ^= z >> 31
+    return (np.float32(z >> 40) * np.float32(1.0 / 16777216.0) - np.float32(0.5)) * np.float32(3.0)
+
+
+@pytest.mark.parametrize("kv_fp16", [False, True])
+def test_kv_fill_closed_form(kv_fp16):
+    """The oracle's seeded KV fill is the documented function of (seed, layer,
+    kind, position, element), so a cache of any layout or capacity filled by
+    the HIP library holds the same values (the long-context parity tests rely
+    on it).  Positions past n stay untouched (zero)."""
+    img = synth.build_image("tiny", seed=1234, context=64)
+    m = O.Model(img, kv_fp16=kv_fp16, context=64)
+    m.kv_fill_random(40, seed=3)
+    for layer, pos in ((0, 0), (2, 37), (3, 39)):
+        k, v = m.kv_read(layer, pos)
+        for kind, got in ((0, k), (1, v)):
+            want = np.array([_kv_fill_closed_form(3, layer, kind, pos, e) for e in range(got.size)], np.float32)
+            if kv_fp16:
+                want = want.astype(np.float16).astype(np.float32)
+            assert np.array_equal(got, want), (layer, pos, kind)
+    k, v = m.kv_read(1, 40)
+    assert not k.any() and not v.any()
+    assert float(np.max(np.abs(m.kv_read(2, 5)[0]))) <= 1.5
+    m.close()
