@@ -100,6 +100,8 @@ class HipBackend:
         _call(lib().llmdot_hip_upload_weight(self._ctx, key.encode(), ggml_type, ptr(data), data.nbytes, rows, cols))
 
     def release_weight(self, key: str) -> None:
+        if not self._ctx:   # disposed: the context released (or will release) every weight
+            return
         _call(lib().llmdot_hip_release_weight(self._ctx, key.encode()))
 
     def has_weight(self, key: str) -> bool:

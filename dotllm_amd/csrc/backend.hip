@@ -95,6 +95,10 @@ struct llmdot_hip_ctx {
     // from and joined back into `stream` with events
     hipStream_t side[2] = {nullptr, nullptr};
     hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
+    // models created on this context and not yet destroyed; llmdot_hip_destroy
+    // with models alive defers the release to the last model's destroy
+    int models = 0;
+    bool closing = false;
 };
 
 namespace {
@@ -178,8 +182,8 @@ extern "C" int32_t llmdot_hip_create(int32_t device, llmdot_hip_ctx** out) {
     return 0;
 }
 
-extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
-    if (!ctx) return 0;
+namespace {
+void ctx_release(llmdot_hip_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->weights) (void)hipFree(kv.second.dev);
@@ -198,6 +202,16 @@ extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
     if (ctx->fork) (void)hipEventDestroy(ctx->fork);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
+}
+}  // namespace
+
+extern "C" int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx) {
+    if (!ctx) return 0;
+    if (ctx->models > 0) {   // its models still use the stream and weights
+        ctx->closing = true;
+        return 0;
+    }
+    ctx_release(ctx);
     return 0;
 }
 
@@ -974,11 +988,13 @@ bool use_batched_prefill(const llmdot_hip_model* m, int n) {
 
 extern "C" int32_t llmdot_hip_model_destroy(llmdot_hip_model* m) {
     if (!m) return 0;
-    (void)hipSetDevice(m->ctx->device);
-    (void)hipStreamSynchronize(m->ctx->stream);
+    llmdot_hip_ctx* ctx = m->ctx;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     for (void* p : m->owned) (void)hipFree(p);
     delete m;
+    if (--ctx->models == 0 && ctx->closing) ctx_release(ctx);
     return 0;
 }
 
@@ -994,8 +1010,10 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     if (!attn_supported(d.heads, d.kv_heads, d.head_dim))
         return fail(LLMDOT_E_UNSUPPORTED, "attention shape not supported (head_dim 64/96/128, group 1/2/4/8)");
     if (int rc = ensure_device(ctx)) return rc;
+    if (ctx->closing) return fail(LLMDOT_E_INVALID, "the context has been destroyed");
     auto* m = new llmdot_hip_model();
     m->ctx = ctx;
+    ctx->models++;   // every path out (llmdot_hip_model_destroy included) balances this
     m->d = d;
     m->prefix = d.key_prefix ? d.key_prefix : "";
     m->d.key_prefix = nullptr;

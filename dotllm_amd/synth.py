@@ -13,9 +13,12 @@ Shapes:
   llama1b   llama  d2048 L16 H32/8  hd64  F8192  V128256  Q4_K_M mix, theta 500000
   mistral7b llama  d4096 L32 H32/8  hd128 F14336 V32000   Q4_K_M mix, theta 10000
   phi3mini  phi3   d3072 L32 H32/32 hd96  F8192  V32064   Q6_K/Q8_0 mix, theta 10000
+  small5    llama  d1024 L4  H8/4   hd128 F2816  V32000   Q5_K_M mix, theta 10000
 Q4_K_M mix: Q6_K for output.weight and every attn_v, Q4_K for every other
 matrix including token_embd.  The phi3mini mix: Q6_K for token_embd, output,
 attn_v and ffn_down; Q8_0 for attn_q, attn_k, attn_output, ffn_gate, ffn_up.
+Q5_K_M mix: as Q4_K_M with Q5_K in place of Q4_K (small5 exercises Q5_K and a
+query-group size of 2 end to end).
 """
 from __future__ import annotations
 
@@ -37,6 +40,8 @@ SPECS = {
                       vocab=32000, rope_base=10000.0, context=4608, mix="q4_k_m"),
     "phi3mini": dict(arch="phi3", hidden=3072, layers=32, heads=32, kv_heads=32, head_dim=96, ffn=8192,
                      vocab=32064, rope_base=10000.0, context=2560, mix="phi3"),
+    "small5": dict(arch="llama", hidden=1024, layers=4, heads=8, kv_heads=4, head_dim=128, ffn=2816, vocab=32000,
+                   rope_base=10000.0, context=512, mix="q5_k_m"),
 }
 
 
@@ -47,6 +52,8 @@ def tensor_type(mix: str, name: str) -> int:
         return Q8_0
     if mix == "q4_k_m":
         return Q6_K if (name == "output.weight" or ".attn_v." in name) else Q4_K
+    if mix == "q5_k_m":
+        return Q6_K if (name == "output.weight" or ".attn_v." in name) else _lib.Q5_K
     if mix == "phi3":
         if name in ("token_embd.weight", "output.weight") or ".attn_v." in name or ".ffn_down." in name:
             return Q6_K

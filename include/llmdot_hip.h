@@ -48,6 +48,9 @@ typedef struct llmdot_hip_model llmdot_hip_model;
 const char* llmdot_hip_last_error(void);
 int32_t llmdot_hip_device_count(int32_t* count);
 int32_t llmdot_hip_create(int32_t device, llmdot_hip_ctx** out);
+/* Releases the context.  With models created on it still alive the release
+ * is deferred until the last of them is destroyed (the context accepts no new
+ * models meanwhile), so destroy order mistakes leave no dangling handle. */
 int32_t llmdot_hip_destroy(llmdot_hip_ctx* ctx);
 
 typedef struct llmdot_hip_device_info {

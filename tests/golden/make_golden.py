@@ -14,6 +14,13 @@ Outputs (small, committed):
   tiny_greedy.json  tiny Q8_0 model (seed 1234), 16-token prompt (seed 7):
                   32 greedy tokens and, per step, the top-5 logits and the
                   logits' sum and sum of squares
+
+  python tests/golden/make_golden.py mistral7b    (about 20 minutes on 8 cores)
+
+  mistral7b_greedy64.json  7B-shape Q4_K_M model (seed 1234), 16-token prompt
+                  (seed 7), with fp16 and with fp32 KV: 64 greedy tokens and,
+                  per step, the top-16 logits, the top-2 gap, and the logits'
+                  mean and root mean square; plus a fingerprint of the image
 """
 import json
 import os
@@ -80,5 +87,43 @@ def main():
     print("wrote dequant.npz, gemv.npz, tiny_greedy.json")
 
 
+def image_fingerprint(img) -> str:
+    """SHA-256 over 4 KiB taken every 4 MiB of the image, plus its length."""
+    import hashlib
+    b = np.asarray(img, dtype=np.uint8).reshape(-1)
+    h = hashlib.sha256(str(b.size).encode())
+    for off in range(0, b.size, 4 << 20):
+        h.update(b[off:off + 4096].tobytes())
+    return h.hexdigest()
+
+
+def mistral7b_greedy64():
+    img = synth.build_image("mistral7b", seed=1234, context=96)
+    prompt = synth.prompt(32000, 16, seed=7)
+    O.set_threads(os.cpu_count() or 1)
+    runs = []
+    for kv_fp16 in (True, False):
+        m = O.Model(img, kv_fp16=kv_fp16, context=96)
+        toks, logits = m.generate(prompt, 64, return_logits=True)
+        m.close()
+        steps = []
+        for row in logits:
+            top = np.argsort(row)[::-1][:16]
+            r64 = row.astype(np.float64)
+            steps.append({"top16": [int(i) for i in top], "top16_logits": [float(row[i]) for i in top],
+                          "gap": float(row[top[0]] - row[top[1]]), "mean": float(r64.mean()),
+                          "rms": float(np.sqrt(np.mean(r64 * r64)))})
+        runs.append({"kv_fp16": kv_fp16, "tokens": [int(t) for t in toks], "steps": steps})
+        print(f"kv_fp16={kv_fp16}: {len(toks)} tokens", flush=True)
+    with open(os.path.join(HERE, "mistral7b_greedy64.json"), "w") as f:
+        json.dump({"model": "mistral7b", "weights_seed": 1234, "image_context": 96, "prompt_seed": 7,
+                   "prompt": [int(t) for t in prompt], "image_fingerprint": image_fingerprint(img),
+                   "runs": runs}, f, indent=1)
+    print("wrote mistral7b_greedy64.json")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["mistral7b"]:
+        mistral7b_greedy64()
+    else:
+        main()

@@ -106,7 +106,7 @@ NEAR_TIE = 1e-2   # reference top-2 logit gap below which argmax may legitimatel
 DEEP_LOGIT_TOL = 5e-2
 
 
-def _big_model_check(hip, name, n_prompt, n_gen, ctx, tol32=LOGIT_TOL):
+def _big_model_check(hip, name, n_prompt, n_gen, ctx, tol32=LOGIT_TOL, near_tie32=NEAR_TIE):
     """GPU decode with fp32 KV against the pure reference (the spec's bars) and
     with fp16 KV against the reference with K/V rounded through fp16 on store.
 
@@ -117,7 +117,8 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, tol32=LOGIT_TOL):
     reference's first near-tie, with logits within tolerance up to that step;
     (2) teacher-forced on the reference's own tokens, every one of the n_gen
     steps must have logits within tolerance, and the same argmax wherever the
-    reference's top-2 gap is at least NEAR_TIE."""
+    reference's top-2 gap is at least NEAR_TIE (near_tie32 for the fp32-KV run,
+    which a model whose fp32 logits agree to ~1e-5 may set far lower)."""
     img = synth.build_image(name, seed=1234, context=ctx)
     spec = synth.SPECS[name]
     prompt = synth.prompt(spec["vocab"], n_prompt, seed=7)
@@ -127,7 +128,8 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, tol32=LOGIT_TOL):
         ref_toks, ref_logits = ref.generate(prompt, n_gen, return_logits=True)
         top2 = np.sort(ref_logits, axis=1)[:, -2:]
         gap = top2[:, 1] - top2[:, 0]
-        ties = np.where(gap < NEAR_TIE)[0]
+        near_tie = NEAR_TIE if kv_fp16 else near_tie32
+        ties = np.where(gap < near_tie)[0]
         well_posed = int(ties[0]) if ties.size else n_gen   # steps before the first near-tie
         eng = _engine(hip, img, kv_fp16, context=ctx)
         toks, logits = eng.generate_all(prompt, greedy(n_gen), return_logits=True)
@@ -146,13 +148,14 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, tol32=LOGIT_TOL):
             if pos >= n_prompt - 1:
                 step = pos - (n_prompt - 1)
                 errs.append(float(np.max(np.abs(gl - rl))))
-                if gap[step] >= NEAR_TIE:
+                if gap[step] >= near_tie:
                     assert int(np.argmax(gl)) == int(np.argmax(rl)), (kv_fp16, step)
         ref.close()
         eng.dispose()
-        print(f"{name} kv_fp16={kv_fp16}: free-running tokens identical for {well_posed} steps "
-              f"(first reference near-tie), max |dlogit| {err_free:.3e}; teacher-forced {len(errs)} steps "
-              f"max |dlogit| {max(errs):.3e}")
+        same = next((i for i, (a, b) in enumerate(zip(toks, ref_toks)) if a != b), min(len(toks), len(ref_toks)))
+        print(f"{name} kv_fp16={kv_fp16}: free-running tokens identical for {same} steps (required: {well_posed}, "
+              f"the first reference gap below {near_tie:g}), max |dlogit| {err_free:.3e}; teacher-forced "
+              f"{len(errs)} steps max |dlogit| {max(errs):.3e}")
         assert err_free <= tol, (kv_fp16, err_free)
         assert max(errs) <= tol, (kv_fp16, max(errs))
 
@@ -160,6 +163,12 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, tol32=LOGIT_TOL):
 def test_llama1b_greedy_64(hip, oracle_threads):
     """1B-shape Q4_K_M (Q6_K head + attn_v): 8-token prompt, 64 greedy tokens."""
     _big_model_check(hip, "llama1b", 8, 64, 80)
+
+
+def test_small5_greedy_64(hip, oracle_threads):
+    """Q5_K_M mix (Q5_K + Q6_K attn_v/head), query groups of 2 (8/4 heads),
+    head_dim 128: 8-token prompt, 64 greedy tokens."""
+    _big_model_check(hip, "small5", 8, 64, 80, near_tie32=1e-4)
 
 
 def test_mistral7b_steps(hip, oracle_threads):
@@ -220,3 +229,87 @@ def test_mistral7b_long_context(hip, oracle_threads, mistral7b_long_image, ctx, 
     eng.dispose()
     print(f"mistral7b ctx {ctx} kv_fp16={kv_fp16}: max |dlogit| per step {['%.3e' % e for e in errs]}")
     assert max(errs) <= tol, errs
+
+
+def test_context_destroyed_before_model(tiny_image):
+    """Disposing the backend while an engine still uses it defers the release
+    to the engine's dispose: the engine keeps working and nothing dangles."""
+    from dotllm_amd.backend import HipBackend
+    be = HipBackend(0)
+    eng = _engine(be, tiny_image, True)
+    ref = eng.process_token(1, 0)
+    be.dispose()
+    again = eng.process_token(1, 0)
+    assert np.array_equal(ref, again)
+    eng.dispose()
+
+
+def _golden(name):
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+    with open(path) as f:
+        return json.load(f)
+
+
+# fp16 KV over 64 steps of the 32-layer 7B shape: the storage format alone
+# moves the oracle's own logits by up to 0.103 (its fp16-KV against its fp32-KV
+# run, top-16 logits, first 54 steps, recorded in the fixture), and a 1e-7
+# input difference flips an fp16 rounding now and then, so GPU and oracle with
+# the same format are held to that scale.
+FP16_KV_LONG_TOL = 1e-1
+
+
+def test_mistral7b_greedy64_golden(hip):
+    """The headline model, 64 greedy tokens after a 16-token prompt, against
+    the oracle's run frozen in tests/golden/mistral7b_greedy64.json (written by
+    tests/golden/make_golden.py; about 20 CPU-minutes, too slow to repeat
+    here), with fp16 and with fp32 KV.  Free-running: tokens identical up to
+    the oracle's first near-tie.  Teacher-forced on the oracle's tokens, every
+    step: logits at the oracle's top 16 within the bound, mean and RMS of the
+    whole vector within it (both are 1-Lipschitz in the max norm), and the
+    same argmax wherever the oracle's top-2 gap is at least NEAR_TIE."""
+    from golden.make_golden import image_fingerprint
+    g = _golden("mistral7b_greedy64.json")
+    img = synth.build_image(g["model"], seed=g["weights_seed"], context=g["image_context"])
+    assert image_fingerprint(img) == g["image_fingerprint"], "the synthetic generator changed: rewrite the fixture"
+    prompt = g["prompt"]
+    assert synth.prompt(32000, len(prompt), seed=g["prompt_seed"]) == prompt
+    n_gen = len(g["runs"][0]["tokens"])
+    for run in g["runs"]:
+        kv_fp16 = run["kv_fp16"]
+        tol = FP16_KV_LONG_TOL if kv_fp16 else DEEP_LOGIT_TOL
+        steps = run["steps"]
+        gaps = np.array([st["gap"] for st in steps])
+        ties = np.where(gaps < NEAR_TIE)[0]
+        well_posed = int(ties[0]) if ties.size else n_gen
+
+        def err_of(logits, st):
+            idx = np.array(st["top16"])
+            l64 = logits.astype(np.float64)
+            return max(float(np.max(np.abs(logits[idx] - np.array(st["top16_logits"], np.float32)))),
+                       abs(float(l64.mean()) - st["mean"]), abs(float(np.sqrt(np.mean(l64 * l64))) - st["rms"]))
+
+        eng = _engine(hip, img, kv_fp16, context=len(prompt) + n_gen + 8)
+        try:
+            toks, logits = eng.generate_all(prompt, greedy(n_gen), return_logits=True)
+            same = next((i for i, (a, b) in enumerate(zip(toks, run["tokens"])) if a != b), n_gen)
+            free = [err_of(logits[i], steps[i]) for i in range(min(well_posed + 1, n_gen))]
+            eng.reset()
+            stream = list(prompt) + list(run["tokens"])
+            forced, flips = [], []
+            for pos, tk in enumerate(stream[:len(prompt) + n_gen - 1]):
+                gl = eng.process_token(int(tk), pos)
+                if pos >= len(prompt) - 1:
+                    i = pos - (len(prompt) - 1)
+                    forced.append(err_of(gl, steps[i]))
+                    if steps[i]["gap"] >= NEAR_TIE and int(np.argmax(gl)) != steps[i]["top16"][0]:
+                        flips.append(i)
+        finally:
+            eng.dispose()
+        print(f"mistral7b greedy64 kv_fp16={kv_fp16}: free-running tokens identical for {same} steps "
+              f"(required: {well_posed}, the oracle's first gap below {NEAR_TIE:g}), max error {max(free):.3e}; "
+              f"teacher-forced max error {max(forced):.3e} (step {int(np.argmax(forced))})")
+        assert same >= well_posed, kv_fp16
+        assert max(free) <= tol and max(forced) <= tol, kv_fp16
+        assert not flips, (kv_fp16, flips)

@@ -171,6 +171,14 @@ def test_prefill_llama1b(hip, oracle_threads):
         _prompt_check(hip, img, prompt, 96, kv_fp16, LOGIT_TOL, [0, 15], kv_tol=5e-2)
 
 
+def test_prefill_small5(hip, oracle_threads):
+    """Q5_K_M mix (Q5_K GEMMs on the batched path), GQA 8/4, head_dim 128."""
+    img = synth.build_image("small5", seed=1234, context=96)
+    prompt = synth.prompt(32000, 80, seed=7)
+    for kv_fp16 in (False, True):
+        _prompt_check(hip, img, prompt, 96, kv_fp16, LOGIT_TOL, [0, 3])
+
+
 def test_prefill_phi3mini(hip, oracle_threads):
     """Phi-3-mini shape: Q6_K/Q8_0, MHA, head_dim 96."""
     img = synth.build_image("phi3mini", seed=1234, context=32)
