@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <set>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -53,6 +54,7 @@ struct Weight {
     int64_t rows = 0, cols = 0;
     size_t nbytes = 0;
     uint8_t* dev = nullptr;
+    int pins = 0;   // live models reading it (their captured steps hold dev)
 };
 
 struct DevBuf {
@@ -135,7 +137,16 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
                                           std::to_string(need));
     auto it = ctx->weights.find(key);
     if (it != ctx->weights.end()) {
-        (void)hipFree(it->second.dev);
+        Weight& old = it->second;
+        if (old.pins > 0) {   // a model's captured step reads this buffer: new bytes in place only
+            if (old.type != type || old.rows != rows || old.cols != cols)
+                return fail(LLMDOT_E_INVALID, "weight '" + key + "' is in use by a model with another shape or type");
+            HIPCHK(hipStreamSynchronize(ctx->stream));
+            HIPCHK(hipMemcpy(old.dev, bytes, (size_t)need, hipMemcpyHostToDevice));
+            if (out) *out = &old;
+            return 0;
+        }
+        (void)hipFree(old.dev);
         ctx->weights.erase(it);
     }
     Weight w;
@@ -239,6 +250,7 @@ extern "C" int32_t llmdot_hip_release_weight(llmdot_hip_ctx* ctx, const char* ke
     if (!ctx || !key) return fail(LLMDOT_E_INVALID, "null argument");
     auto it = ctx->weights.find(key);
     if (it == ctx->weights.end()) return fail(LLMDOT_E_NOT_FOUND, std::string("Tensor '") + key + "' not found.");
+    if (it->second.pins > 0) return fail(LLMDOT_E_INVALID, std::string("Tensor '") + key + "' is in use by a model.");
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(it->second.dev);
@@ -633,6 +645,7 @@ struct LayerW {
 
 struct llmdot_hip_model {
     llmdot_hip_ctx* ctx = nullptr;
+    std::set<std::string> pinned;   // context weight keys this model reads
     llmdot_hip_model_desc d{};
     std::string prefix;
     std::vector<LayerW> L;
@@ -686,9 +699,13 @@ int dalloc(llmdot_hip_model* m, size_t n, void** p) {
     return 0;
 }
 
+// A context weight the model reads; it stays pinned (no release, no
+// reallocation) until the model is destroyed.
 const Weight* find_w(llmdot_hip_model* m, const std::string& name) {
     auto it = m->ctx->weights.find(m->prefix + name);
-    return it == m->ctx->weights.end() ? nullptr : &it->second;
+    if (it == m->ctx->weights.end()) return nullptr;
+    if (m->pinned.insert(it->first).second) it->second.pins++;
+    return &it->second;
 }
 
 int need_w(llmdot_hip_model* m, const std::string& name, int64_t rows, int64_t cols, const Weight** out) {
@@ -993,6 +1010,10 @@ extern "C" int32_t llmdot_hip_model_destroy(llmdot_hip_model* m) {
     (void)hipStreamSynchronize(ctx->stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     for (void* p : m->owned) (void)hipFree(p);
+    for (const auto& k : m->pinned) {
+        auto it = ctx->weights.find(k);
+        if (it != ctx->weights.end()) it->second.pins--;
+    }
     delete m;
     if (--ctx->models == 0 && ctx->closing) ctx_release(ctx);
     return 0;

@@ -65,9 +65,12 @@ int32_t llmdot_hip_get_device_info(llmdot_hip_ctx* ctx, llmdot_hip_device_info* 
 /* ---- persistent weights (the weightKey cache of MatMul, ICB:9; the Metal
  *      backend's UploadPersistentBytes("w_"+name), src/Llmdot.Metal/MetalBackend.cs:92-100).
  *      The bytes are the tensor's GGUF blocks, [rows][ByteCount(type, cols)],
- *      kept in HBM in that native layout.  Uploading an existing key replaces it. */
+ *      kept in HBM in that native layout.  Uploading an existing key replaces it;
+ *      a key a live model reads keeps its buffer: new bytes of the same type and
+ *      shape are copied in place, anything else is LLMDOT_E_INVALID. */
 int32_t llmdot_hip_upload_weight(llmdot_hip_ctx* ctx, const char* key, uint32_t ggml_type,
                                  const void* bytes, size_t nbytes, int64_t rows, int64_t cols);
+/* LLMDOT_E_INVALID while a live model reads the key. */
 int32_t llmdot_hip_release_weight(llmdot_hip_ctx* ctx, const char* key);
 int32_t llmdot_hip_has_weight(llmdot_hip_ctx* ctx, const char* key, int32_t* present);
 

@@ -244,6 +244,27 @@ def test_context_destroyed_before_model(tiny_image):
     eng.dispose()
 
 
+def test_weights_pinned_by_model(tiny_image):
+    """A weight a live model reads cannot be released or reallocated (its
+    captured step holds the buffer); same-shape bytes are copied in place."""
+    from dotllm_amd.backend import HipBackend
+    be = HipBackend(0)
+    lm = LoadedModel.load(tiny_image)
+    eng = InferenceEngine(lm, be, kv_fp16=True)
+    key = lm.key_prefix + "blk.0.attn_q.weight"
+    ref = eng.process_token(1, 0)
+    with pytest.raises(ValueError):
+        be.release_weight(key)
+    t = lm.tensor("blk.0.attn_q.weight")
+    with pytest.raises(ValueError):   # another shape
+        be.upload_weight(key, t.ggml_type, t.data, t.rows // 2, t.cols)
+    be.upload_weight(key, t.ggml_type, t.data, t.rows, t.cols)   # the same bytes, in place
+    assert np.array_equal(eng.process_token(1, 0), ref)
+    eng.dispose()
+    assert not be.has_weight(key)   # the last engine released the model's weights
+    be.dispose()
+
+
 def _golden(name):
     import json
     import os
