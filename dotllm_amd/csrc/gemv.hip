@@ -38,6 +38,7 @@
 #include "kernels.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 #include <type_traits>
 
@@ -446,14 +447,21 @@ __device__ __forceinline__ void run_sums(XF<NS>& x) {
 // loads (lanes past the row end read unit 0 and contribute 0): no branches,
 // so no load is serialised behind another.  Row i's per-quarter-wavefront
 // sums go to red_w[i][0..3].
-template <typename TT, int NB, typename RowPtr>
-__device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, RowPtr&& row_ptr, float (*red_w)[4]) {
+// HV > 1 (Q4_K only): the workgroup is HV halves over the same units; half 0
+// loads and quantises the activations and hands them to the other halves
+// through LDS (xq_s), so each activation byte leaves L2 once per HV x rows.
+template <typename TT, int NB, int HV = 1, typename RowPtr>
+__device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, RowPtr&& row_ptr, float (*red_w)[4],
+                                          bool own_x = true, uint32_t* xq_s = nullptr, int units = 0) {
     constexpr int RB = TT::RB;
     constexpr bool INT = std::is_same<TT, TQ4K>::value;
+    static_assert(HV == 1 || INT, "shared activations are quantised ones");
     const int lane = threadIdx.x & 63;
     XRaw xr;
-    if constexpr (INT) issue_x<32>(a, [&](int) { return uu * 32; }, xr);
-    else issue_x<TT::RUN>(a, [&](int run) { return TT::xoff(uu, run); }, xr);
+    if (own_x) {
+        if constexpr (INT) issue_x<32>(a, [&](int) { return uu * 32; }, xr);
+        else issue_x<TT::RUN>(a, [&](int run) { return TT::xoff(uu, run); }, xr);
+    }
     constexpr int D = TT::DEPTH;     // batches in flight
     typename TT::Raw buf[D][RB];
 #pragma unroll
@@ -462,14 +470,30 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, R
         for (int i = 0; i < RB; i++) TT::load(buf[k][i], row_ptr(k * RB + i), uu);
     __builtin_amdgcn_sched_barrier(0);
     float v[32];
-    finish_x(xr, has, v);
+    if (own_x) finish_x(xr, has, v);
 #pragma unroll
     for (int k = TT::PRE; k < NB && k < D; k++)
 #pragma unroll
         for (int i = 0; i < RB; i++) TT::load(buf[k][i], row_ptr(k * RB + i), uu);
     typename std::conditional<INT, XQ, XF<INT ? 1 : TT::NS>>::type x;
     if constexpr (INT) {
-        quantize32(v, x);
+        if (own_x) quantize32(v, x);
+        if constexpr (HV > 1) {
+            constexpr int XW = 4 * XQ_PLANES + 2;   // dwords per unit: planes, s, sum
+            if (own_x && has) {
+#pragma unroll
+                for (int j = 0; j < 4 * XQ_PLANES; j++) xq_s[j * units + uu] = x.pl[j];
+                xq_s[(XW - 2) * units + uu] = __float_as_uint(x.s);
+                xq_s[(XW - 1) * units + uu] = __float_as_uint(x.sum);
+            }
+            __syncthreads();
+            if (!own_x) {
+#pragma unroll
+                for (int j = 0; j < 4 * XQ_PLANES; j++) x.pl[j] = xq_s[j * units + uu];
+                x.s = __uint_as_float(xq_s[(XW - 2) * units + uu]);
+                x.sum = __uint_as_float(xq_s[(XW - 1) * units + uu]);
+            }
+        }
     } else {
 #pragma unroll
         for (int e = 0; e < 32; e++) x.v[e] = v[e];
@@ -498,21 +522,28 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, R
 // ---- the kernel -------------------------------------------------------------------
 // NB batches of RB dot rows; SwiGLU batches hold RB/2 gate then RB/2 up rows.
 // Segments of the second type T2 take NB2 <= NB batches per workgroup.
-template <uint32_t T, int EPI, int NB, bool NORM, uint32_t T2 = T, int NB2 = NB>
+// HV halves (HV_MAX_UNITS units at most) each take NB batches of the same units.
+constexpr int HV_MAX_UNITS = 256;
+
+template <uint32_t T, int EPI, int NB, bool NORM, uint32_t T2 = T, int NB2 = NB, int HV = 1>
 __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     using TT = typename TypeOf<T>::type;
     using TT2 = typename TypeOf<T2>::type;
     static_assert(TT2::RB == TT::RB, "mixed-type launches need equal batch geometry");
+    static_assert(HV == 1 || T2 == T, "halves are for single-type launches");
     constexpr int RB = TT::RB;
     constexpr bool SW = EPI == EPI_SWIGLU;
     constexpr int OPB = SW ? RB / 2 : RB;     // output rows per batch
-    constexpr int ROWS_WG = NB * OPB;
+    constexpr int ROWS_H = NB * OPB;          // output rows per half
+    constexpr int ROWS_WG = HV * ROWS_H;
     constexpr int NSUM = NB * RB;
     static_assert(ROWS_WG <= 64, "epilogue uses one wavefront");
     __shared__ float red[MAXW][NSUM][4];
     __shared__ float ssq[MAXW];
+    __shared__ uint32_t xq_s[HV > 1 ? (4 * XQ_PLANES + 2) * HV_MAX_UNITS : 1];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) / HV;   // waves per half
+    const int half = wave / nw, hw = wave - half * nw;
     // segment and first row of this workgroup
     int blk = blockIdx.x, si = 0;
     for (; si < a.nseg - 1; si++) {
@@ -527,24 +558,25 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     constexpr int SLAB = EPI == EPI_ADD ? (ROWS_WG % 8 == 0 ? 8 : ROWS_WG) : OPB;
     auto out_row = [&](int o) { return ((o / SLAB) * seg.wgs + blk) * SLAB + o % SLAB; };
     const int K = a.cols;
-    const int u = wave * 64 + lane;
+    const int u = hw * 64 + lane;
     const bool has = u < K / 32;
     const int uu = has ? u : 0;
     const bool second = T2 != T && seg.type == T2;   // uniform per workgroup
     static_assert(NB2 <= NB, "second-type segments take at most NB batches");
     const int rows_wg = second ? NB2 * OPB : ROWS_WG;
+    const int b0 = half * NB;   // this half's first batch of the workgroup
     const int64_t rbytes = second ? (int64_t)(K / block_elems(T2)) * block_bytes(T2)
                                   : (int64_t)(K / block_elems(T)) * block_bytes(T);
 
-    auto row_ptr = [&](int i) -> const uint8_t* {   // dot row i of this workgroup
-        const int b = i / RB, k = i % RB;
+    auto row_ptr = [&](int i) -> const uint8_t* {   // dot row i of this half
+        const int b = b0 + i / RB, k = i % RB;
         const uint8_t* base = seg.w;
         int r;
         if (SW) {
             r = out_row(b * OPB + (k % OPB));
             if (k >= OPB) base = seg.w2;
         } else {
-            r = out_row(i);
+            r = out_row(b * RB + k);
         }
         return base + (int64_t)(r < seg.rows ? r : 0) * rbytes;
     };
@@ -568,14 +600,14 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         }
     }
     if (T2 != T && second) gemv_rows<TT2, NB2>(a, uu, has, row_ptr, red[wave]);
-    else gemv_rows<TT, NB>(a, uu, has, row_ptr, red[wave]);
+    else gemv_rows<TT, NB, HV>(a, uu, has, row_ptr, red[wave], half == 0, xq_s, K / 32);
     if (NORM) {
         const int nq = K >> 3;
         float hsq = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) hsq += (int)threadIdx.x + k * (int)blockDim.x < nq ? sq[k] : 0.f;
         const float w = wave_sum(hsq);
-        if (lane == 0) ssq[wave] = w;
+        if (lane == 0) ssq[wave] = w;   // over every wave: each entry of a.ssq is read by one thread
     }
     __syncthreads();
     if (threadIdx.x >= 64) return;
@@ -586,17 +618,18 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     if (NORM) {
 #pragma clang fp contract(off)
         float ss = 0.f;
-        for (int w = 0; w < nw; w++) ss += ssq[w];
+        for (int w = 0; w < HV * nw; w++) ss += ssq[w];
         inv = 1.0f / sqrtf(ss / (float)K + a.eps);   // RmsNorm: 1 / sqrt(sum/n + eps)
     }
-    auto total = [&](int i) {
+    const int th = t / ROWS_H, tl = t - th * ROWS_H;   // half of output row t, and its row in the half
+    auto total = [&](int i) {   // dot i of half th over that half's waves
         float s = 0.f;
-        for (int w = 0; w < nw; w++) s += (red[w][i][0] + red[w][i][1]) + (red[w][i][2] + red[w][i][3]);
+        for (int w = th * nw; w < (th + 1) * nw; w++) s += (red[w][i][0] + red[w][i][1]) + (red[w][i][2] + red[w][i][3]);
         return s * inv;
     };
-    const int row = out_row(t);
+    const int b = tl / OPB, k = tl % OPB;
+    const int row = out_row((th * NB + b) * OPB + k);
     const bool valid = t < rows_wg && row < seg.rows;
-    const int b = t / OPB, k = t % OPB;
     if (EPI == EPI_STORE) {
         if (valid) seg.out[row] = total(b * RB + k);
     } else if (EPI == EPI_ADD) {
@@ -663,14 +696,16 @@ int type_rb(uint32_t t) {
     }
 }
 
-template <uint32_t T, int EPI, bool NORM>
+template <uint32_t T, int EPI, bool NORM, int HV = 1>
 hipError_t launch_te(const GemvArgs& a, int nb, int grid, int threads, hipStream_t s) {
     switch (nb) {
-    case 1: gemv_kernel<T, EPI, 1, NORM><<<grid, threads, 0, s>>>(a); break;
-    case 2: gemv_kernel<T, EPI, 2, NORM><<<grid, threads, 0, s>>>(a); break;
-    case 4: gemv_kernel<T, EPI, 4, NORM><<<grid, threads, 0, s>>>(a); break;
-    case 8: gemv_kernel<T, EPI, 8, NORM><<<grid, threads, 0, s>>>(a); break;
-    case 7: gemv_kernel<T, EPI, 7, NORM><<<grid, threads, 0, s>>>(a); break;
+    case 1: gemv_kernel<T, EPI, 1, NORM, T, 1, HV><<<grid, threads, 0, s>>>(a); break;
+    case 2: gemv_kernel<T, EPI, 2, NORM, T, 2, HV><<<grid, threads, 0, s>>>(a); break;
+    case 4: gemv_kernel<T, EPI, 4, NORM, T, 4, HV><<<grid, threads, 0, s>>>(a); break;
+    case 8:
+        if constexpr (HV * 8 * TypeOf<T>::type::RB <= 64) { gemv_kernel<T, EPI, 8, NORM, T, 8, HV><<<grid, threads, 0, s>>>(a); break; }
+        else return hipErrorInvalidValue;
+    case 7: gemv_kernel<T, EPI, 7, NORM, T, 7, HV><<<grid, threads, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -679,7 +714,14 @@ hipError_t launch_te(const GemvArgs& a, int nb, int grid, int threads, hipStream
 // Instantiated forms: STORE with or without RmsNorm, ADD without, SWIGLU and
 // ARGMAX with (the decode step's uses and the op-level MatMul).
 template <uint32_t T>
-hipError_t launch_t(int epi, const GemvArgs& a, int nb, int grid, int threads, hipStream_t s) {
+hipError_t launch_t(int epi, const GemvArgs& a, int nb, int grid, int threads, hipStream_t s, int hv = 1) {
+    if constexpr (T == GGML_Q4_K) {
+        if (hv == 2) {
+            if (epi == EPI_ADD) return launch_te<T, EPI_ADD, false, 2>(a, nb, grid, threads, s);
+            return hipErrorInvalidValue;
+        }
+    }
+    if (hv != 1) return hipErrorInvalidValue;
     switch (epi) {
     case EPI_STORE:
         return a.norm ? launch_te<T, EPI_STORE, true>(a, nb, grid, threads, s)
@@ -708,6 +750,15 @@ bool gemv_width_ok(uint32_t type, int cols) {
 
 // Wavefronts a launch should have at least (4 per CU: fewer, longer
 // workgroups amortise the activation loads); LLMDOT_GEMV_WAVES overrides it.
+// LLMDOT_GEMV_HALVES=0 keeps one half per workgroup (A/B timing and tests).
+static bool env_halves_off() {
+    static const bool off = [] {
+        const char* e = getenv("LLMDOT_GEMV_HALVES");
+        return e && strcmp(e, "0") == 0;
+    }();
+    return off;
+}
+
 static int target_waves() {
     static const int w = [] {
         const char* e = getenv("LLMDOT_GEMV_WAVES");
@@ -732,6 +783,16 @@ int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
     return nb;
 }
 
+// Halves per workgroup: 2 for Q4_K residual-add launches (the attention output
+// projection, 4096 x 4096 at the 7B shape: 6.48 -> 6.16 us) whose units fit the
+// shared activation buffer and whose two halves fit MAXW wavefronts.  The
+// larger STORE / SwiGLU GEMVs measured equal or slower with halves.
+int gemv_halves(uint32_t type, int epi, int cols, bool mixed) {
+    const int units = cols / 32, nw = (units + 63) / 64;
+    if (type != GGML_Q4_K || mixed || epi != EPI_ADD || env_halves_off()) return 1;
+    return units <= HV_MAX_UNITS && 2 * nw <= MAXW ? 2 : 1;
+}
+
 int gemv_rows_per_wg(uint32_t type, int epi, int nb) {
     return nb * (epi == EPI_SWIGLU ? type_rb(type) / 2 : type_rb(type));
 }
@@ -739,7 +800,7 @@ int gemv_rows_per_wg(uint32_t type, int epi, int nb) {
 int gemv_max_grid(uint32_t type, int epi, int rows, int cols) {
     if (generic_shape(type, cols)) return (rows + 3) / 4;
     const int rwg = gemv_rows_per_wg(type, epi, gemv_plan(type, epi, rows, cols));
-    return (rows + rwg - 1) / rwg + 2;   // segments round up separately
+    return (rows + rwg - 1) / rwg + 2;   // segments round up separately (halves only lower the count)
 }
 
 hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
@@ -778,7 +839,8 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
         rows_total += a.seg[i].rows;
     }
     const int nb = gemv_plan(type, epi, rows_total, a.cols);
-    const int rwg = gemv_rows_per_wg(type, epi, nb);
+    const int hv = gemv_halves(type, epi, a.cols, t2 != type);
+    const int rwg = hv * gemv_rows_per_wg(type, epi, nb);
     // Q6_K segments of a mixed launch: half the batches per workgroup (a Q6_K
     // row costs about twice a Q4_K row), so their workgroups end with the rest
     const int nb2 = nb > 1 ? nb / 2 : 1;
@@ -791,7 +853,7 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     }
     if (grid <= 0) return hipSuccess;
     if (epi == EPI_ARGMAX && a.am.cap < grid) return hipErrorInvalidValue;
-    const int threads = 64 * ((a.cols / 32 + 63) / 64);
+    const int threads = hv * 64 * ((a.cols / 32 + 63) / 64);
     hipError_t e;
     if (t2 != type) {   // Q4_K with Q6_K segments (Q/K/V of the Q4_K_M mix)
         switch (nb) {
@@ -804,7 +866,7 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
         return hipGetLastError();
     }
     switch (type) {
-    case GGML_Q4_K: e = launch_t<GGML_Q4_K>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q4_K: e = launch_t<GGML_Q4_K>(epi, a, nb, grid, threads, s, hv); break;
     case GGML_Q5_K: e = launch_t<GGML_Q5_K>(epi, a, nb, grid, threads, s); break;
     case GGML_Q6_K: e = launch_t<GGML_Q6_K>(epi, a, nb, grid, threads, s); break;
     case GGML_Q8_0: e = launch_t<GGML_Q8_0>(epi, a, nb, grid, threads, s); break;
