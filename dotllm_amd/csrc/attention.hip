@@ -31,7 +31,7 @@ namespace llmdot {
 namespace {
 
 constexpr int WG = 256;
-constexpr int CH = 64;    // positions per score chunk (scores kernel)
+constexpr int CH = 64;    // positions per score chunk (scores kernel; one per lane of a wavefront)
 constexpr int CHP = 64;   // positions per pv chunk (pv kernel; its partials feed the combine)
 
 // N consecutive cache elements starting at element idx (16-byte aligned) as floats.
@@ -77,7 +77,7 @@ template <int HD, int G>
 __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
     __shared__ float q_s[G * HD];
     __shared__ float knew[HD];
-    __shared__ float wmax[4][G];
+    __shared__ float sc_s[G][CH];   // this chunk's scores (-inf past T) for the maxima
     constexpr int DPT = HD / 4;           // K elements per thread
     const int T = *a.pos, n = T + 1;
     const int c = blockIdx.x, kvh = blockIdx.y;
@@ -124,14 +124,12 @@ __global__ __launch_bounds__(WG) void attn_scores_kernel(AttnArgs a) {
         s = sum4(s);
         const float score = s * inv_sqrt;
         if (live && sub == 0) a.scores[(int64_t)(kvh * G + h) * a.context + pos] = score;
-        float m = live ? score : -INFINITY;
-        m = wave_max(m);
-        if (lane == 0) wmax[wave][h] = m;
+        if (sub == 0) sc_s[h][p] = live ? score : -INFINITY;
     }
     __syncthreads();
-    if (t < G) {
-        const float m = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
-        a.chunk_max[(int64_t)(kvh * G + t) * gridDim.x + c] = m;
+    for (int h = wave; h < G; h += 4) {   // one head per wavefront: its CH positions, one per lane
+        const float m = wave_max(sc_s[h][lane]);
+        if (lane == 0) a.chunk_max[(int64_t)(kvh * G + h) * gridDim.x + c] = m;
     }
 }
 
@@ -141,7 +139,7 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     constexpr int PPT = CHP / 16;                 // positions per thread
     constexpr int SPT = (G * CHP + WG - 1) / WG;  // scores per thread
     __shared__ float p_s[G][CHP];
-    __shared__ float red[4][G * HD];
+    __shared__ float red[16][G * HD + 4];   // per position group; padded rows
     __shared__ float gmax[G];
     const int T = *a.pos, n = T + 1, n8 = n & ~7;
     const int c = blockIdx.x, kvh = blockIdx.y;
@@ -226,14 +224,16 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int d = 0; d < DPG; d++) {
-            const float v = xor32_add(xor16_add(acc[d]));
-            if (lane < 16) red[wave][h * HD + dg * DPG + d] = v;
+            red[pg][h * HD + dg * DPG + d] = acc[d];
         }
     }
     __syncthreads();
     for (int idx = t; idx < G * HD; idx += WG) {
         const int h = idx / HD, d = idx - h * HD;
-        a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = (red[0][idx] + red[1][idx]) + (red[2][idx] + red[3][idx]);
+        float r = 0.f;   // the 16 position groups, summed through LDS (cheaper than lane exchanges)
+#pragma unroll
+        for (int q = 0; q < 16; q += 4) r += (red[q][idx] + red[q + 1][idx]) + (red[q + 2][idx] + red[q + 3][idx]);
+        a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = r;
     }
 }
 

@@ -289,7 +289,9 @@ def test_mistral7b_greedy64_golden(hip):
     the oracle's first near-tie.  Teacher-forced on the oracle's tokens, every
     step: logits at the oracle's top 16 within the bound, mean and RMS of the
     whole vector within it (both are 1-Lipschitz in the max norm), and the
-    same argmax wherever the oracle's top-2 gap is at least NEAR_TIE."""
+    same argmax wherever the oracle's top-2 gap is at least NEAR_TIE and at
+    least twice the step's measured logit error (a smaller gap is a near-tie
+    at that error)."""
     from golden.make_golden import image_fingerprint
     g = _golden("mistral7b_greedy64.json")
     img = synth.build_image(g["model"], seed=g["weights_seed"], context=g["image_context"])
@@ -323,8 +325,11 @@ def test_mistral7b_greedy64_golden(hip):
                 gl = eng.process_token(int(tk), pos)
                 if pos >= len(prompt) - 1:
                     i = pos - (len(prompt) - 1)
-                    forced.append(err_of(gl, steps[i]))
-                    if steps[i]["gap"] >= NEAR_TIE and int(np.argmax(gl)) != steps[i]["top16"][0]:
+                    e = err_of(gl, steps[i])
+                    forced.append(e)
+                    # a different argmax is a failure unless the step's own logit error
+                    # explains it: the oracle's top two must lie within 2 e of each other
+                    if int(np.argmax(gl)) != steps[i]["top16"][0] and steps[i]["gap"] >= max(NEAR_TIE, 2 * e):
                         flips.append(i)
         finally:
             eng.dispose()
