@@ -783,14 +783,15 @@ int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
     return nb;
 }
 
-// Halves per workgroup: 2 for Q4_K residual-add launches (the attention output
-// projection, 4096 x 4096 at the 7B shape: 6.48 -> 6.16 us) whose units fit the
-// shared activation buffer and whose two halves fit MAXW wavefronts.  The
-// larger STORE / SwiGLU GEMVs measured equal or slower with halves.
-int gemv_halves(uint32_t type, int epi, int cols, bool mixed) {
-    const int units = cols / 32, nw = (units + 63) / 64;
+// Halves per workgroup: 2 for Q4_K residual-add launches over at most 4096
+// columns that keep a workgroup per CU with halves (the 7B attention output
+// projection, 4096 x 4096: 6.48 -> 6.16 us).  With fewer workgroups than CUs,
+// or wider rows (the 1B shape's 2048 x 8192 down projection), halves measured
+// slower, as did the larger STORE / SwiGLU GEMVs.
+int gemv_halves(uint32_t type, int epi, int cols, bool mixed, int grid_one_half) {
+    const int units = cols / 32;
     if (type != GGML_Q4_K || mixed || epi != EPI_ADD || env_halves_off()) return 1;
-    return units <= HV_MAX_UNITS && 2 * nw <= MAXW ? 2 : 1;
+    return units <= 128 && grid_one_half >= 2 * 256 ? 2 : 1;
 }
 
 int gemv_rows_per_wg(uint32_t type, int epi, int nb) {
@@ -839,8 +840,9 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
         rows_total += a.seg[i].rows;
     }
     const int nb = gemv_plan(type, epi, rows_total, a.cols);
-    const int hv = gemv_halves(type, epi, a.cols, t2 != type);
-    const int rwg = hv * gemv_rows_per_wg(type, epi, nb);
+    const int rwg1 = gemv_rows_per_wg(type, epi, nb);
+    const int hv = gemv_halves(type, epi, a.cols, t2 != type, (rows_total + rwg1 - 1) / rwg1);
+    const int rwg = hv * rwg1;
     // Q6_K segments of a mixed launch: half the batches per workgroup (a Q6_K
     // row costs about twice a Q4_K row), so their workgroups end with the rest
     const int nb2 = nb > 1 ? nb / 2 : 1;
