@@ -139,7 +139,11 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     constexpr int PPT = CHP / 16;                 // positions per thread
     constexpr int SPT = (G * CHP + WG - 1) / WG;  // scores per thread
     __shared__ float p_s[G][CHP];
-    __shared__ float red[16][G * HD + 4];   // per position group; padded rows
+    // partial sums of the 16 position groups: with several heads per kv head
+    // through LDS (one padded row per group), for one head by lane exchanges
+    // inside each wavefront first (measured faster for each case)
+    constexpr int NGR = G > 1 ? 16 : 4;
+    __shared__ float red[NGR][G * HD + 4];
     __shared__ float gmax[G];
     const int T = *a.pos, n = T + 1, n8 = n & ~7;
     const int c = blockIdx.x, kvh = blockIdx.y;
@@ -224,15 +228,20 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int d = 0; d < DPG; d++) {
-            red[pg][h * HD + dg * DPG + d] = acc[d];
+            if constexpr (G > 1) {
+                red[pg][h * HD + dg * DPG + d] = acc[d];
+            } else {
+                const float v = xor32_add(xor16_add(acc[d]));
+                if (lane < 16) red[wave][h * HD + dg * DPG + d] = v;
+            }
         }
     }
     __syncthreads();
     for (int idx = t; idx < G * HD; idx += WG) {
         const int h = idx / HD, d = idx - h * HD;
-        float r = 0.f;   // the 16 position groups, summed through LDS (cheaper than lane exchanges)
+        float r = 0.f;
 #pragma unroll
-        for (int q = 0; q < 16; q += 4) r += (red[q][idx] + red[q + 1][idx]) + (red[q + 2][idx] + red[q + 3][idx]);
+        for (int q = 0; q < NGR; q += 4) r += (red[q][idx] + red[q + 1][idx]) + (red[q + 2][idx] + red[q + 3][idx]);
         a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = r;
     }
 }
