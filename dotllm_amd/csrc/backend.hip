@@ -101,6 +101,15 @@ struct llmdot_hip_ctx {
     // with models alive defers the release to the last model's destroy
     int models = 0;
     bool closing = false;
+    // fp32 copies models keep of non-F32 norm weights (LM:63-75): an in-place
+    // re-upload of the key converts the new bytes into each of them
+    struct NormCopy {
+        std::string key;
+        float* dst;
+        int n;
+        const void* owner;
+    };
+    std::vector<NormCopy> norm_copies;
 };
 
 namespace {
@@ -143,6 +152,9 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
                 return fail(LLMDOT_E_INVALID, "weight '" + key + "' is in use by a model with another shape or type");
             HIPCHK(hipStreamSynchronize(ctx->stream));
             HIPCHK(hipMemcpy(old.dev, bytes, (size_t)need, hipMemcpyHostToDevice));
+            for (const auto& c : ctx->norm_copies)   // models reading an fp32 copy of this norm
+                if (c.key == key) HIPCHK(launch_dequant(old.dev, c.dst, type, 1, c.n, ctx->stream));
+            HIPCHK(hipStreamSynchronize(ctx->stream));
             if (out) *out = &old;
             return 0;
         }
@@ -720,12 +732,16 @@ int need_w(llmdot_hip_model* m, const std::string& name, int64_t rows, int64_t c
 }
 
 // Norm weights as fp32 on the device (LoadedModel.GetDequantizedWeights, LM:63-75).
+// F32 norms are read in place; other types are converted into a model-owned
+// copy that the context re-converts when the key is re-uploaded in place.
 int norm_f32(llmdot_hip_model* m, const Weight* w, int n, float** out) {
     if (w->rows * w->cols != n) return fail(LLMDOT_E_INVALID, "norm weight has wrong size");
     if (w->type == GGML_F32) { *out = reinterpret_cast<float*>(w->dev); return 0; }
     void* p;
     if (int rc = dalloc(m, sizeof(float) * (size_t)n, &p)) return rc;
     HIPCHK(launch_dequant(w->dev, (float*)p, w->type, 1, n, m->ctx->stream));
+    for (const auto& kv : m->ctx->weights)
+        if (&kv.second == w) m->ctx->norm_copies.push_back({kv.first, (float*)p, n, m});
     *out = (float*)p;
     return 0;
 }
@@ -1009,6 +1025,9 @@ extern "C" int32_t llmdot_hip_model_destroy(llmdot_hip_model* m) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    auto& nc = ctx->norm_copies;
+    nc.erase(std::remove_if(nc.begin(), nc.end(), [m](const llmdot_hip_ctx::NormCopy& c) { return c.owner == m; }),
+             nc.end());
     for (void* p : m->owned) (void)hipFree(p);
     for (const auto& k : m->pinned) {
         auto it = ctx->weights.find(k);

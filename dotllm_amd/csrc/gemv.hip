@@ -658,8 +658,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     } else if (EPI == EPI_ARGMAX) {
         const float y = valid ? total(t) : -INFINITY;
         if (valid) seg.out[row] = y;
-        float bv = y;
-        int bi = valid ? row : 0x7FFFFFFF;
+        // NaN never wins (a NaN logit at index 0 is applied by the second pass)
+        const bool cand = valid && !__builtin_isnan(y);
+        float bv = cand ? y : -INFINITY;
+        int bi = cand ? row : 0x7FFFFFFF;
         wave_argmax(bv, bi);
         if (t == 0) {   // one candidate per workgroup; launch_argmax_finish reduces them
             a.am.cand_val[blockIdx.x] = bv;
@@ -878,7 +880,9 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess || epi != EPI_ARGMAX) return e;
-    return launch_argmax_finish(a.am, grid, s);
+    ArgmaxState am = a.am;
+    am.first = a.seg[0].out;   // logits[0]: VectorMath.ArgMax's NaN-at-[0] rule
+    return launch_argmax_finish(am, grid, s);
 }
 
 }  // namespace llmdot

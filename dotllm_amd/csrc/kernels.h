@@ -41,6 +41,10 @@ struct ArgmaxState {
     int32_t* token_log;   // optional: token_log[*step] = argmax while *step < log_cap
     int32_t log_cap;
     int32_t* step;        // optional: incremented by the second pass
+    // element 0 of the reduced vector: VectorMath.ArgMax (VM:412-425) starts
+    // from input[0] and compares with '>', so a NaN there is never replaced
+    // and the result is 0; NaN elsewhere never wins (set by the launchers)
+    const float* first;
 };
 
 struct GemvArgs {

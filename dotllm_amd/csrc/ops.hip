@@ -156,6 +156,7 @@ __global__ __launch_bounds__(WG) void argmax_finish_kernel(ArgmaxState st, int n
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; w++) am_pick(v, idx, sv[w], si[w]);
         if (idx == 0x7FFFFFFF) idx = 0;   // all NaN: ArgMax returns 0
+        if (st.first && __builtin_isnan(*st.first)) idx = 0;   // NaN at [0] is never replaced (VM:414-419)
         *st.token_out = idx;
         if (st.step) {
             const int k = *st.step;
@@ -249,10 +250,12 @@ hipError_t launch_scale(const float* in, float sc, float* out, int n, hipStream_
 int argmax_grid(int n) { return (n + AM_PER_WG - 1) / AM_PER_WG; }
 hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream_t s) {
     if (n <= 0 || st.cap < argmax_grid(n)) return hipErrorInvalidValue;
-    argmax_kernel<<<argmax_grid(n), WG, 0, s>>>(x, n, st);
+    ArgmaxState st1 = st;
+    st1.first = x;
+    argmax_kernel<<<argmax_grid(n), WG, 0, s>>>(x, n, st1);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_argmax_finish(st, argmax_grid(n), s);
+    return launch_argmax_finish(st1, argmax_grid(n), s);
 }
 hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s) {
     if (ncand <= 0 || ncand > st.cap) return hipErrorInvalidValue;

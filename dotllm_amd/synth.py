@@ -79,7 +79,7 @@ def tensor_seed(seed: int, name: str) -> int:
     return (int(seed) * 0x9E3779B1 + zlib.crc32(name.encode())) & 0xFFFFFFFFFFFFFFFF
 
 
-def metadata(spec: dict, context: int | None = None) -> list:
+def metadata(spec: dict, context: int | None = None, eos: int = -1) -> list:
     a = spec["arch"]
     ctx = int(context or spec["context"])
     toks = [f"<t{i}>" for i in range(spec["vocab"])]
@@ -100,7 +100,7 @@ def metadata(spec: dict, context: int | None = None) -> list:
         ("tokenizer.ggml.model", gguf.STR, "gpt2"),
         ("tokenizer.ggml.tokens", gguf.ARR, (gguf.STR, toks)),
         ("tokenizer.ggml.bos_token_id", gguf.I32, 1),
-        ("tokenizer.ggml.eos_token_id", gguf.I32, -1),
+        ("tokenizer.ggml.eos_token_id", gguf.I32, int(eos)),
     ]
 
 
@@ -122,12 +122,18 @@ def tensor_sigma(name: str, spec: dict, sigma: float, scaled_init: bool) -> floa
 
 
 def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
-                threads: int | None = None, spec: dict | None = None, scaled_init: bool = True) -> np.ndarray:
-    """Builds the whole GGUF file image in memory (uint8 numpy array)."""
+                threads: int | None = None, spec: dict | None = None, scaled_init: bool = True,
+                eos: int = -1, tied: bool = False, norm_type: int = F32) -> np.ndarray:
+    """Builds the whole GGUF file image in memory (uint8 numpy array).
+
+    eos: tokenizer.ggml.eos_token_id (-1: never stops); tied: no output.weight,
+    so the LM head reads token_embd.weight (InferenceEngine.cs:585-589);
+    norm_type: F32 or F16 RMSNorm weights (ones either way)."""
     spec = spec or SPECS[name]
-    tl = tensor_list(spec)
+    tl = [(n, r, c, (norm_type if n.endswith("_norm.weight") else t)) for n, r, c, t in tensor_list(spec)
+          if not (tied and n == "output.weight")]
     infos = [(n, (c,) if r == 1 else (c, r), t, byte_count(t, r * c)) for n, r, c, t in tl]
-    hdr, offsets, total = gguf.header_bytes(metadata(spec, context), infos)
+    hdr, offsets, total = gguf.header_bytes(metadata(spec, context, eos), infos)
     img = np.empty(total, dtype=np.uint8)
     img[:len(hdr)] = np.frombuffer(hdr, dtype=np.uint8)
     base = len(hdr)
@@ -135,7 +141,12 @@ def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int |
         nb = info[3]
         view = img[base + off: base + off + nb]
         if n.endswith("_norm.weight"):
-            view.view(np.float32)[:] = 1.0
+            if t == F32:
+                view.view(np.float32)[:] = 1.0
+            elif t == _lib.F16:
+                view.view(np.float16)[:] = 1.0
+            else:
+                raise ValueError("norm weights are F32 or F16")
         else:
             synth_tensor(t, r, c, tensor_seed(seed, n), view, tensor_sigma(n, spec, sigma, scaled_init), threads)
         nxt = base + off + nb

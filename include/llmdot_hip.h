@@ -136,7 +136,6 @@ typedef struct llmdot_hip_sampling {
  * boundary.  LLMDOT_E_UNSUPPORTED for 4096 < top_k < n. */
 int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, int32_t n, const llmdot_hip_sampling* opt,
                           const int32_t* recent, int32_t n_recent, float r, int32_t* token);
-
 /* ---- device-pointer variants (inputs already resident in HBM; used by
  *      harnesses that time kernels without PCIe traffic). ------------------- */
 int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, void** dptr);
