@@ -104,6 +104,7 @@ SIGNATURES = {
     "llmdot_hip_dequantize": [_P, _P, _P, _U32, _I32, _I32],
     "llmdot_hip_argmax": [_P, _P, _I32, _PI32],
     "llmdot_hip_sample": [_P, _P, _I32, C.POINTER(Sampling), _PI32, _I32, _F, _PI32],
+    "llmdot_hip_sample_noalloc": [_P, _P, _I32, C.POINTER(Sampling), _P, _I32, _F, _P],
     "llmdot_hip_device_alloc": [_P, C.c_size_t, _PP],
     "llmdot_hip_device_free": [_P, _P],
     "llmdot_hip_memcpy_h2d": [_P, _P, _P, C.c_size_t],

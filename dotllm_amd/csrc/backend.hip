@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <set>
 #include <string>
 #include <unordered_map>
@@ -174,6 +175,54 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
 
 }  // namespace
 
+// ======================================================= allocation-free ==
+// llmdot_hip_sample_noalloc keeps its scratch in this file-scope device array
+// instead of allocating: the sampler's work vector (one float per logit), the
+// argmax candidates (one per 4096 logits) and two words (the draw counter and
+// the uniform draw).  Each device holds its own copy until the process ends;
+// its address is looked up once per device (with that device current) when a
+// context is created, and only that address is handed to kernels and copies.
+namespace {
+constexpr int NOALLOC_MAX_N = 262144;                                  // logits per call
+constexpr int NOALLOC_CAND = NOALLOC_MAX_N / 4096;                     // argmax_grid(NOALLOC_MAX_N)
+constexpr size_t NOALLOC_WORK = sizeof(float) * (size_t)NOALLOC_MAX_N; // work[n]
+constexpr size_t NOALLOC_CAND_VAL = NOALLOC_WORK;                      // float[NOALLOC_CAND]
+constexpr size_t NOALLOC_CAND_IDX = NOALLOC_CAND_VAL + 4 * NOALLOC_CAND;   // int32[NOALLOC_CAND]
+constexpr size_t NOALLOC_INTS = NOALLOC_CAND_IDX + 4 * NOALLOC_CAND;   // [0] draw counter, [1] draw bits
+constexpr size_t NOALLOC_BYTES = NOALLOC_INTS + 256;                   // 1 MiB + 768 B
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+__attribute__((used)) __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+bool g_scratch_done[NOALLOC_MAX_DEVICES] = {};
+std::string g_scratch_err[NOALLOC_MAX_DEVICES];
+
+// Once per device, with `device` current: the device address of `scratch`.
+void scratch_setup(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_done[device]) return;
+    g_scratch_done[device] = true;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        g_scratch_err[device] = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+        (void)hipGetLastError();
+        return;
+    }
+    g_scratch_ptr[device] = static_cast<uint8_t*>(p);
+}
+
+uint8_t* scratch_of(int device, std::string* err) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) { *err = "device index beyond the scratch table"; return nullptr; }
+    if (!g_scratch_ptr[device]) *err = g_scratch_err[device].empty() ? "scratch not set up" : g_scratch_err[device];
+    return g_scratch_ptr[device];
+}
+}  // namespace
+
 // =============================================================== context ==
 
 extern "C" const char* llmdot_hip_last_error(void) { return g_err.c_str(); }
@@ -201,6 +250,7 @@ extern "C" int32_t llmdot_hip_create(int32_t device, llmdot_hip_ctx** out) {
         delete ctx;
         return fail(LLMDOT_E_DEVICE, std::string("stream creation failed: ") + hipGetErrorString(e));
     }
+    scratch_setup(device);   // llmdot_hip_sample_noalloc reports a failure here
     *out = ctx;
     return 0;
 }
@@ -549,6 +599,47 @@ extern "C" int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, i
     sa.work = (float*)ctx->scratch[1].p; sa.token_out = ctx->am_ints;
     HIPCHK(launch_sample(sa, ctx->stream));
     return copy_out(ctx, token, ctx->am_ints, sizeof(int32_t));
+}
+
+extern "C" int32_t llmdot_hip_sample_noalloc(llmdot_hip_ctx* ctx, const float* logits_dev, int32_t n,
+                                             const llmdot_hip_sampling* opt, const int32_t* recent_dev,
+                                             int32_t n_recent, float r, int32_t* token_dev) {
+    if (!ctx || !logits_dev || !opt || !token_dev || n <= 0 || n_recent < 0 || (n_recent > 0 && !recent_dev))
+        return fail(LLMDOT_E_INVALID, "bad Sample arguments");
+    if (n > NOALLOC_MAX_N)
+        return fail(LLMDOT_E_UNSUPPORTED, "llmdot_hip_sample_noalloc: " + std::to_string(n) +
+                                              " logits exceed its scratch of " + std::to_string(NOALLOC_MAX_N));
+    const bool sampled = opt->temperature > 0.f;   // Sampler.cs:26-27: greedy otherwise
+    if (sampled && !sample_supported(n, opt->top_k))
+        return fail(LLMDOT_E_UNSUPPORTED, "TopK between " + std::to_string(SAMPLE_MAX_K) + " and the vocabulary size is not supported");
+    if (int rc = ensure_device(ctx)) return rc;
+    std::string err;
+    uint8_t* base = scratch_of(ctx->device, &err);
+    if (!base) return fail(LLMDOT_E_DEVICE, "llmdot_hip_sample_noalloc: " + err);
+    float* work = reinterpret_cast<float*>(base);
+    int32_t* ints = reinterpret_cast<int32_t*>(base + NOALLOC_INTS);
+    if (!sampled) {
+        ArgmaxState st{};
+        st.cand_val = reinterpret_cast<float*>(base + NOALLOC_CAND_VAL);
+        st.cand_idx = reinterpret_cast<int32_t*>(base + NOALLOC_CAND_IDX);
+        st.cap = NOALLOC_CAND;
+        st.token_out = token_dev;
+        HIPCHK(launch_argmax(logits_dev, n, st, ctx->stream));
+        return 0;
+    }
+    // the draw counter (this is draw 0) and the uniform draw, written by kernels
+    // so that the call records no memset or host copy
+    uint32_t rbits;
+    memcpy(&rbits, &r, 4);
+    HIPCHK(launch_set_scalar(ints, 1, ctx->stream));
+    HIPCHK(launch_set_scalar(ints + 1, (int32_t)rbits, ctx->stream));
+    SampleArgs sa{};
+    sa.logits = logits_dev; sa.n = n; sa.inv_temp = 1.0f / opt->temperature;
+    sa.top_k = opt->top_k; sa.top_p = opt->top_p; sa.penalty = opt->repeat_penalty; sa.window = opt->repeat_window;
+    sa.hist = recent_dev; sa.hist_base = n_recent; sa.step = ints; sa.rvals = reinterpret_cast<const float*>(ints + 1);
+    sa.work = work; sa.token_out = token_dev;
+    HIPCHK(launch_sample(sa, ctx->stream));
+    return 0;
 }
 
 // ========================================================= device pointers ==

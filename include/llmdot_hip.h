@@ -136,6 +136,21 @@ typedef struct llmdot_hip_sampling {
  * boundary.  LLMDOT_E_UNSUPPORTED for 4096 < top_k < n. */
 int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, int32_t n, const llmdot_hip_sampling* opt,
                           const int32_t* recent, int32_t n_recent, float r, int32_t* token);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): llmdot_hip_sample over device pointers -- logits_dev [n],
+ * recent_dev [n_recent] (may be NULL when n_recent is 0) and token_dev [1] all
+ * in HBM -- enqueued on the context's stream (call llmdot_hip_synchronize
+ * before reading token_dev).  The same kernels and results as
+ * llmdot_hip_sample; their scratch (1 MiB + 768 B) is a static array of the
+ * library, one per device, so this call allocates nothing.  n is at most
+ * 262144 (LLMDOT_E_UNSUPPORTED beyond).  Every call on a device shares that
+ * device's scratch: calls that overlap on one device (several contexts or
+ * threads) race; calls on one context's stream do not. */
+int32_t llmdot_hip_sample_noalloc(llmdot_hip_ctx* ctx, const float* logits_dev, int32_t n,
+                                  const llmdot_hip_sampling* opt, const int32_t* recent_dev, int32_t n_recent,
+                                  float r, int32_t* token_dev);
+
 /* ---- device-pointer variants (inputs already resident in HBM; used by
  *      harnesses that time kernels without PCIe traffic). ------------------- */
 int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, void** dptr);
