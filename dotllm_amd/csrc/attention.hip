@@ -10,9 +10,12 @@
 //
 // The reference's ExpApprox is not multiplicative, so an online (rescaling)
 // softmax cannot reproduce it; the global max must be known before any
-// exponent.  The sequence is split into chunks per kv head (grid = chunks x
-// kv heads; chunks past T exit), over three launches (each reads what the
-// previous wrote, so no fences or atomics are needed):
+// exponent.  The sequence is split into 64-position chunks per kv head (grid
+// = chunks x kv heads; chunks past T exit).  Up to 16384 positions the
+// scores and the values run in one launch (attn_fused_kernel: the workgroups
+// of a kv head exchange their chunk maxima through tagged slots), then the
+// combine; beyond that, or with LLMDOT_HIP_ATTN_FUSED=0, three launches (each
+// reads what the previous wrote, so no fences or atomics are needed):
 //   scores:  64-position chunks: RoPE + KV write + scores + chunk max (per q head).
 //            4 threads per position, each loading a quarter of the K row with
 //            16-byte loads; every K row is read once for all G q heads.
@@ -33,6 +36,7 @@ namespace {
 constexpr int WG = 256;
 constexpr int CH = 64;    // positions per score chunk (scores kernel; one per lane of a wavefront)
 constexpr int CHP = 64;   // positions per pv chunk (pv kernel; its partials feed the combine)
+constexpr int XSTRIDE = 512;   // tagged chunk-maximum slots per q head (4 KiB apart)
 
 // N consecutive cache elements starting at element idx (16-byte aligned) as floats.
 template <int N>
@@ -246,6 +250,293 @@ __global__ __launch_bounds__(WG) void attn_pv_kernel(AttnArgs a) {
     }
 }
 
+// N consecutive cache elements of a row as raw dwords (fp16 pairs or fp32),
+// loaded with no branch on the element type so that every load of a thread
+// is issued before the first one is waited on; converted at use.
+template <int N, bool F16>
+struct KvRaw {
+    static constexpr int W = F16 ? N / 2 : N;   // dwords
+    static constexpr bool V4 = W % 4 == 0 && (N * (F16 ? 2 : 4)) % 16 == 0;
+    uint32_t w[W];
+    __device__ __forceinline__ void load(const void* cache, int64_t idx) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(cache) +
+                                                              idx * (F16 ? 2 : 4));
+        if constexpr (V4) {
+#pragma unroll
+            for (int i = 0; i < W / 4; i++) {
+                const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
+                w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < W; i++) w[i] = p[i];
+        }
+    }
+    __device__ __forceinline__ float at(int e) const {
+        if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+        else return __uint_as_float(w[e]);
+    }
+};
+
+// Tagged slot: (tag << 32) | float bits, stored and loaded at system scope so
+// that the access goes past the per-XCD L2s (which are not coherent with each
+// other) and a reader sees either an older tag or the whole new pair.
+__device__ __forceinline__ void slot_put(uint64_t* p, uint32_t tag, float v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t slot_get(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// One poll of the tagged chunk maxima of the G heads of kv head kvh: four
+// slots per lane and head.
+template <int G>
+__device__ __forceinline__ void poll_issue(uint64_t (&v)[G][4], const uint64_t* xmax, int kvh, int lane, int nch,
+                                           int mc) {
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        const uint64_t* slots = xmax + ((int64_t)kvh * G + j) * mc;
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[j][i] = slot_get(slots + min(lane + 64 * i, nch - 1));
+    }
+}
+template <int HW>
+__device__ __forceinline__ bool poll_ready(const uint64_t (&v)[HW][4], uint32_t tag) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < HW; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) ok = ok && (uint32_t)(v[j][i] >> 32) == tag;
+    return __all(ok) != 0;
+}
+template <int HW>
+__device__ __forceinline__ void poll_max(const uint64_t (&v)[HW][4], float (&res)[HW]) {
+#pragma unroll
+    for (int j = 0; j < HW; j++) {
+        float mm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) mm = fmaxf(mm, __uint_as_float((uint32_t)v[j][i]));
+        res[j] = wave_max(mm);
+    }
+}
+
+// Scores and values in one launch.  Workgroup (chunk c, kv head k) covers 64
+// positions with two pairs of wavefronts: wavefronts 0-1 load the K rows
+// (two threads per row), form the scores (RoPE and the new token's KV write
+// as attn_scores_kernel), publish the chunk maxima in tagged slots and wait
+// until every live chunk of the kv head has published; wavefronts 2-3 load
+// the V rows into LDS at the same time.  The wait counter is per wavefront,
+// so the exchange waits only for K.  Then all four form the exponentials
+// against the global maxima and the chunk partials for attn_combine_kernel
+// (as attn_pv_kernel).  The wait needs the kv head's workgroups to run
+// together: workgroups are dispatched in index order and a kv head's chunks
+// are consecutive, so once they are all dispatched none of them waits on a
+// workgroup that cannot start; a wait that still runs past spin_max polls
+// gives up and sets *err (the host reports it).
+template <int HD, int G, bool F16>
+__global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
+    constexpr int HALF_ROW = HD / 2;              // K / V elements per loading thread
+    constexpr int DPG = HD / 16;                  // V elements per thread and position (values)
+    constexpr int PPT = CH / 16;                  // positions per thread (values)
+    constexpr int NGR = G > 1 ? 16 : 4;
+    constexpr int EB = F16 ? 2 : 4;               // bytes per cache element
+    constexpr int VBUF = CH * HD * EB;            // V rows of the chunk, raw
+    constexpr int RED = NGR * (G * HD + 4) * 4;   // position-group partial sums
+    __shared__ float q_s[G * HD];
+    __shared__ float knew[HD], vnew[HD];
+    __shared__ float sc_s[G][CH];                 // scores (-inf past T), then exponentials
+    __shared__ float gmax[G];
+    __shared__ __align__(16) uint8_t pool[VBUF > RED ? VBUF : RED];   // V rows, then the partial sums
+    const int T = *a.pos, n = T + 1, n8 = n & ~7;
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    const int p0 = c * CH;
+    if (p0 >= n) return;
+    const int nch = (n + CH - 1) / CH;            // live chunks of every kv head
+    const int cnt = min(CH, n - p0);
+    const int mc = XSTRIDE;                       // slots per head: one 4 KiB page each
+    const uint32_t tag = *a.epoch * (uint32_t)a.layers + (uint32_t)a.layer + 1u;
+    const int half = a.rope_half;
+    const float* cs = a.cos_tab + (int64_t)T * half;
+    const float* sn = a.sin_tab + (int64_t)T * half;
+    const int64_t cache_base = (int64_t)kvh * a.context * HD;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const bool kwave = wave < 2;
+
+    // Loads in the order they are consumed (each wavefront's wait counter
+    // retires them in issue order): q, the RoPE table and the new token's k
+    // and v first, then the thread's half row of K (wavefronts 0-1) or of V
+    // (2-3).  Rows past T read row p0 (written) and are masked; row T is
+    // written below by this workgroup and taken from LDS instead.
+    constexpr int QI = (G * HD + WG - 1) / WG;    // q elements per thread
+    const bool owner = T >= p0 && T < p0 + CH;
+    float qa[QI], qb[QI], qc[QI], qs[QI];
+#pragma unroll
+    for (int j = 0; j < QI; j++) {
+        const int idx = min(t + j * WG, G * HD - 1);
+        const int h = idx / HD, d = idx - h * HD;
+        const float* x = a.q + (int64_t)(kvh * G + h) * HD;
+        const int i = d < half ? d : (d < 2 * half ? d - half : 0);
+        qa[j] = x[d];
+        qb[j] = x[d < half ? d + half : (d < 2 * half ? d - half : d)];
+        qc[j] = cs[i];
+        qs[j] = sn[i];
+    }
+    // the new token's k pair and v element (read by every workgroup, used by
+    // the owner: a load under a branch would be waited on inside it)
+    float ka, kb, kc, ks, vn;
+    {
+        const float* x = a.k + (int64_t)kvh * HD;
+        const int d = t < HD ? t : 0, i = d < half ? d : (d < 2 * half ? d - half : 0);
+        ka = x[d];
+        kb = x[d < half ? d + half : (d < 2 * half ? d - half : d)];
+        kc = cs[i];
+        ks = sn[i];
+        vn = a.v[(int64_t)kvh * HD + d];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // the small loads stay ahead of the rows
+    const int lt = t & 127, rp = lt >> 1, rh = lt & 1;   // row (position) and half of it
+    const int rpos = p0 + rp;
+    const bool rlive = rpos < n;
+    KvRaw<HALF_ROW, F16> row;
+    row.load(kwave ? a.kcache : a.vcache,
+             cache_base + (int64_t)(rlive && rpos != T ? rpos : p0) * HD + rh * HALF_ROW);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int j = 0; j < QI; j++) {
+        const int idx = t + j * WG;
+        if (idx < G * HD) q_s[idx] = rope_pair(qa[j], qb[j], qc[j], qs[j], idx % HD, half);
+    }
+    if (owner && t < HD) {   // this workgroup owns the new token: K/V slot T
+        const int64_t slot = cache_base + (int64_t)T * HD + t;
+        knew[t] = store_kv(a.kcache, slot, rope_pair(ka, kb, kc, ks, t, half), F16);
+        vnew[t] = store_kv(a.vcache, slot, vn, F16);
+    }
+    __syncthreads();
+    if (kwave) {
+        // scores: two threads per position, each over half of the row
+        float kf[HALF_ROW];
+#pragma unroll
+        for (int d = 0; d < HALF_ROW; d++) kf[d] = row.at(d);
+        if (owner && rpos == T) {   // one branch around the loop, taken in one workgroup
+#pragma unroll
+            for (int d = 0; d < HALF_ROW; d++) kf[d] = knew[rh * HALF_ROW + d];
+        }
+        const float inv_sqrt = 1.0f / sqrtf((float)HD);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float* qv = q_s + h * HD + rh * HALF_ROW;
+            float sdot = 0.f;
+#pragma unroll
+            for (int d = 0; d < HALF_ROW; d++) sdot += qv[d] * kf[d];
+            sdot += fx(lane_xor1, sdot);
+            if (rh == 0) sc_s[h][rp] = rlive ? sdot * inv_sqrt : -INFINITY;
+        }
+    } else {
+        // V half rows into LDS, raw
+        uint32_t* vb = reinterpret_cast<uint32_t*>(pool) + (rp * HD + rh * HALF_ROW) * EB / 4;
+#pragma unroll
+        for (int i = 0; i < KvRaw<HALF_ROW, F16>::W; i++) vb[i] = row.w[i];
+    }
+    __syncthreads();
+    if (kwave) {
+        // Chunk maxima out, global maxima in: wavefronts 0 and 1 publish and
+        // gather heads wave, wave + 2, ... (the wavefronts that loaded V have
+        // finished with memory and stay out of the polling traffic); each
+        // lane polls four slots per head (chunks lane + 64 i, clamped to the
+        // last live one).
+        for (int h = wave; h < G; h += 2) {
+            const float m = wave_max(sc_s[h][lane]);
+            if (lane == 0) slot_put(a.xmax + ((int64_t)kvh * G + h) * mc + c, tag, m);
+        }
+        for (int h = wave; h < G; h += 2) {
+            uint64_t v[1][4];
+            float res[1];
+            for (int it = 0;; it++) {
+                poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, nch, mc);
+                if (poll_ready<1>(v, tag)) break;
+                if (it >= a.spin_max) {
+                    if (lane == 0) atomicOr(a.err, 1);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            poll_max<1>(v, res);
+            if (lane == 0) gmax[h] = res[0];
+        }
+    }
+    __syncthreads();
+    // the values phase: this thread's V slices (positions pg + 16 i, DPG
+    // elements from dg * DPG) as floats; the new token's from LDS
+    const int dg = t & 15, pg = t >> 4;
+    float vv[PPT][DPG];
+#pragma unroll
+    for (int i = 0; i < PPT; i++) {
+        const int e0 = (pg + 16 * i) * HD + dg * DPG;
+#pragma unroll
+        for (int d = 0; d < DPG; d++) {
+            if constexpr (F16) vv[i][d] = (float)reinterpret_cast<const _Float16*>(pool)[e0 + d];
+            else vv[i][d] = reinterpret_cast<const float*>(pool)[e0 + d];
+        }
+    }
+    if (owner) {   // the new token's V slice from LDS (its cache row was loaded stale)
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+            if (p0 + pg + 16 * i == T) {
+#pragma unroll
+                for (int d = 0; d < DPG; d++) vv[i][d] = vnew[dg * DPG + d];
+            }
+    }
+    for (int idx = t; idx < G * CH; idx += WG) {
+        const int h = idx / CH, pp = idx - h * CH;
+        const int sidx = p0 + pp;
+        float e;
+        {
+#pragma clang fp contract(off)
+            const float x = sc_s[h][pp] - gmax[h];
+            // Softmax: ExpApprox on the vector lanes (first 8*floor(n/8)), expf on the tail
+            e = sidx < n8 ? exp_approx(x) : expf(x);
+        }
+        sc_s[h][pp] = pp < cnt ? e : 0.f;
+    }
+    __syncthreads();   // exponentials visible; the V rows are in registers (pool reused below)
+    for (int h = wave; h < G; h += 4) {   // this chunk's sum of exponentials
+        const float z = wave_sum(sc_s[h][lane]);
+        if (lane == 0) a.part_sum[(int64_t)c * a.heads + kvh * G + h] = z;
+    }
+    float (*red)[G * HD + 4] = reinterpret_cast<float (*)[G * HD + 4]>(pool);
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float acc[DPG];
+#pragma unroll
+        for (int d = 0; d < DPG; d++) acc[d] = 0.f;
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const float pr = sc_s[h][pg + 16 * i];
+#pragma unroll
+            for (int d = 0; d < DPG; d++) acc[d] += pr * vv[i][d];
+        }
+#pragma unroll
+        for (int d = 0; d < DPG; d++) {
+            if constexpr (G > 1) {
+                red[pg][h * HD + dg * DPG + d] = acc[d];
+            } else {
+                const float v = xor32_add(xor16_add(acc[d]));
+                if (lane < 16) red[wave][h * HD + dg * DPG + d] = v;
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = t; idx < G * HD; idx += WG) {
+        const int h = idx / HD, d = idx - h * HD;
+        float r = 0.f;
+#pragma unroll
+        for (int q = 0; q < NGR; q += 4) r += (red[q][idx] + red[q + 1][idx]) + (red[q + 2][idx] + red[q + 3][idx]);
+        a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = r;
+    }
+}
+
 // out = sum_c part_out[c] / sum_c part_sum[c] for one q head per workgroup
 // (a separate launch: the chunk partials are visible without fences).  NG
 // groups of HD threads each take every NG-th chunk; the group sums are then
@@ -281,6 +572,16 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(AttnArgs a) {
 template <int HD, int G>
 hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
     const int nchunks = attn_max_chunks(a.heads, a.kv_heads, a.context);
+    if (a.fused) {
+        if (!a.xmax || !a.epoch || !a.err || !attn_fused_ok(a.heads, a.kv_heads, a.head_dim, a.context))
+            return hipErrorInvalidValue;
+        if (a.kv_fp16) attn_fused_kernel<HD, G, true><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
+        else attn_fused_kernel<HD, G, false><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attn_combine_kernel<HD><<<a.heads, (1024 / HD) * HD, 0, s>>>(a);
+        return hipGetLastError();
+    }
     attn_scores_kernel<HD, G><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -307,6 +608,12 @@ hipError_t launch_hd(const AttnArgs& a, hipStream_t s) {
 int attn_max_chunks(int heads, int kv_heads, int context) {
     (void)heads; (void)kv_heads;
     return (context + CH - 1) / CH;
+}
+
+int attn_xmax_slots(int heads) { return heads * XSTRIDE; }
+
+bool attn_fused_ok(int heads, int kv_heads, int head_dim, int context) {
+    return attn_supported(heads, kv_heads, head_dim) && (context + CH - 1) / CH <= 256;
 }
 
 bool attn_supported(int heads, int kv_heads, int head_dim) {

@@ -766,7 +766,12 @@ struct llmdot_hip_model {
     int rope_half = 0;
     // attention scratch
     float *scores = nullptr, *chunk_max = nullptr, *part_out = nullptr, *part_sum = nullptr;
-    // argmax + device-side loop state: ints[0] token, [1] pos, [2] step
+    uint64_t* xmax = nullptr;   // tagged chunk maxima of the one-launch attention
+    bool attn_fused = false;
+    int attn_spin = 1 << 18;
+    // argmax + device-side loop state: ints[0] token, [1] pos, [2] step,
+    // [3] epoch (decode steps run, never reset: tags the attention's slots),
+    // [4] error flags set by device waits that gave up
     int32_t* ints = nullptr;
     int32_t* token_log = nullptr;
     float* am_val = nullptr;
@@ -793,6 +798,8 @@ namespace {
 int32_t* m_token(llmdot_hip_model* m) { return m->ints; }
 int32_t* m_pos(llmdot_hip_model* m) { return m->ints + 1; }
 int32_t* m_step(llmdot_hip_model* m) { return m->ints + 2; }
+uint32_t* m_epoch(llmdot_hip_model* m) { return reinterpret_cast<uint32_t*>(m->ints + 3); }
+int32_t* m_err(llmdot_hip_model* m) { return m->ints + 4; }
 
 int dalloc(llmdot_hip_model* m, size_t n, void** p) {
     hipError_t e = hipMalloc(p, n + WEIGHT_PAD);
@@ -870,6 +877,7 @@ int enqueue_head(llmdot_hip_model* m) {
     ga.am.cand_val = m->am_val; ga.am.cand_idx = m->am_idx; ga.am.cap = m->am_cap;
     ga.am.token_out = m_token(m); ga.am.pos = m_pos(m);
     ga.am.token_log = m->token_log; ga.am.log_cap = d.context + 1; ga.am.step = m_step(m);
+    ga.am.epoch = m_epoch(m);
     HIPCHK(step_gemv(m, m->out->type, EPI_ARGMAX, ga));
     return 0;
 }
@@ -915,6 +923,8 @@ int enqueue_step(llmdot_hip_model* m) {
         aa.out = m->attn;
         aa.heads = d.heads; aa.kv_heads = d.kv_heads; aa.head_dim = d.head_dim; aa.rope_half = m->rope_half;
         aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
+        aa.fused = m->attn_fused ? 1 : 0; aa.xmax = m->xmax; aa.epoch = m_epoch(m);
+        aa.layer = l; aa.layers = d.layers; aa.spin_max = m->attn_spin; aa.err = m_err(m);
         HIPCHK(launch_attention(aa, s));
         {   // O projection + residual (IE:444-449, IE:189), h packed for the FFN RmsNorm
             GemvArgs ga{};
@@ -1238,6 +1248,10 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     if ((rc = A(sizeof(float) * (size_t)d.heads * nch, &p))) return bail(rc); m->chunk_max = (float*)p;
     if ((rc = A(sizeof(float) * (size_t)nch * qdim, &p))) return bail(rc); m->part_out = (float*)p;
     if ((rc = A(sizeof(float) * (size_t)nch * d.heads, &p))) return bail(rc); m->part_sum = (float*)p;
+    m->attn_fused = attn_fused_ok(d.heads, d.kv_heads, d.head_dim, d.context);
+    if (const char* v = getenv("LLMDOT_HIP_ATTN_FUSED")) m->attn_fused = m->attn_fused && strcmp(v, "0") != 0;
+    if (const char* v = getenv("LLMDOT_HIP_ATTN_SPIN")) m->attn_spin = atoi(v) >= 0 ? atoi(v) : m->attn_spin;
+    if ((rc = A(sizeof(uint64_t) * (size_t)attn_xmax_slots(d.heads), &p))) return bail(rc); m->xmax = (uint64_t*)p;
     if ((rc = A(64, &p))) return bail(rc); m->ints = (int32_t*)p;
     if ((rc = A(sizeof(int32_t) * (size_t)(d.context + 1), &p))) return bail(rc); m->token_log = (int32_t*)p;
     {
@@ -1275,12 +1289,28 @@ int check_pos(llmdot_hip_model* m, int32_t pos) {
     if (pos < 0 || pos >= m->d.context) return fail(LLMDOT_E_RANGE, "position outside the KV cache");
     return 0;
 }
+// Device waits that gave up (the attention's chunk-maximum exchange) leave a
+// flag; it is reported once and cleared.
+int check_device_flags(llmdot_hip_model* m) {
+    hipStream_t s = m->ctx->stream;
+    int32_t err = 0;
+    HIPCHK(hipMemcpyAsync(&err, m_err(m), sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    HIPCHK(hipStreamSynchronize(s));
+    if (err) {
+        HIPCHK(launch_set_scalar(m_err(m), 0, s));
+        HIPCHK(hipStreamSynchronize(s));
+        return fail(LLMDOT_E_DEVICE, "decode attention: a workgroup gave up waiting for the chunk maxima of its kv "
+                                     "head (spin limit); the step's results are invalid");
+    }
+    return 0;
+}
+
 int fetch_outputs(llmdot_hip_model* m, float* logits, int32_t* am) {
     hipStream_t s = m->ctx->stream;
     if (logits) HIPCHK(hipMemcpyAsync(logits, m->logits, sizeof(float) * (size_t)m->d.vocab, hipMemcpyDeviceToHost, s));
     if (am) HIPCHK(hipMemcpyAsync(am, m_token(m), sizeof(int32_t), hipMemcpyDeviceToHost, s));
     HIPCHK(hipStreamSynchronize(s));
-    return 0;
+    return check_device_flags(m);
 }
 }  // namespace
 
@@ -1388,6 +1418,7 @@ int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, 
     }
     HIPCHK(hipMemcpyAsync(tokens_out, m->token_log, sizeof(int32_t) * (size_t)produce, hipMemcpyDeviceToHost, s));
     HIPCHK(hipStreamSynchronize(s));
+    if (int rc = check_device_flags(m)) return rc;
     int n = produce;
     if (eos >= 0)
         for (int i = 0; i < produce; i++)
@@ -1529,6 +1560,7 @@ extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t fir
     HIPCHK(hipEventElapsedTime(&total, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    if (int rc = check_device_flags(m)) return rc;
     const double gemv_ms = per_kernel ? total : 0.0;
     out->total_ms = total;
     out->gemv_ms = (float)gemv_ms;

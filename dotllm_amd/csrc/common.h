@@ -169,6 +169,15 @@ __device__ __forceinline__ float rope_elem(const float* x, int d, int half, cons
     return x[d];
 }
 
+// rope_elem with the operands already loaded: a = x[d], b = its partner
+// (x[d + half] below half, x[d - half] above), c/s = cos/sin of the pair.
+__device__ __forceinline__ float rope_pair(float a, float b, float c, float s, int d, int half) {
+#pragma clang fp contract(off)
+    if (d < half) return a * c - b * s;
+    if (d < 2 * half) return b * s + a * c;
+    return a;
+}
+
 // Stores one KV cache element (fp16: round to nearest even) and returns the
 // value as later reads see it.
 __device__ __forceinline__ float store_kv(void* cache, int64_t idx, float v, int fp16) {

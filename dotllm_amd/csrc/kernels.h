@@ -45,6 +45,7 @@ struct ArgmaxState {
     // from input[0] and compares with '>', so a NaN there is never replaced
     // and the result is 0; NaN elsewhere never wins (set by the launchers)
     const float* first;
+    uint32_t* epoch;      // optional: incremented by the second pass (decode-step counter)
 };
 
 struct GemvArgs {
@@ -111,8 +112,24 @@ struct AttnArgs {
     float* part_sum;        // [max_chunks][heads]
     float* out;             // [heads][head_dim]
     int heads, kv_heads, head_dim, rope_half, context, kv_fp16;
+    // One-launch scores and values (fused != 0): the workgroups of a kv head
+    // exchange their chunk maxima through tagged 64-bit slots, (tag << 32) |
+    // float bits, stored and loaded at system scope (past the per-XCD L2s), so
+    // a reader sees an older tag or the whole new pair; tag = epoch * layers +
+    // layer + 1 is new for every (decode step, layer).  A wait gives up after
+    // spin_max polls and sets *err.
+    int fused;
+    uint64_t* xmax;         // [kv_heads][group][max_chunks]
+    const uint32_t* epoch;  // decode steps so far (advanced by the head's argmax pass)
+    int layer, layers, spin_max;
+    int32_t* err;
 };
+// Slots of AttnArgs::xmax for `heads` q heads.
+int attn_xmax_slots(int heads);
 int attn_max_chunks(int heads, int kv_heads, int context);
+// Whether the one-launch path applies (every chunk maximum of a head fits
+// one wavefront's four slots per lane).
+bool attn_fused_ok(int heads, int kv_heads, int head_dim, int context);
 bool attn_supported(int heads, int kv_heads, int head_dim);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 

@@ -164,6 +164,7 @@ __global__ __launch_bounds__(WG) void argmax_finish_kernel(ArgmaxState st, int n
             *st.step = k + 1;
         }
         if (st.pos) *st.pos += 1;
+        if (st.epoch) *st.epoch += 1u;
     }
 }
 

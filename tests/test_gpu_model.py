@@ -339,3 +339,62 @@ def test_mistral7b_greedy64_golden(hip):
         assert same >= well_posed, kv_fp16
         assert max(free) <= tol and max(forced) <= tol, kv_fp16
         assert not flips, (kv_fp16, flips)
+
+
+def _fresh_engine_env(img, env, context, kv_fp16=True):
+    """An engine created with extra environment settings (read at model creation)."""
+    import os
+    from dotllm_amd.backend import HipBackend
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        be = HipBackend(0)
+        eng = InferenceEngine(LoadedModel.load(img), be, kv_fp16=kv_fp16, context=context)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    return be, eng
+
+
+@pytest.mark.parametrize("name,kv_fp16,tol", [("tiny", False, 1e-4), ("mistral7b", True, DEEP_LOGIT_TOL)])
+def test_attention_one_launch_matches_three(name, kv_fp16, tol, tiny_image, mistral7b_long_image):
+    """The one-launch attention (chunk maxima exchanged between workgroups)
+    and the three-launch form compute the same sums in different orders (the
+    dot products are split over two threads per key instead of four): over
+    decode steps at a 448 / 2048-position seeded cache, logits within fp32
+    noise for the 4-layer tiny model, within the 32-layer bound for the 7B
+    shape (where a reordered sum alone moves the logits by up to 3.8e-2)."""
+    img, n = (tiny_image, 448) if name == "tiny" else (mistral7b_long_image, 2048)
+    outs = []
+    for fused in ("1", "0"):
+        be, eng = _fresh_engine_env(img, {"LLMDOT_HIP_ATTN_FUSED": fused}, n + 16, kv_fp16=kv_fp16)
+        eng.kv_fill_random(n, seed=3)
+        outs.append([eng.process_token(t, n + i) for i, t in enumerate((5, 77, 901))])
+        eng.dispose()
+        be.dispose()
+    errs = [float(np.max(np.abs(a - b))) for a, b in zip(*outs)]
+    print(f"{name}: one launch vs three, max |dlogit| per step {['%.2e' % e for e in errs]}")
+    assert max(errs) <= tol
+
+
+def test_attention_wait_limit_reports_error(tiny_image):
+    """A workgroup that gives up waiting for the other chunks' maxima (forced
+    from the host with a spin limit of 0 polls) makes the step fail with a
+    device error instead of returning its logits; the flag is cleared after
+    being reported.  Every kernel still runs to completion."""
+    from dotllm_amd import _lib
+    be, eng = _fresh_engine_env(tiny_image, {"LLMDOT_HIP_ATTN_SPIN": "0"}, 512)
+    eng.kv_fill_random(448, seed=2)
+    errors = 0
+    for i in range(4):
+        try:
+            eng.process_token(3, 448 + i)
+        except _lib.HipError as e:
+            assert e.code == _lib.E_DEVICE and "gave up waiting" in str(e)
+            errors += 1
+    eng.dispose()
+    be.dispose()
+    assert errors >= 1
