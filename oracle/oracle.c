@@ -24,9 +24,15 @@
 #define VEC 8 /* Vector<float>.Count on x86-64 AVX2 */
 
 static int g_threads = 1;
+/* Reduction order: 0 = the reference's; 1 = another valid fp32 order used
+ * only to measure how far summation order alone moves the results (see
+ * orc_set_order in oracle.h). */
+static int g_order = 0;
 
 void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 int orc_get_threads(void) { return g_threads; }
+void orc_set_order(int order) { g_order = order ? 1 : 0; }
+int orc_get_order(void) { return g_order; }
 
 static inline float bits_to_float(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
 static inline uint32_t float_to_bits(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
@@ -34,6 +40,24 @@ static inline uint32_t float_to_bits(float f) { uint32_t b; memcpy(&b, &f, 4); r
 /* Vector.Dot(acc, Vector<float>.One): per-128-bit-lane DPPS, then lane sum. */
 static inline float hsum8(const float v[VEC]) {
     return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+
+/* Order 1's lane count for the reductions the reference runs over
+ * Vector<float> lanes (what .NET gives with 512-bit vectors). */
+#define VEC_ALT 16
+static inline float hsum16(const float v[VEC_ALT]) { return hsum8(v) + hsum8(v + 8); }
+
+/* Sum of x[0..n) in the lanes-then-tail order of the reference's vector loops:
+ * 8 lanes (order 0) or 16 (order 1), horizontal sum, then the tail in order. */
+static float lane_sum(const float* x, int n) {
+    const int L = g_order ? VEC_ALT : VEC;
+    float acc[VEC_ALT] = {0};
+    int i = 0;
+    for (; i <= n - L; i += L)
+        for (int l = 0; l < L; l++) acc[l] = acc[l] + x[i + l];
+    float s = L == VEC ? hsum8(acc) : hsum16(acc);
+    for (; i < n; i++) s += x[i];
+    return s;
 }
 
 /* ---------------------------------------------------------------- HH ---- */
@@ -778,18 +802,27 @@ void orc_softmax(float* in, int n, int has_softcap, float cap) {
         in[j] = expf(in[j] - max);
         sum += in[j];
     }
+    if (g_order) sum = lane_sum(in, n);   /* the same exponentials, summed in order 1 */
     float invSum = 1.0f / sum;
     for (int i = 0; i < n; i++) in[i] = in[i] * invSum;
 }
 
 /* VectorMath.RmsNorm, VM:308-340 */
 void orc_rms_norm(const float* in, const float* w, float* out, int n, float eps) {
-    float ssv[VEC] = {0};
+    float ss;
     int i = 0;
-    for (; i <= n - VEC; i += VEC)
-        for (int l = 0; l < VEC; l++) ssv[l] = ssv[l] + in[i + l] * in[i + l];
-    float ss = hsum8(ssv);
-    for (; i < n; i++) ss += in[i] * in[i];
+    if (g_order) {
+        float* sq = (float*)malloc(sizeof(float) * (size_t)n);
+        for (int e = 0; e < n; e++) sq[e] = in[e] * in[e];
+        ss = lane_sum(sq, n);
+        free(sq);
+    } else {
+        float ssv[VEC] = {0};
+        for (; i <= n - VEC; i += VEC)
+            for (int l = 0; l < VEC; l++) ssv[l] = ssv[l] + in[i + l] * in[i + l];
+        ss = hsum8(ssv);
+        for (; i < n; i++) ss += in[i] * in[i];
+    }
     ss /= (float)n;
     ss += eps;
     float invNorm = 1.0f / sqrtf(ss);
@@ -1297,6 +1330,60 @@ static inline float kv_store(const orc_model* m, float x) {
     return m->kv_fp16 ? orc_half_to_float(orc_float_to_half(x)) : x;
 }
 
+/* One q head h at `position` over the cached K/V of `layer` (IE:384-442):
+ * score_s = (q . K_s) * (1/sqrt(hd)) with 8-lane partial sums, Softmax, then
+ * out = sum_s V_s * p_s with s ascending.  q head h reads kv head h / (H/Hkv). */
+static void attend_head(const orc_model* m, int layer, int position, int h, const float* qs, float* rs) {
+    const orc_config* c = &m->cfg;
+    int hd = c->head_dim, H = c->heads, Hkv = c->kv_heads, kvdim = Hkv * hd;
+    int seqLen = position + 1;
+    int attnStart = c->sliding_window > 0 ? (seqLen - c->sliding_window > 0 ? seqLen - c->sliding_window : 0) : 0;
+    int attnLen = seqLen - attnStart;
+    const float* keys = m->kcache + (size_t)layer * (size_t)m->cache_ctx * (size_t)kvdim;
+    const float* values = m->vcache + (size_t)layer * (size_t)m->cache_ctx * (size_t)kvdim;
+    int group = H / Hkv;
+    float invSqrt = 1.0f / sqrtf((float)hd);
+    int kvH = h / group;
+    float* score = (float*)malloc(sizeof(float) * (size_t)attnLen);
+    float prod[512];
+    for (int s = attnStart; s < seqLen; s++) {
+        const float* kr = keys + (size_t)s * kvdim + (size_t)kvH * hd;
+        float dot;
+        if (g_order) {
+            for (int d = 0; d < hd; d++) prod[d] = qs[d] * kr[d];
+            dot = lane_sum(prod, hd);
+        } else {
+            float acc[VEC] = {0};
+            int d = 0;
+            for (; d <= hd - VEC; d += VEC)
+                for (int l = 0; l < VEC; l++) acc[l] = acc[l] + qs[d + l] * kr[d + l];
+            dot = hsum8(acc);
+            for (; d < hd; d++) dot += qs[d] * kr[d];
+        }
+        score[s - attnStart] = dot * invSqrt;
+    }
+    orc_softmax(score, attnLen, 0, 0.0f);
+    for (int d = 0; d < hd; d++) rs[d] = 0.0f;
+    if (g_order) {   /* order 1: partial sums over 64-position chunks, chunks in order */
+        for (int s0 = 0; s0 < attnLen; s0 += 64) {
+            for (int d = 0; d < hd; d++) prod[d] = 0.0f;
+            for (int s = s0; s < attnLen && s < s0 + 64; s++) {
+                float sc = score[s];
+                const float* vr = values + (size_t)(attnStart + s) * kvdim + (size_t)kvH * hd;
+                for (int d = 0; d < hd; d++) prod[d] = prod[d] + vr[d] * sc;
+            }
+            for (int d = 0; d < hd; d++) rs[d] = rs[d] + prod[d];
+        }
+    } else {
+        for (int s = 0; s < attnLen; s++) {
+            float sc = score[s];
+            const float* vr = values + (size_t)(attnStart + s) * kvdim + (size_t)kvH * hd;
+            for (int d = 0; d < hd; d++) rs[d] = rs[d] + vr[d] * sc;
+        }
+    }
+    free(score);
+}
+
 /* AttentionForward, IE:304-450 (separate Q/K/V, no q/k norm, no softcap). */
 static int attention(orc_model* m, int layer, int position) {
     orc_config* c = &m->cfg;
@@ -1323,39 +1410,9 @@ static int attention(orc_model* m, int layer, int position) {
             m->vcache[slot + (size_t)h * hd + d] = kv_store(m, vh[d]);
         }
     }
-    int seqLen = position + 1;
-    int attnStart = c->sliding_window > 0 ? (seqLen - c->sliding_window > 0 ? seqLen - c->sliding_window : 0) : 0;
-    int attnLen = seqLen - attnStart;
-    const float* keys = m->kcache + (size_t)layer * (size_t)m->cache_ctx * (size_t)kvdim;
-    const float* values = m->vcache + (size_t)layer * (size_t)m->cache_ctx * (size_t)kvdim;
-    int group = H / Hkv;
-    float invSqrt = 1.0f / sqrtf((float)hd);
     float* result = m->attn_result;
 #pragma omp parallel for num_threads(g_threads) schedule(static)
-    for (int h = 0; h < H; h++) {
-        int kvH = h / group;
-        const float* qs = m->q + h * hd;
-        float* score = (float*)malloc(sizeof(float) * (size_t)attnLen);
-        for (int s = attnStart; s < seqLen; s++) {
-            const float* kr = keys + (size_t)s * kvdim + (size_t)kvH * hd;
-            float acc[VEC] = {0};
-            int d = 0;
-            for (; d <= hd - VEC; d += VEC)
-                for (int l = 0; l < VEC; l++) acc[l] = acc[l] + qs[d + l] * kr[d + l];
-            float dot = hsum8(acc);
-            for (; d < hd; d++) dot += qs[d] * kr[d];
-            score[s - attnStart] = dot * invSqrt;
-        }
-        orc_softmax(score, attnLen, 0, 0.0f);
-        float* rs = result + h * hd;
-        for (int d = 0; d < hd; d++) rs[d] = 0.0f;
-        for (int s = 0; s < attnLen; s++) {
-            float sc = score[s];
-            const float* vr = values + (size_t)(attnStart + s) * kvdim + (size_t)kvH * hd;
-            for (int d = 0; d < hd; d++) rs[d] = rs[d] + vr[d] * sc;
-        }
-        free(score);
-    }
+    for (int h = 0; h < H; h++) attend_head(m, layer, position, h, m->q + h * hd, result + h * hd);
     int outCols = (int)(m->wo[layer]->nelem / (uint32_t)(H * hd));
     rc = matmul_tensor(m, result, m->wo[layer], m->attn_out, outCols);
     memcpy(m->attn_result, m->attn_out, sizeof(float) * (size_t)hidden);
@@ -1468,5 +1525,280 @@ int orc_kv_read(const orc_model* m, int layer, int position, float* k, float* v)
     size_t slot = ((size_t)layer * m->cache_ctx + position) * kvdim;
     memcpy(k, m->kcache + slot, sizeof(float) * (size_t)kvdim);
     memcpy(v, m->vcache + slot, sizeof(float) * (size_t)kvdim);
+    return 0;
+}
+
+/* ===================================================== prompt batches ====== */
+/* Prompt processing with the tokens of a chunk going through each layer
+ * together.  No counterpart in the reference (Generate processes the prompt
+ * one ProcessToken at a time, IE:84-88): this is test infrastructure that
+ * makes long prompts affordable for the expected-value runs.  Every token
+ * gets exactly the operations orc_process_token applies at its position, in
+ * the same order, so the KV cache and the last token's logits are bitwise
+ * those of the sequential loop (tests/test_oracle.py pins this).  The speed
+ * comes from dequantising each weight row once per chunk instead of once per
+ * token, and from evaluating many tokens' identical scalar recurrences side
+ * by side (SIMD across tokens, never across one token's sum). */
+
+/* How TensorOps.MatMul accumulates one activation row (aRows == 1, TO:60-90):
+ * Q2_K/Q4_K/Q5_K fused kernels sum a[i] * deq[i] sequentially (TO:293-329,
+ * 364-431); Q3_K sums ((a[i] * d) * sc) * value sequentially (TO:331-362);
+ * Q4_0/Q8_0 (fused), Q6_K (dequantise, then DotProduct) and every other type
+ * (TO:92-111) add a[i] * deq[i] into 8 lanes, then the horizontal sum and the
+ * scalar tail (TO:118-287, 510-531).  The per-element dequantised values equal
+ * DequantizeRow's bit for bit (same expressions). */
+enum { ACC_SEQ = 0, ACC_LANE8 = 1, ACC_Q3K = 2 };
+static int acc_mode(uint32_t t) {
+    if (t == ORC_Q2_K || t == ORC_Q4_K || t == ORC_Q5_K) return ACC_SEQ;
+    if (t == ORC_Q3_K) return ACC_Q3K;
+    return ACC_LANE8;
+}
+
+#define PF_TB 64   /* tokens per inner block */
+#define PF_RB 8    /* weight rows per inner block */
+
+/* out[t * ldo + c] for the T activation rows at[i * T + t] (transposed), rows
+ * c of the dequantised block deq[j * K + i]. */
+/* Vectorised across tokens only: each (row, token) sum keeps its own order,
+ * and without -ffast-math the compiler may not reassociate it. */
+__attribute__((target_clones("avx2", "default"), optimize("tree-vectorize")))
+static void pf_rows_seq(const float* at, int T, int K, const float* deq, int nr, float* out, int ldo, int c0) {
+    for (int t0 = 0; t0 < T; t0 += PF_TB) {
+        int tb = T - t0 < PF_TB ? T - t0 : PF_TB;
+        float acc[PF_RB][PF_TB];
+        memset(acc, 0, sizeof acc);
+        if (g_order) {   /* order 1: a partial per 32-element group, groups added in order */
+            float gp[PF_RB][PF_TB];
+            for (int g0 = 0; g0 < K; g0 += 32) {
+                memset(gp, 0, sizeof gp);
+                for (int i = g0; i < g0 + 32 && i < K; i++) {
+                    const float* ai = at + (size_t)i * T + t0;
+                    for (int j = 0; j < nr; j++) {
+                        const float w = deq[(size_t)j * K + i];
+                        for (int t = 0; t < tb; t++) gp[j][t] = gp[j][t] + ai[t] * w;
+                    }
+                }
+                for (int j = 0; j < nr; j++)
+                    for (int t = 0; t < tb; t++) acc[j][t] = acc[j][t] + gp[j][t];
+            }
+        } else {
+            for (int i = 0; i < K; i++) {
+                const float* ai = at + (size_t)i * T + t0;
+                for (int j = 0; j < nr; j++) {
+                    const float w = deq[(size_t)j * K + i];
+                    for (int t = 0; t < tb; t++) acc[j][t] = acc[j][t] + ai[t] * w;
+                }
+            }
+        }
+        for (int j = 0; j < nr; j++)
+            for (int t = 0; t < tb; t++) out[(size_t)(t0 + t) * ldo + c0 + j] = acc[j][t];
+    }
+}
+
+__attribute__((target_clones("avx2", "default"), optimize("tree-vectorize")))
+static void pf_rows_lane8(const float* at, int T, int K, const float* deq, int nr, float* out, int ldo, int c0) {
+    const int L = g_order ? VEC_ALT : VEC;   /* lanes: the reference's 8, or order 1's 16 */
+    const int KL = (K / L) * L;
+    for (int t0 = 0; t0 < T; t0 += PF_TB) {
+        int tb = T - t0 < PF_TB ? T - t0 : PF_TB;
+        float acc[PF_RB][VEC_ALT][PF_TB];
+        memset(acc, 0, sizeof acc);
+        for (int k = 0; k < KL; k += L)
+            for (int l = 0; l < L; l++) {
+                const float* ai = at + (size_t)(k + l) * T + t0;
+                for (int j = 0; j < nr; j++) {
+                    const float w = deq[(size_t)j * K + k + l];
+                    for (int t = 0; t < tb; t++) acc[j][l][t] = acc[j][l][t] + ai[t] * w;
+                }
+            }
+        for (int j = 0; j < nr; j++)
+            for (int t = 0; t < tb; t++) {
+                float v[VEC_ALT];
+                for (int l = 0; l < L; l++) v[l] = acc[j][l][t];
+                float dot = L == VEC ? hsum8(v) : hsum16(v);
+                for (int i = KL; i < K; i++) dot += at[(size_t)i * T + t0 + t] * deq[(size_t)j * K + i];
+                out[(size_t)(t0 + t) * ldo + c0 + j] = dot;
+            }
+    }
+}
+
+/* Q3_K: per element the block scale d, the 6-bit group scale and the signed
+ * 3-bit value, applied as ((a * d) * sc) * value (TO:331-362). */
+static void pf_rows_q3k(const float* at, int T, int K, const uint8_t* wrow, float* out, int ldo, int c) {
+    const int qk = 256, bsz = 110;
+    for (int t = 0; t < T; t++) {
+        float dot = 0.0f;
+        for (int blk = 0; blk < K / qk; blk++) {
+            const uint8_t* p = wrow + blk * bsz;
+            float d = h2f_at(p);
+            for (int i = 0; i < qk; i++) {
+                int sc = orc_extract6(p, 4, (i / 16) * 6);
+                int q = (p[48 + i / 4] >> ((i % 4) * 2)) & 0x3;
+                int mm = (p[16 + i / 8] >> (i % 8)) & 0x1;
+                dot += at[(size_t)(blk * qk + i) * T + t] * d * (float)sc * (float)(q - (mm << 2));
+            }
+        }
+        out[(size_t)t * ldo + c] = dot;
+    }
+}
+
+/* Row r of a Q4_K / Q5_K tensor as DequantizeRow gives it (DK:76-140): the
+ * same per-element expression d * sc * (q - c) - dmin * m with the two
+ * 6-bit fields extracted once per sub-block instead of once per element;
+ * every other type goes through dequantize_row itself. */
+static int pf_deq_row(const uint8_t* src, float* dst, uint32_t type, int row, int K) {
+    if (type != ORC_Q4_K && type != ORC_Q5_K) return dequantize_row(src, dst, type, row, K);
+    const int q5 = type == ORC_Q5_K, bsz = q5 ? 176 : 144;
+    const uint8_t* base = src + (int64_t)row * (K / 256) * bsz;
+    for (int b = 0; b < K / 256; b++) {
+        const uint8_t* p = base + b * bsz;
+        const float d = h2f_at(p), dmin = h2f_at(p + 2);
+        for (int g = 0; g < 8; g++) {
+            const int sc = orc_extract6(p, 4, g * 12), mi = orc_extract6(p, 4, g * 12 + 6);
+            for (int i = 32 * g; i < 32 * g + 32; i++) {
+                float v;
+                if (q5) {
+                    int qLow = (p[48 + i / 2] >> ((i % 2) * 4)) & 0xF, qHigh = (p[16 + i / 8] >> (i % 8)) & 0x1;
+                    v = d * (float)sc * (float)(qLow + (qHigh << 4) - 16) - dmin * (float)mi;
+                } else {
+                    int q = (p[16 + i / 2] >> ((i % 2) * 4)) & 0xF;
+                    v = d * (float)sc * (float)(q - 8) - dmin * (float)mi;
+                }
+                dst[b * 256 + i] = v;
+            }
+        }
+    }
+    return 0;
+}
+
+/* out[t][0..N) = MatMulFromTensor(a[t], w) for t < T (IE:604-617), each row
+ * as its own single-row call would compute it. */
+static int pf_matmul(const float* a, int T, const gg_tensor* w, float* out, int N) {
+    const int K = (int)w->dims[0];
+    const uint32_t type = w->type;
+    if (type == ORC_BF16 || orc_byte_count(type, (uint64_t)K) < 0) return -1;
+    float* at = (float*)malloc(sizeof(float) * (size_t)K * (size_t)T);
+    if (!at) return -1;
+    for (int t = 0; t < T; t++)
+        for (int i = 0; i < K; i++) at[(size_t)i * T + t] = a[(size_t)t * K + i];
+    const int mode = type == ORC_F32 ? ACC_LANE8 : acc_mode(type);
+    const int64_t rb = orc_byte_count(type, (uint64_t)K);
+    int fail = 0;
+#pragma omp parallel num_threads(g_threads) reduction(| : fail)
+    {
+        float* deq = (float*)malloc(sizeof(float) * (size_t)K * PF_RB);   /* one per thread */
+#pragma omp for schedule(dynamic, 4)
+        for (int c0 = 0; c0 < N; c0 += PF_RB) {
+            const int nr = N - c0 < PF_RB ? N - c0 : PF_RB;
+            if (mode == ACC_Q3K) {
+                for (int j = 0; j < nr; j++) pf_rows_q3k(at, T, K, w->data + (int64_t)(c0 + j) * rb, out, N, c0 + j);
+                continue;
+            }
+            int bad = !deq;
+            for (int j = 0; j < nr && !bad; j++)
+                if (pf_deq_row(w->data, deq + (size_t)j * K, type, c0 + j, K) != 0) bad = 1;
+            if (!bad) {
+                if (mode == ACC_SEQ) pf_rows_seq(at, T, K, deq, nr, out, N, c0);
+                else pf_rows_lane8(at, T, K, deq, nr, out, N, c0);
+            }
+            fail |= bad;
+        }
+        free(deq);
+    }
+    free(at);
+    return fail ? -1 : 0;
+}
+
+int orc_matmul_rows(const float* a, int rows, const uint8_t* b, uint32_t type, int a_cols, int b_cols, float* out) {
+    gg_tensor w;
+    memset(&w, 0, sizeof w);
+    w.type = type;
+    w.dims[0] = (uint64_t)a_cols;
+    w.dims[1] = (uint64_t)b_cols;
+    w.data = b;
+    return pf_matmul(a, rows, &w, out, b_cols);
+}
+
+int orc_prefill(orc_model* m, const int* tokens, int n, int pos0, float* logits) {
+    orc_config* c = &m->cfg;
+    if (n <= 0) return 0;
+    if (pos0 < 0 || pos0 + n > m->cache_ctx) return -2;
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= m->embd->dims[1]) return -3;
+    const int d = c->hidden, hd = c->head_dim, H = c->heads, Hkv = c->kv_heads;
+    const int qdim = H * hd, kvdim = Hkv * hd, F = c->ffn;
+    const int half = (c->rope_dim > 0 ? c->rope_dim : hd) / 2;
+    const int CH = 512;
+    const int cap = n < CH ? n : CH;
+    float* X = (float*)malloc(sizeof(float) * (size_t)cap * d);    /* hidden states */
+    float* Nn = (float*)malloc(sizeof(float) * (size_t)cap * d);   /* normed */
+    float* Q = (float*)malloc(sizeof(float) * (size_t)cap * qdim);
+    float* Kb = (float*)malloc(sizeof(float) * (size_t)cap * kvdim);
+    float* Vb = (float*)malloc(sizeof(float) * (size_t)cap * kvdim);
+    float* A = (float*)malloc(sizeof(float) * (size_t)cap * qdim);  /* attention output */
+    float* O = (float*)malloc(sizeof(float) * (size_t)cap * d);
+    float* G = (float*)malloc(sizeof(float) * (size_t)cap * F);
+    float* U = (float*)malloc(sizeof(float) * (size_t)cap * F);
+    int rc = (X && Nn && Q && Kb && Vb && A && O && G && U) ? 0 : -4;
+    const int64_t rowBytes = orc_byte_count(m->embd->type, (uint64_t)m->embd->dims[0]);
+    for (int c0 = 0; c0 < n && !rc; c0 += cap) {
+        const int T = n - c0 < cap ? n - c0 : cap;
+        for (int t = 0; t < T; t++)   /* GetEmbedding, IE:148-156 */
+            orc_dequantize(m->embd->data + (int64_t)tokens[c0 + t] * rowBytes, X + (size_t)t * d, m->embd->type, 1,
+                           (int)m->embd->dims[0]);
+        for (int l = 0; l < c->layers && !rc; l++) {
+            for (int t = 0; t < T; t++) orc_rms_norm(X + (size_t)t * d, m->attn_norm_f[l], Nn + (size_t)t * d, d, c->eps);
+            rc |= pf_matmul(Nn, T, m->wq[l], Q, qdim);
+            rc |= pf_matmul(Nn, T, m->wk[l], Kb, kvdim);
+            rc |= pf_matmul(Nn, T, m->wv[l], Vb, kvdim);
+            if (rc) break;
+            for (int t = 0; t < T; t++) {   /* RoPE and the KV write of each token (IE:362-381) */
+                const int pos = pos0 + c0 + t;
+                float* qt = Q + (size_t)t * qdim;
+                float* kt = Kb + (size_t)t * kvdim;
+                const float* vt = Vb + (size_t)t * kvdim;
+                for (int h = 0; h < H; h++) orc_rope_table(qt + h * hd, qt + h * hd, hd, pos, m->rope_freqs, half, 1);
+                size_t slot = ((size_t)l * (size_t)m->cache_ctx + (size_t)pos) * (size_t)kvdim;
+                for (int h = 0; h < Hkv; h++) {
+                    float* kh = kt + h * hd;
+                    orc_rope_table(kh, kh, hd, pos, m->rope_freqs, half, 1);
+                    for (int e = 0; e < hd; e++) {
+                        m->kcache[slot + (size_t)h * hd + e] = kv_store(m, kh[e]);
+                        m->vcache[slot + (size_t)h * hd + e] = kv_store(m, vt[h * hd + e]);
+                    }
+                }
+            }
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 1)
+            for (int th = 0; th < T * H; th++) {
+                const int t = th / H, h = th % H;
+                attend_head(m, l, pos0 + c0 + t, h, Q + (size_t)t * qdim + h * hd, A + (size_t)t * qdim + h * hd);
+            }
+            rc |= pf_matmul(A, T, m->wo[l], O, d);
+            if (rc) break;
+            for (int t = 0; t < T; t++) {
+                orc_add_inplace(X + (size_t)t * d, O + (size_t)t * d, d);
+                orc_rms_norm(X + (size_t)t * d, m->ffn_norm_f[l], Nn + (size_t)t * d, d, c->eps);
+            }
+            rc |= pf_matmul(Nn, T, m->wg[l], G, F);
+            rc |= pf_matmul(Nn, T, m->wu[l], U, F);
+            if (rc) break;
+            for (int t = 0; t < T; t++) {   /* FfnForward SwiGLU (IE:457-476) */
+                orc_silu_inplace(G + (size_t)t * F, F);
+                orc_mul(G + (size_t)t * F, U + (size_t)t * F, G + (size_t)t * F, F);
+            }
+            rc |= pf_matmul(G, T, m->wd[l], O, d);
+            if (rc) break;
+            for (int t = 0; t < T; t++) orc_add_inplace(X + (size_t)t * d, O + (size_t)t * d, d);
+        }
+        if (!rc && c0 + T == n) {   /* the last token: final norm and logits (IE:575-602) */
+            memcpy(m->hidden, X + (size_t)(T - 1) * d, sizeof(float) * (size_t)d);
+            memcpy(m->normtmp, m->hidden, sizeof(float) * (size_t)d);
+            orc_rms_norm(m->normtmp, m->out_norm_f, m->hidden, d, c->eps);
+            rc |= pf_matmul(m->hidden, 1, m->out, m->logits, c->vocab);
+        }
+    }
+    free(X); free(Nn); free(Q); free(Kb); free(Vb); free(A); free(O); free(G); free(U);
+    if (rc) return rc;
+    if (logits) memcpy(logits, m->logits, sizeof(float) * (size_t)c->vocab);
     return 0;
 }

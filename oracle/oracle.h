@@ -78,6 +78,16 @@ int  orc_sample(const float* logits, int n, float temperature, int top_k, float 
 
 void orc_set_threads(int n);   /* row-parallel GEMV/attention; results are bitwise identical */
 int  orc_get_threads(void);
+/* Reduction order of orc_prefill (and of RmsNorm, Softmax and attention,
+ * which it shares with orc_process_token): 0 (default) is the reference's;
+ * 1 is another valid fp32 order -- 16 lanes instead of Vector<float>'s 8
+ * (what .NET gives with 512-bit vectors), a partial per 32-element group in
+ * the scalar K-quant GEMV sums, per-64-position partials in the attention's
+ * value sum.  Order 1 measures how far summation order alone moves the
+ * results (the tolerance floor of tests against other implementations);
+ * the fused single-row GEMVs of orc_process_token ignore it. */
+void orc_set_order(int order);
+int  orc_get_order(void);
 
 /* ---- model ------------------------------------------------------------- */
 typedef struct orc_config {
@@ -104,6 +114,15 @@ int  orc_model_set_context(orc_model* m, int context);
 
 /* ProcessToken (IE:134-146): writes VocabSize logits. */
 int orc_process_token(orc_model* m, int token, int position, float* logits);
+/* The last token's logits and the KV cache of n sequential ProcessToken calls
+ * (tokens[i] at position pos0 + i, IE:84-88), computed with the tokens of a
+ * chunk going through each layer together; bitwise identical to the loop.
+ * No reference counterpart (test infrastructure for long prompts). */
+int orc_prefill(orc_model* m, const int* tokens, int n, int pos0, float* logits);
+/* out[r][0..b_cols) = MatMul of activation row r (aRows == 1 each, TO:60-90)
+ * for r < rows, through orc_prefill's batched path: bitwise orc_matmul per
+ * row (tests pin this for every type). */
+int orc_matmul_rows(const float* a, int rows, const uint8_t* b, uint32_t type, int a_cols, int b_cols, float* out);
 /* Generate (IE:74-132) with greedy sampling.  tokens_out holds max_tokens
  * entries; logits_out (nullable) holds [max_tokens][vocab]: the logits each
  * sampled token was taken from.  eos < 0 disables the EOS stop. */

@@ -53,6 +53,8 @@ _SIG = {
     "orc_argmax": ([_P, _I], _I),
     "orc_sample": ([_P, _I, _F, _I, _F, _F, _I, _P, _I, _F], _I),
     "orc_set_threads": ([_I], None),
+    "orc_set_order": ([_I], None),
+    "orc_get_order": ([], _I),
     "orc_get_threads": ([], _I),
     "orc_model_open_buffer": ([_P, C.c_size_t, _I, C.c_char_p, _I], _P),
     "orc_model_open_file": ([C.c_char_p, _I, C.c_char_p, _I], _P),
@@ -60,6 +62,8 @@ _SIG = {
     "orc_model_config": ([_P, C.POINTER(Config)], None),
     "orc_model_set_context": ([_P, _I], _I),
     "orc_process_token": ([_P, _I, _I, _P], _I),
+    "orc_prefill": ([_P, _P, _I, _I, _P], _I),
+    "orc_matmul_rows": ([_P, _I, _P, C.c_uint32, _I, _I, _P], _I),
     "orc_generate": ([_P, _P, _I, _I, _I, _P, C.POINTER(C.c_int), _P], _I),
     "orc_kv_fill_random": ([_P, _I, C.c_uint64], _I),
     "orc_kv_read": ([_P, _I, _I, _P, _P], _I),
@@ -90,6 +94,11 @@ def set_threads(n: int) -> None:
     lib().orc_set_threads(int(n))
 
 
+def set_order(order: int) -> None:
+    """0: the reference's reduction order; 1: another valid fp32 order (see oracle.h)."""
+    lib().orc_set_order(int(order))
+
+
 def half_to_float(h: int) -> float:
     return lib().orc_half_to_float(h)
 
@@ -116,6 +125,17 @@ def matmul(a: np.ndarray, b: np.ndarray, ggml_type: int, a_cols: int, b_cols: in
     n = result_len or b_cols
     out = np.zeros(n, dtype=np.float32)
     if lib().orc_matmul(_p(a), _p(b), _p(out), n, ggml_type, a_cols, b_cols) != 0:
+        raise NotImplementedError(f"MatMul for type {ggml_type}")
+    return out
+
+
+def matmul_rows(a: np.ndarray, b: np.ndarray, ggml_type: int, a_cols: int, b_cols: int) -> np.ndarray:
+    """[rows][b_cols]: each activation row as its own single-row MatMul, through
+    the batched path of the prompt processing (bitwise the same)."""
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1, a_cols)
+    b = np.ascontiguousarray(b).reshape(-1).view(np.uint8)
+    out = np.zeros((a.shape[0], b_cols), dtype=np.float32)
+    if lib().orc_matmul_rows(_p(a), a.shape[0], _p(b), ggml_type, a_cols, b_cols, _p(out)) != 0:
         raise NotImplementedError(f"MatMul for type {ggml_type}")
     return out
 
@@ -235,6 +255,16 @@ class Model:
         rc = lib().orc_process_token(self._m, int(token), int(position), _p(out))
         if rc != 0:
             raise IndexError(f"ProcessToken failed ({rc})")
+        return out
+
+    def prefill(self, tokens, pos0: int = 0) -> np.ndarray:
+        """Logits of the last of len(tokens) ProcessToken calls from pos0, with the
+        chunk's tokens going through each layer together (bitwise the same)."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        out = np.zeros(self.config.vocab, dtype=np.float32)
+        rc = lib().orc_prefill(self._m, _p(t), t.size, int(pos0), _p(out))
+        if rc != 0:
+            raise IndexError(f"prefill failed ({rc})")
         return out
 
     def generate(self, prompt, max_tokens: int, eos: int | None = None, return_logits: bool = False):

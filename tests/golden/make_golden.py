@@ -16,11 +16,27 @@ Outputs (small, committed):
                   logits' sum and sum of squares
 
   python tests/golden/make_golden.py mistral7b    (about 20 minutes on 8 cores)
+  python tests/golden/make_golden.py floor7b      (adds the order-1 floor to it)
+  python tests/golden/make_golden.py long c3|c4|c5   (10-40 minutes each)
 
   mistral7b_greedy64.json  7B-shape Q4_K_M model (seed 1234), 16-token prompt
                   (seed 7), with fp16 and with fp32 KV: 64 greedy tokens and,
                   per step, the top-16 logits, the top-2 gap, and the logits'
                   mean and root mean square; plus a fingerprint of the image
+                  (floor7b adds, per step, the order-1 floor described below)
+
+  long_<config>.npz  the full-size workloads, from the oracle's batched prompt
+                  path (orc_prefill, bitwise the sequential loop) with greedy
+                  decoding after it:
+                    c3  llama1b,   512-token prompt + 256 tokens, fp32 KV
+                    c4  mistral7b, 2048-token prompt + 16 tokens, fp16 KV
+                    c5  phi3mini,  2048-token prompt + 256 tokens, fp32 KV
+                  per step: the top-16 logits, the top-2 gap, the logits' mean
+                  and root mean square; the KV rows of a few (layer, position)
+                  pairs; and per step the floor: max |logit difference| between
+                  the oracle in the reference's reduction order and in another
+                  valid fp32 order (orc_set_order(1)), teacher-forced on the same
+                  tokens -- what summation order alone moves the results by
 """
 import json
 import os
@@ -122,8 +138,121 @@ def mistral7b_greedy64():
     print("wrote mistral7b_greedy64.json")
 
 
+def step_stats(row):
+    """Top-16 indices and values (descending), top-2 gap, mean and RMS of one logits row."""
+    top = np.argsort(row, kind="stable")[::-1][:16]
+    r64 = row.astype(np.float64)
+    return top, row[top], float(row[top[0]] - row[top[1]]), float(r64.mean()), float(np.sqrt(np.mean(r64 * r64)))
+
+
+LONG = {
+    # name: (model, prompt tokens, generated tokens, fp16 KV, KV sample layers, KV sample positions)
+    "c3": ("llama1b", 512, 256, False, (0, 7, 15), (0, 1, 255, 511, 700)),
+    "c4": ("mistral7b", 2048, 16, True, (0, 15, 31), (0, 1, 1023, 2047, 2060)),
+    "c5": ("phi3mini", 2048, 256, False, (0, 15, 31), (0, 1, 1023, 2047, 2250)),
+}
+
+
+def long_run(key):
+    """Greedy run of one full-size workload in the reference's order, and the
+    same tokens teacher-forced through the order-1 oracle for the floor."""
+    import time
+    name, n_prompt, n_gen, kv_fp16, layers, positions = LONG[key]
+    ctx = n_prompt + n_gen + 8
+    img = synth.build_image(name, seed=1234, context=ctx)
+    vocab = synth.SPECS[name]["vocab"]
+    prompt = synth.prompt(vocab, n_prompt, seed=7)
+    O.set_threads(int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1)))
+    m0 = O.Model(img, kv_fp16=kv_fp16, context=ctx)
+    m1 = O.Model(img, kv_fp16=kv_fp16, context=ctx)
+    t0 = time.time()
+    O.set_order(0)
+    l0 = m0.prefill(prompt, 0)
+    O.set_order(1)
+    l1 = m1.prefill(prompt, 0)
+    O.set_order(0)
+    print(f"{key}: prompt of {n_prompt} in {time.time() - t0:.0f}s", flush=True)
+    toks, tidx, tval, gap, mean, rms, floor = [], [], [], [], [], [], []
+    for s in range(n_gen):
+        ti, tv, g, mu, r = step_stats(l0)
+        tok = O.argmax(l0)
+        assert tok == int(ti[0])
+        toks.append(tok); tidx.append(ti); tval.append(tv); gap.append(g); mean.append(mu); rms.append(r)
+        floor.append(float(np.max(np.abs(l1 - l0))))
+        if s + 1 < n_gen:
+            O.set_order(0)
+            l0 = m0.prefill([tok], n_prompt + s)
+            O.set_order(1)
+            l1 = m1.prefill([tok], n_prompt + s)
+            O.set_order(0)
+        if s % 16 == 15:
+            print(f"{key}: step {s + 1}/{n_gen}, floor so far {max(floor):.3e}, {time.time() - t0:.0f}s", flush=True)
+    kv = {}
+    for part in ("k", "v"):
+        kv[part] = np.zeros((len(layers), len(positions), m0.config.kv_heads * m0.config.head_dim), np.float32)
+        kv[part + "_floor"] = np.zeros((len(layers), len(positions)), np.float32)
+    for i, l in enumerate(layers):
+        for j, p in enumerate(positions):
+            k0, v0 = m0.kv_read(l, p)
+            k1, v1 = m1.kv_read(l, p)
+            kv["k"][i, j], kv["v"][i, j] = k0, v0
+            kv["k_floor"][i, j] = np.max(np.abs(k1 - k0))
+            kv["v_floor"][i, j] = np.max(np.abs(v1 - v0))
+    m0.close(); m1.close()
+    meta = dict(config=key, model=name, weights_seed=1234, prompt_seed=7, n_prompt=n_prompt, n_gen=n_gen,
+                kv_fp16=kv_fp16, image_context=ctx, image_fingerprint=image_fingerprint(img))
+    np.savez_compressed(os.path.join(HERE, f"long_{key}.npz"), meta=np.array(json.dumps(meta)),
+                        prompt=np.asarray(prompt, np.int32), tokens=np.asarray(toks, np.int32),
+                        top_idx=np.asarray(tidx, np.int32), top_val=np.asarray(tval, np.float32),
+                        gap=np.asarray(gap), mean=np.asarray(mean), rms=np.asarray(rms), floor=np.asarray(floor),
+                        kv_layers=np.asarray(layers, np.int32), kv_positions=np.asarray(positions, np.int32), **kv)
+    print(f"wrote long_{key}.npz in {time.time() - t0:.0f}s; max floor {max(floor):.3e}", flush=True)
+
+
+def floor7b():
+    """Adds to mistral7b_greedy64.json, per step of each run, the order-1 floor:
+    the reference-order logits are recomputed through orc_prefill (and must
+    equal the fixture's bit for bit), the order-1 logits on the same tokens."""
+    path = os.path.join(HERE, "mistral7b_greedy64.json")
+    with open(path) as f:
+        g = json.load(f)
+    img = synth.build_image(g["model"], seed=g["weights_seed"], context=g["image_context"])
+    assert image_fingerprint(img) == g["image_fingerprint"]
+    O.set_threads(int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1)))
+    prompt = g["prompt"]
+    for run in g["runs"]:
+        m0 = O.Model(img, kv_fp16=run["kv_fp16"], context=g["image_context"])
+        m1 = O.Model(img, kv_fp16=run["kv_fp16"], context=g["image_context"])
+        O.set_order(0)
+        l0 = m0.prefill(prompt, 0)
+        O.set_order(1)
+        l1 = m1.prefill(prompt, 0)
+        O.set_order(0)
+        for s, st in enumerate(run["steps"]):
+            top = st["top16"]
+            assert [int(i) for i in np.argsort(l0, kind="stable")[::-1][:16]] == top
+            assert np.array_equal(l0[top], np.asarray(st["top16_logits"], np.float32)), s
+            st["floor"] = float(np.max(np.abs(l1 - l0)))
+            if s + 1 < len(run["steps"]):
+                tok = run["tokens"][s]
+                O.set_order(0)
+                l0 = m0.prefill([tok], len(prompt) + s)
+                O.set_order(1)
+                l1 = m1.prefill([tok], len(prompt) + s)
+                O.set_order(0)
+        m0.close(); m1.close()
+        print(f"kv_fp16={run['kv_fp16']}: max floor {max(st['floor'] for st in run['steps']):.3e}", flush=True)
+    with open(path, "w") as f:
+        json.dump(g, f, indent=1)
+    print("updated mistral7b_greedy64.json")
+
+
 if __name__ == "__main__":
     if sys.argv[1:] == ["mistral7b"]:
         mistral7b_greedy64()
+    elif sys.argv[1:] == ["floor7b"]:
+        floor7b()
+    elif len(sys.argv) == 3 and sys.argv[1] == "long":
+        long_run(sys.argv[2])
     else:
         main()
