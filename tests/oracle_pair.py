@@ -1,0 +1,93 @@
+"""The oracle in the reference's summation order beside the same oracle in
+another valid fp32 order (orc_set_order(1)), fed the same tokens.
+
+The first gives the expected values; the distance between the two is how far
+summation order alone moves them -- the floor below which no implementation
+with different reductions (the device's tree sums, 24-bit GEMV activations,
+MFMA tiles) can be held.  Both step through the batched prompt path, which is
+bitwise the sequential ProcessToken loop in the reference order
+(tests/test_oracle_prefill.py) and applies order 1 to every reduction.
+
+Bounds built from it (logit_bounds): a step's logits within
+max(2e-2, 2 x the running maximum of the floor up to that step); greedy tokens
+compared up to the first top-2 gap below max(1e-2, twice that bound's floor
+part).  The factor 2: one reordering is one sample of the order noise, not an
+upper bound for another implementation, and the device departs from the
+reference's order in every reduction at once (and uses 24-bit activations in
+the GEMVs, two fp16 activation planes in the prompt GEMMs); measured device
+errors ran at 0.45 to 1.35 times the floor of the same steps.
+"""
+import numpy as np
+
+from oracle import oracle as O
+
+LOGIT_TOL = 2e-2
+NEAR_TIE = 1e-2
+FLOOR_MARGIN = 2.0
+
+
+def logit_bounds(floors):
+    """Per step: (max(2e-2, 2 x running max of floors), max(1e-2, 4 x running max))."""
+    run = np.maximum.accumulate(np.asarray(floors, dtype=np.float64))
+    return np.maximum(LOGIT_TOL, FLOOR_MARGIN * run), np.maximum(NEAR_TIE, 2 * FLOOR_MARGIN * run)
+
+
+class OraclePair:
+    def __init__(self, img, kv_fp16, context=None):
+        self.m0 = O.Model(img, kv_fp16=kv_fp16, context=context)
+        self.m1 = O.Model(img, kv_fp16=kv_fp16, context=context)
+        self.config = self.m0.config
+        self.floors = []   # max |logit difference| of every call so far
+
+    def _both(self, f):
+        try:
+            O.set_order(0)
+            l0 = f(self.m0)
+            O.set_order(1)
+            l1 = f(self.m1)
+        finally:
+            O.set_order(0)
+        self.floors.append(float(np.max(np.abs(l1 - l0))))
+        return l0
+
+    def prefill(self, tokens, pos0=0):
+        """Logits (reference order) of the last of tokens[i] at pos0 + i."""
+        return self._both(lambda m: m.prefill([int(t) for t in tokens], pos0))
+
+    def step(self, token, pos):
+        return self.prefill([token], pos)
+
+    def kv_fill_random(self, n, seed):
+        self.m0.kv_fill_random(n, seed)
+        self.m1.kv_fill_random(n, seed)
+
+    def kv_read(self, layer, pos):
+        return self.m0.kv_read(layer, pos)
+
+    def kv_floor(self, layer, pos):
+        """max |K/V difference| between the two orders at (layer, pos)."""
+        k0, v0 = self.m0.kv_read(layer, pos)
+        k1, v1 = self.m1.kv_read(layer, pos)
+        return max(float(np.max(np.abs(k1 - k0))), float(np.max(np.abs(v1 - v0))))
+
+    def bounds(self):
+        """logit_bounds of the calls so far: (logit bound, near-tie threshold) per call."""
+        return logit_bounds(self.floors)
+
+    def close(self):
+        self.m0.close()
+        self.m1.close()
+
+
+def greedy_run(img, kv_fp16, context, prompt, n_gen):
+    """The reference's greedy Generate (IE:74-132) in the reference order, the
+    order-1 oracle teacher-forced on its tokens beside it.  Returns (tokens,
+    logits [n_gen][vocab], pair) -- the logits of step s are those token s was
+    taken from; pair.floors[s] is that step's floor."""
+    pair = OraclePair(img, kv_fp16, context)
+    logits = [pair.prefill(prompt, 0)]
+    toks = [O.argmax(logits[0])]
+    for s in range(1, n_gen):
+        logits.append(pair.step(toks[-1], len(prompt) + s - 1))
+        toks.append(O.argmax(logits[-1]))
+    return toks, np.asarray(logits), pair

@@ -93,6 +93,31 @@ def test_gemv_matches_reference(hip, t, rows, cols):
     assert rel_err(y, ref) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_q4k_gemv_full_shapes(hip, rows, cols):
+    """The isolated Q4_K GEMV workload at its three shapes: weights N(0, 0.02)
+    quantized to the reference's Q4_K layout, x ~ N(0, 1).  The GEMV within
+    1e-3 of the reference MatMul (TO:364-395), and the whole matrix's
+    dequantisation bit-exact (DK:76-106)."""
+    w = np.zeros(rows * byte_count(Q4_K, cols), dtype=np.uint8)
+    synth.synth_tensor(Q4_K, rows, cols, 0xC2 + rows + cols, w)
+    x = np.random.default_rng(rows ^ cols).normal(0, 1, size=cols).astype(np.float32)
+    O.set_threads(16)
+    try:
+        ref = O.matmul(x, w, Q4_K, cols, rows)
+        deq = O.dequantize(w, Q4_K, rows, cols)
+    finally:
+        O.set_threads(1)
+    y = np.zeros(rows, dtype=np.float32)
+    hip.mat_mul(x, w, y, Q4_K, cols, rows)
+    err = rel_err(y, ref)
+    out = np.zeros(rows * cols, dtype=np.float32)
+    hip.dequantize_to_float(w, out, Q4_K, rows, cols)
+    print(f"Q4_K {rows} x {cols}: GEMV relative error {err:.2e}")
+    assert err <= GEMV_TOL
+    assert np.array_equal(out.view(np.uint32), deq.view(np.uint32))
+
+
 def test_gemv_resident_weight_key(hip):
     rows, cols = 128, 512
     w = weights(Q4_K, rows, cols, 9)
