@@ -910,12 +910,24 @@ static int sample_from(const float* p, int n, float r) {
 }
 
 /* Sampler.Sample, Sampler.cs:24-62.  recent = the recent-token list, r = the
- * uniform draw. */
-int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, float penalty, int window,
-               const int* recent, int n_recent, float r) {
+ * uniform draw.
+ *
+ * aliased = 1 is the reference as written: `scaled` is the first n floats of
+ * samplingBuf (Sampler.cs:30) and FindNucleus is handed samplingBuf again as
+ * its output `values` (Sampler.cs:48-50), so while it writes the sorted
+ * probabilities (values[i] = probabilities[indices[i]], Sampler.cs:150) it
+ * overwrites the probabilities it still reads: rank i reads the value already
+ * written at rank indices[i] whenever indices[i] < i.  Two consequences: the
+ * nucleus can close early with repeated (larger) values, and when it spans all
+ * n tokens the fall-through draw (Sampler.cs:61) walks the rewritten buffer --
+ * the probabilities in sorted order -- and returns a rank, not a token id.
+ * aliased = 0 gives FindNucleus a buffer of its own: the nucleus of the true
+ * probabilities, and the fall-through draw over them in token order. */
+int orc_sample_ex(const float* logits, int n, float temperature, int top_k, float top_p, float penalty, int window,
+                  const int* recent, int n_recent, float r, int aliased) {
     if (temperature <= 0.0f) return orc_argmax(logits, n);
     float* scaled = (float*)malloc(sizeof(float) * (size_t)n);
-    float* buf = (float*)malloc(sizeof(float) * (size_t)n);
+    float* buf = aliased ? scaled : (float*)malloc(sizeof(float) * (size_t)n);
     int* ibuf = (int*)malloc(sizeof(int) * (size_t)n);
     memcpy(scaled, logits, sizeof(float) * (size_t)n);
     apply_repeat_penalty(scaled, n, penalty, window, recent, n_recent);
@@ -939,10 +951,15 @@ int orc_sample(const float* logits, int n, float temperature, int top_k, float t
         }
         if (result < 0) result = sample_from(scaled, n, r);
     }
+    if (buf != scaled) free(buf);
     free(scaled);
-    free(buf);
     free(ibuf);
     return result;
+}
+
+int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, float penalty, int window,
+               const int* recent, int n_recent, float r) {
+    return orc_sample_ex(logits, n, temperature, top_k, top_p, penalty, window, recent, n_recent, r, 1);
 }
 
 /* ============================================================ GGUF ====== */

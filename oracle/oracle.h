@@ -75,6 +75,10 @@ int  orc_argmax(const float* x, int n);                       /* VM:412-425 */
 /* Sampler.Sample (Sampler.cs:24-62) with the uniform draw r given. */
 int  orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, float penalty, int window,
                 const int* recent, int n_recent, float r);
+/* aliased = 1: the reference as written (FindNucleus writes into the buffer it
+ * reads); 0: FindNucleus with a buffer of its own. */
+int  orc_sample_ex(const float* logits, int n, float temperature, int top_k, float top_p, float penalty,
+                   int window, const int* recent, int n_recent, float r, int aliased);
 
 void orc_set_threads(int n);   /* row-parallel GEMV/attention; results are bitwise identical */
 int  orc_get_threads(void);

@@ -52,6 +52,7 @@ _SIG = {
     "orc_rope_base": ([_P, _P, _I, _I, _F, _I, _I], None),
     "orc_argmax": ([_P, _I], _I),
     "orc_sample": ([_P, _I, _F, _I, _F, _F, _I, _P, _I, _F], _I),
+    "orc_sample_ex": ([_P, _I, _F, _I, _F, _F, _I, _P, _I, _F, _I], _I),
     "orc_set_threads": ([_I], None),
     "orc_set_order": ([_I], None),
     "orc_get_order": ([], _I),
@@ -211,12 +212,16 @@ def argmax(x):
     return lib().orc_argmax(_p(x), x.size)
 
 
-def sample(logits, temperature, top_k, top_p, repeat_penalty, window, recent, r):
-    """Sampler.Sample (Sampler.cs:24-62) with the uniform draw r given."""
+def sample(logits, temperature, top_k, top_p, repeat_penalty, window, recent, r, aliased=True):
+    """Sampler.Sample (Sampler.cs:24-62) with the uniform draw r given.
+
+    aliased=True is the reference as written, FindNucleus writing its sorted
+    values into the buffer that holds the probabilities it reads
+    (Sampler.cs:30, 48-50, 150); aliased=False gives it a buffer of its own."""
     x = np.ascontiguousarray(logits, dtype=np.float32)
     rec = np.ascontiguousarray(list(recent) if len(recent) else [0], dtype=np.int32)
-    return lib().orc_sample(_p(x), x.size, float(temperature), int(top_k), float(top_p), float(repeat_penalty),
-                            int(window), _p(rec), len(recent), float(r))
+    return lib().orc_sample_ex(_p(x), x.size, float(temperature), int(top_k), float(top_p), float(repeat_penalty),
+                               int(window), _p(rec), len(recent), float(r), int(bool(aliased)))
 
 
 class Model:

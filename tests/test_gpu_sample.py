@@ -9,7 +9,12 @@ top-p path: the device places the nucleus boundary and the draw with fp64 sums,
 the reference with sequential float sums, so the token must equal the oracle's
 unless r or TopP lies within float rounding of a cumulative boundary; a mismatch
 is accepted only if the oracle itself returns the device's token for r or TopP
-moved by at most 1e-4.
+moved by at most 1e-4.  The device computes the nucleus of the true
+probabilities: the oracle's FindNucleus with a buffer of its own
+(aliased=False).  The reference as written reuses the probability buffer for
+the sorted values (Sampler.cs:30, 48-50) and departs from that wherever a rank
+inside the nucleus holds a token id below its rank; where none does, the device
+matches the reference as written too (test_top_p_matches_reference_...).
 """
 from dataclasses import replace
 
@@ -31,15 +36,16 @@ def opts(temperature, top_k, top_p=1.0, penalty=1.0, window=0):
                            repeat_penalty_window_size=window)
 
 
-def ref(x, o, recent, r):
-    return O.sample(x, o.temperature, o.top_k, o.top_p, o.repeat_penalty, o.repeat_penalty_window_size, recent, r)
+def ref(x, o, recent, r, aliased=False):
+    return O.sample(x, o.temperature, o.top_k, o.top_p, o.repeat_penalty, o.repeat_penalty_window_size, recent, r,
+                    aliased=aliased)
 
 
-def near_boundary(x, o, recent, r, tok, eps=1e-4):
+def near_boundary(x, o, recent, r, tok, eps=1e-4, aliased=False):
     for d in (eps / 16, -eps / 16, eps / 4, -eps / 4, eps, -eps):
-        if ref(x, o, recent, min(max(r + d, 0.0), 1.0)) == tok:
+        if ref(x, o, recent, min(max(r + d, 0.0), 1.0), aliased) == tok:
             return True
-        if o.top_p < 1.0 and ref(x, replace(o, top_p=o.top_p + d), recent, r) == tok:
+        if o.top_p < 1.0 and ref(x, replace(o, top_p=o.top_p + d), recent, r, aliased) == tok:
             return True
     return False
 
@@ -94,6 +100,29 @@ def test_top_p_matches_oracle(hip, n, k, top_p):
         if got != want:
             mismatches += 1
             assert near_boundary(x, o, [], r, got), (r, want, got)
+    assert mismatches <= 1
+
+
+def test_top_p_matches_reference_without_back_reference(hip):
+    """Logits whose nucleus sits on high token ids (a block of 64 ids from
+    3000 raised by 8): no rank inside the nucleus holds an id below its rank,
+    so the reference as written (aliased buffers) and the device agree."""
+    n = 4096
+    x = logits_for(n, 77, 1.0)
+    x[3000:3064] += 8.0
+    o = opts(0.8, 0, 0.9)
+    p = np.exp((x - x.max()) / 0.8).astype(np.float64)
+    p /= p.sum()
+    order = np.argsort(-p, kind="stable")
+    m = int(np.searchsorted(np.cumsum(p[order]), 0.9)) + 1
+    assert m < 1000 and all(int(order[i]) >= i for i in range(m))
+    mismatches = 0
+    for r in R_ALL:
+        want, got = ref(x, o, [], r, aliased=True), hip.sample(x, o, [], r)
+        assert want == ref(x, o, [], r)
+        if got != want:
+            mismatches += 1
+            assert near_boundary(x, o, [], r, got, aliased=True), (r, want, got)
     assert mismatches <= 1
 
 

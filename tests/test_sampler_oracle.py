@@ -121,6 +121,11 @@ def test_top_k_draw_is_the_inverse_cdf(seed):
 
 @pytest.mark.parametrize("seed", range(3))
 def test_nucleus_size_and_draw_closed_form(seed):
+    """The nucleus of the true probabilities (FindNucleus with a buffer of its
+    own): its size and the renormalised draw inside it follow the fp64
+    cumulative distribution in descending order.  (With the reference's
+    aliasing, random logits over 300 ids reach back into rewritten slots;
+    the tests below pin that form.)"""
     rng = np.random.default_rng(100 + seed)
     n = 300
     x = rng.normal(0, 1.5, n).astype(np.float32)
@@ -136,7 +141,7 @@ def test_nucleus_size_and_draw_closed_form(seed):
             j = int(np.searchsorted(cdf[:m] / S, r))
             if np.min(np.abs(cdf[:m] / S - r)) < 5e-3:
                 continue
-            tok = sample(x, top_k=0, top_p=top_p, r=r)
+            tok = O.sample(x, 1.0, 0, top_p, 1.0, 0, [], r, aliased=False)
             assert tok == order[j], (top_p, r)
 
 
@@ -145,3 +150,73 @@ def test_full_distribution_draw_walks_index_order():
     x = np.log(np.array([0.1, 0.2, 0.3, 0.4], np.float32))   # 4 < 8: expf terms only
     for r, want in ((0.05, 0), (0.15, 1), (0.35, 2), (0.65, 3), (0.95, 3)):
         assert sample(x, top_k=0, top_p=1.0, r=r) == want
+
+
+def _nucleus_sorted(p):
+    """FindNucleus's selection sort (Sampler.cs:133-144) of the indices."""
+    idx = list(range(len(p)))
+    for i in range(len(p) - 1):
+        m = i
+        for j in range(i + 1, len(p)):
+            if p[idx[j]] > p[idx[m]]:
+                m = j
+        idx[i], idx[m] = idx[m], idx[i]
+    return idx
+
+
+def test_top_p_buffer_aliasing_constructed():
+    """The reference hands FindNucleus the buffer that holds the probabilities
+    as its output (Sampler.cs:30, 48-50).  Probabilities 0.1, 0.2, 0.4, 0.3 at
+    TopP 0.95: sorted ranks are ids 2, 3, 1, 0; writing rank 1 (0.3) into slot 1
+    overwrites id 1's 0.2, so rank 2 reads 0.3, the sum reaches 1.0 >= 0.95 and
+    the nucleus closes at 3 tokens with weights 0.4, 0.3, 0.3.  With a buffer of
+    its own the sum is 0.9 after 3, the nucleus is all 4 tokens, and the draw
+    walks the probabilities in token order."""
+    x = np.log(np.array([0.1, 0.2, 0.4, 0.3], np.float32))   # n < 8: exp terms only
+    assert _nucleus_sorted(_softmax_ref64(x)) == [2, 3, 1, 0]
+    # aliased: draw over (id 2: 0.4, id 3: 0.3, id 1: 0.3)
+    for r, want in ((0.05, 2), (0.39, 2), (0.45, 3), (0.69, 3), (0.75, 1), (0.99, 1)):
+        assert sample(x, top_p=0.95, r=r) == want, r
+    # own buffer: the full distribution in index order (0.1, 0.2, 0.4, 0.3)
+    for r, want in ((0.05, 0), (0.15, 1), (0.45, 2), (0.75, 3), (0.99, 3)):
+        assert O.sample(x, 1.0, 0, 0.95, 1.0, 0, [], r, aliased=False) == want, r
+    # the two differ at r = 0.05, 0.15, 0.45, 0.75
+    assert sum(sample(x, top_p=0.95, r=r) != O.sample(x, 1.0, 0, 0.95, 1.0, 0, [], r, aliased=False)
+               for r in (0.05, 0.15, 0.45, 0.75)) == 4
+
+
+def test_top_p_aliasing_fall_through_returns_a_rank():
+    """When the (rewritten) running sum reaches TopP only at the last rank, the
+    nucleus is all n tokens and the reference draws from `scaled` (Sampler.cs:61),
+    which now holds the sorted probabilities: the result is a rank, not a token
+    id.  Probabilities 0.1, 0.3, 0.6 at TopP 0.999: ranks are ids 2, 1, 0, no
+    slot is read after it is written except rank 2 (id 0) reading slot 0 (now
+    0.6), so the buffer becomes 0.6, 0.3, 0.6 (sum 1.5) and r = 0.5 returns 0
+    (rank 0, which is id 2)."""
+    x = np.log(np.array([0.1, 0.3, 0.6], np.float32))
+    assert _nucleus_sorted(_softmax_ref64(x)) == [2, 1, 0]
+    assert sample(x, top_p=0.999, r=0.5) == 0
+    assert sample(x, top_p=0.999, r=0.7) == 1
+    assert sample(x, top_p=0.999, r=1.0) == 2
+    # own buffer: r walks 0.1, 0.3, 0.6 in token order
+    assert O.sample(x, 1.0, 0, 0.999, 1.0, 0, [], 0.3, aliased=False) == 1
+    assert O.sample(x, 1.0, 0, 0.999, 1.0, 0, [], 0.5, aliased=False) == 2
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_top_p_aliasing_is_harmless_without_a_back_reference(seed):
+    """The two forms agree whenever no rank inside the nucleus has a token id
+    below its rank (indices[i] >= i for every i < nucleus size) and the nucleus
+    is proper: then every value is read before its slot is written.  Random
+    logits with the peak mass on high ids, checked over an r grid."""
+    rng = np.random.default_rng(seed)
+    n = 200
+    x = rng.normal(0, 1.0, n).astype(np.float32)
+    x[100:110] += 6.0     # the nucleus sits on ids 100..109
+    p = _softmax_ref64(x)
+    idx = _nucleus_sorted(p)
+    for top_p in (0.5, 0.8, 0.9):
+        m = int(np.searchsorted(np.cumsum(p[idx]), top_p)) + 1
+        assert m < n and all(idx[i] >= i for i in range(m))
+        for r in R_GRID:
+            assert sample(x, top_p=top_p, r=r) == O.sample(x, 1.0, 0, top_p, 1.0, 0, [], r, aliased=False)
