@@ -119,6 +119,8 @@ SIGNATURES = {
     "llmdot_hip_decode_step": [_P, _I32, _I32, _P, _PI32],
     "llmdot_hip_prefill": [_P, _PI32, _I32, _I32, _P, _PI32],
     "llmdot_hip_generate": [_P, _PI32, _I32, _I32, _I32, _PI32, _PI32, _P],
+    "llmdot_hip_generate_begin": [_P, _PI32, _I32, _I32, _I32, C.POINTER(Sampling), C.POINTER(C.c_float)],
+    "llmdot_hip_generate_next": [_P, _I32, _PI32, _PI32, _PI32, _P],
     "llmdot_hip_generate_sampled": [_P, _PI32, _I32, _I32, _I32, C.POINTER(Sampling), C.POINTER(C.c_float), _PI32,
                                     _PI32, _P],
     "llmdot_hip_kv_read": [_P, _I32, _I32, _P, _P],

@@ -558,6 +558,8 @@ extern "C" int32_t llmdot_hip_dequantize(llmdot_hip_ctx* ctx, const void* src, f
     uint8_t* ds;
     float* dy;
     if (int rc = stage_in(ctx, 0, reinterpret_cast<const uint8_t*>(src), nb, &ds)) return rc;
+    // zeros after the blocks: Q3_K's last q bytes lie 2 bytes past its block
+    HIPCHK(hipMemsetAsync(ds + nb, 0, WEIGHT_PAD, ctx->stream));
     if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)num_rows * row_elements, &dy)) return rc;
     HIPCHK(launch_dequant(ds, dy, type, num_rows, row_elements, ctx->stream));
     return copy_out(ctx, dst, dy, sizeof(float) * (size_t)num_rows * row_elements);
@@ -791,6 +793,13 @@ struct llmdot_hip_model {
     int32_t* s_hist = nullptr;
     float* s_draws = nullptr;
     float* s_work = nullptr;
+    // streaming Generate: tokens [0, yielded) returned, [yielded, computed)
+    // computed on the device and not yet returned
+    struct GenState {
+        bool active = false, sampled = false, done = false;
+        llmdot_hip_sampling opt{};
+        int hist_base = 0, produce = 0, max_tokens = 0, eos = -1, yielded = 0, computed = 0;
+    } gen;
 };
 
 namespace {
@@ -1274,6 +1283,7 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
 
 extern "C" int32_t llmdot_hip_model_reset(llmdot_hip_model* m) {
     if (!m) return fail(LLMDOT_E_INVALID, "null model");
+    m->gen.active = false;
     if (int rc = set_int(m, m_pos(m), 0)) return rc;
     if (int rc = set_int(m, m_step(m), 0)) return rc;
     HIPCHK(hipStreamSynchronize(m->ctx->stream));
@@ -1316,6 +1326,7 @@ int fetch_outputs(llmdot_hip_model* m, float* logits, int32_t* am) {
 
 extern "C" int32_t llmdot_hip_decode_step(llmdot_hip_model* m, int32_t token, int32_t position, float* logits, int32_t* am) {
     if (!m) return fail(LLMDOT_E_INVALID, "null model");
+    m->gen.active = false;   // the step changes the state a streaming Generate continues from
     if (int rc = check_token(m, token)) return rc;
     if (int rc = check_pos(m, position)) return rc;
     if (int rc = set_int(m, m_token(m), token)) return rc;
@@ -1327,6 +1338,7 @@ extern "C" int32_t llmdot_hip_decode_step(llmdot_hip_model* m, int32_t token, in
 extern "C" int32_t llmdot_hip_prefill(llmdot_hip_model* m, const int32_t* tokens, int32_t n, int32_t pos0, float* logits,
                                       int32_t* am) {
     if (!m || (!tokens && n > 0) || n < 0) return fail(LLMDOT_E_INVALID, "bad prefill arguments");
+    m->gen.active = false;
     if (n == 0) return 0;
     if (int rc = check_pos(m, pos0)) return rc;
     if (int rc = check_pos(m, pos0 + n - 1)) return rc;
@@ -1359,12 +1371,13 @@ int enqueue_sample(llmdot_hip_model* m, const llmdot_hip_sampling* opt, int hist
     return 0;
 }
 
-int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens, int32_t eos,
-                  const llmdot_hip_sampling* opt, const float* draws, int32_t* tokens_out, int32_t* n_out,
-                  float* logits_out) {
-    if (!m || (!prompt && n_prompt > 0) || n_prompt < 0 || max_tokens < 0 || (!tokens_out && max_tokens > 0) || !n_out)
+// Generate up to the first token (IE:79-101, then the first Sample): the cache
+// reset, the prompt, and token 0 left in the token log; the session is armed.
+int generate_begin(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens, int32_t eos,
+                   const llmdot_hip_sampling* opt, const float* draws) {
+    if (!m || (!prompt && n_prompt > 0) || n_prompt < 0 || max_tokens < 0)
         return fail(LLMDOT_E_INVALID, "bad Generate arguments");
-    *n_out = 0;
+    m->gen = {};
     const auto& d = m->d;
     const bool sampled = opt && opt->temperature > 0.f;   // Sampler.cs:26-27: greedy otherwise
     if (sampled && !draws && max_tokens > 0) return fail(LLMDOT_E_INVALID, "sampled Generate needs the uniform draws");
@@ -1376,11 +1389,14 @@ int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, 
     for (int t : pr)
         if (int rc = check_token(m, t)) return rc;
     if (np > d.context) return fail(LLMDOT_E_RANGE, "prompt longer than the KV cache");
-    if (max_tokens == 0) return 0;
+    auto& g = m->gen;
+    g.sampled = sampled; g.max_tokens = max_tokens; g.eos = eos; g.hist_base = n_prompt;
+    if (sampled) g.opt = *opt;
+    if (max_tokens == 0) { g.active = true; g.done = true; return 0; }
     // Token g (0-based) is sampled after position np-1+g; producing it needs
     // np + g steps, and positions stop at context - 1.
     const int fit = d.context - np + 1;
-    const int produce = max_tokens < fit ? max_tokens : fit;
+    g.produce = max_tokens < fit ? max_tokens : fit;
     hipStream_t s = m->ctx->stream;
     if (sampled) {
         // recentTokens starts as the prompt (IE:101); draws on the device
@@ -1393,7 +1409,7 @@ int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, 
         }
         if (n_prompt > 0)
             HIPCHK(hipMemcpyAsync(m->s_hist, prompt, sizeof(int32_t) * (size_t)n_prompt, hipMemcpyHostToDevice, s));
-        HIPCHK(hipMemcpyAsync(m->s_draws, draws, sizeof(float) * (size_t)produce, hipMemcpyHostToDevice, s));
+        HIPCHK(hipMemcpyAsync(m->s_draws, draws, sizeof(float) * (size_t)g.produce, hipMemcpyHostToDevice, s));
     }
     if (use_batched_prefill(m, np)) {
         if (int rc = prefill_batched(m, pr.data(), np, 0, true)) return rc;   // KvCache.Reset (IE:79) + prompt
@@ -1407,26 +1423,75 @@ int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, 
         }
     }
     if (sampled)
-        if (int rc = enqueue_sample(m, opt, n_prompt)) return rc;
-    if (logits_out) HIPCHK(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
-    for (int g = 1; g < produce; g++) {
-        if (int rc = run_step(m)) return rc;   // consumes the token the previous head wrote
-        if (sampled)
-            if (int rc = enqueue_sample(m, opt, n_prompt)) return rc;
-        if (logits_out)
-            HIPCHK(hipMemcpyAsync(logits_out + (size_t)g * d.vocab, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
-    }
-    HIPCHK(hipMemcpyAsync(tokens_out, m->token_log, sizeof(int32_t) * (size_t)produce, hipMemcpyDeviceToHost, s));
-    HIPCHK(hipStreamSynchronize(s));
-    if (int rc = check_device_flags(m)) return rc;
-    int n = produce;
-    if (eos >= 0)
-        for (int i = 0; i < produce; i++)
-            if (tokens_out[i] == eos) { n = i + 1; break; }   // IE:112-115
-    *n_out = n;
-    if (produce < max_tokens && n == produce)
-        return fail(LLMDOT_E_RANGE, "generation reached the end of the KV cache");
+        if (int rc = enqueue_sample(m, &g.opt, g.hist_base)) return rc;
+    g.computed = 1;
+    g.active = true;
     return 0;
+}
+
+// One more token on the device: the step that consumes the last computed
+// token (ProcessToken, IE:127), then its Sample.
+int generate_advance(llmdot_hip_model* m) {
+    if (int rc = run_step(m)) return rc;
+    if (m->gen.sampled)
+        if (int rc = enqueue_sample(m, &m->gen.opt, m->gen.hist_base)) return rc;
+    m->gen.computed++;
+    return 0;
+}
+
+// Returns up to max_k further tokens (and, when logits_out is given, the
+// logits each was taken from).  On entry token `yielded` is computed and its
+// logits are the model's current ones.  After the tokens are copied out, the
+// step for the next token is enqueued (not waited for), so the device works
+// while the caller handles these tokens.
+int generate_next(llmdot_hip_model* m, int32_t max_k, int32_t* tokens_out, int32_t* n_out, int32_t* done,
+                  float* logits_out) {
+    if (!m || !n_out || !done || max_k < 1 || !tokens_out) return fail(LLMDOT_E_INVALID, "bad Generate arguments");
+    *n_out = 0;
+    *done = 0;
+    auto& g = m->gen;
+    if (!g.active) return fail(LLMDOT_E_INVALID, "no Generate in progress on this model");
+    if (g.done) { *done = 1; return 0; }
+    const auto& d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int want = std::min(max_k, g.produce - g.yielded);
+    if (logits_out) HIPCHK(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * d.vocab, hipMemcpyDeviceToHost, s));
+    for (int i = 1; i < want; i++) {
+        if (g.computed < g.yielded + i + 1)
+            if (int rc = generate_advance(m)) return rc;
+        if (logits_out)
+            HIPCHK(hipMemcpyAsync(logits_out + (size_t)i * d.vocab, m->logits, sizeof(float) * d.vocab,
+                                  hipMemcpyDeviceToHost, s));
+    }
+    HIPCHK(hipMemcpyAsync(tokens_out, m->token_log + g.yielded, sizeof(int32_t) * (size_t)want, hipMemcpyDeviceToHost, s));
+    HIPCHK(hipStreamSynchronize(s));
+    if (int rc = check_device_flags(m)) { g.active = false; return rc; }
+    int n = want;
+    bool eos_hit = false;
+    if (g.eos >= 0)
+        for (int i = 0; i < want; i++)
+            if (tokens_out[i] == g.eos) { n = i + 1; eos_hit = true; break; }   // IE:112-115
+    *n_out = n;
+    g.yielded += n;
+    if (eos_hit || g.yielded == g.produce) {
+        g.done = true;
+        *done = 1;
+        if (!eos_hit && g.produce < g.max_tokens) return fail(LLMDOT_E_RANGE, "generation reached the end of the KV cache");
+        return 0;
+    }
+    return generate_advance(m);   // the next call's first token
+}
+
+int generate_impl(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens, int32_t eos,
+                  const llmdot_hip_sampling* opt, const float* draws, int32_t* tokens_out, int32_t* n_out,
+                  float* logits_out) {
+    if (!n_out || (!tokens_out && max_tokens > 0)) return fail(LLMDOT_E_INVALID, "bad Generate arguments");
+    *n_out = 0;
+    if (int rc = generate_begin(m, prompt, n_prompt, max_tokens, eos, opt, draws)) return rc;
+    int32_t done = 0;
+    int rc = max_tokens > 0 ? generate_next(m, max_tokens, tokens_out, n_out, &done, logits_out) : 0;
+    m->gen.active = false;
+    return rc;
 }
 
 }  // namespace
@@ -1442,6 +1507,17 @@ extern "C" int32_t llmdot_hip_generate_sampled(llmdot_hip_model* m, const int32_
                                                float* logits_out) {
     if (!opt) return fail(LLMDOT_E_INVALID, "null sampling options");
     return generate_impl(m, prompt, n_prompt, max_tokens, eos, opt, draws, tokens_out, n_out, logits_out);
+}
+
+extern "C" int32_t llmdot_hip_generate_begin(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt,
+                                             int32_t max_tokens, int32_t eos, const llmdot_hip_sampling* opt,
+                                             const float* draws) {
+    return generate_begin(m, prompt, n_prompt, max_tokens, eos, opt, draws);
+}
+
+extern "C" int32_t llmdot_hip_generate_next(llmdot_hip_model* m, int32_t max_k, int32_t* tokens_out, int32_t* n_out,
+                                            int32_t* done, float* logits_out) {
+    return generate_next(m, max_k, tokens_out, n_out, done, logits_out);
 }
 
 extern "C" int32_t llmdot_hip_kv_read(llmdot_hip_model* m, int32_t layer, int32_t position, float* k, float* v) {
@@ -1491,6 +1567,7 @@ extern "C" int32_t llmdot_hip_model_step_bytes(llmdot_hip_model* m, int32_t posi
 
 extern "C" int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* m, int32_t n, uint64_t seed) {
     if (!m) return fail(LLMDOT_E_INVALID, "null model");
+    m->gen.active = false;
     if (n < 0 || n > m->d.context) return fail(LLMDOT_E_RANGE, "fill length outside the KV cache");
     const auto& d = m->d;
     HIPCHK(launch_kv_fill(m->kcache, 0, d.layers, d.kv_heads, d.context, d.head_dim, n, seed, d.kv_fp16, m->ctx->stream));
@@ -1502,6 +1579,7 @@ extern "C" int32_t llmdot_hip_model_kv_fill_random(llmdot_hip_model* m, int32_t 
 extern "C" int32_t llmdot_hip_model_time_prefill(llmdot_hip_model* m, const int32_t* tokens, int32_t n, int32_t pos0,
                                                  float* ms) {
     if (!m || !tokens || n <= 0 || !ms) return fail(LLMDOT_E_INVALID, "bad prefill timing arguments");
+    m->gen.active = false;
     if (!m->pf_eligible) return fail(LLMDOT_E_UNSUPPORTED, "the model's weight types have no batched prefill kernel");
     if (int rc = check_pos(m, pos0)) return rc;
     if (int rc = check_pos(m, pos0 + n - 1)) return rc;
@@ -1528,6 +1606,7 @@ extern "C" int32_t llmdot_hip_model_time_prefill(llmdot_hip_model* m, const int3
 extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t first_token, int32_t position, int32_t steps,
                                                 int32_t per_kernel, llmdot_hip_step_timing* out) {
     if (!m || !out || steps <= 0) return fail(LLMDOT_E_INVALID, "bad timing arguments");
+    m->gen.active = false;
     if (int rc = check_token(m, first_token)) return rc;
     if (int rc = check_pos(m, position)) return rc;
     if (position + steps > m->d.context) return fail(LLMDOT_E_RANGE, "timed steps run past the KV cache");

@@ -25,12 +25,13 @@ constexpr size_t WEIGHT_PAD = 256;
 __host__ __device__ inline constexpr int block_elems(uint32_t t) {
     return t == GGML_F32 || t == GGML_F16 || t == GGML_BF16 ? 1
          : t == GGML_Q4_0 || t == GGML_Q4_1 || t == GGML_Q5_0 || t == GGML_Q5_1 || t == GGML_Q8_0 ? 32
-         : t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K ? 256 : 0;
+         : t == GGML_Q2_K || t == GGML_Q3_K || t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K ? 256 : 0;
 }
 __host__ __device__ inline constexpr int block_bytes(uint32_t t) {
     return t == GGML_F32 ? 4 : t == GGML_F16 || t == GGML_BF16 ? 2
          : t == GGML_Q4_0 ? 18 : t == GGML_Q4_1 ? 20 : t == GGML_Q5_0 ? 22 : t == GGML_Q5_1 ? 24
-         : t == GGML_Q8_0 ? 34 : t == GGML_Q4_K ? 144 : t == GGML_Q5_K ? 176 : t == GGML_Q6_K ? 210 : 0;
+         : t == GGML_Q8_0 ? 34 : t == GGML_Q2_K ? 84 : t == GGML_Q3_K ? 110
+         : t == GGML_Q4_K ? 144 : t == GGML_Q5_K ? 176 : t == GGML_Q6_K ? 210 : 0;
 }
 // TensorSize.ByteCount (TensorSize.cs:7-24); -1 when unsupported.
 inline int64_t byte_count(uint32_t t, int64_t n) {

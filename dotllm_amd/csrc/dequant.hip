@@ -38,6 +38,27 @@ __device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
         const uint8_t* b = row + (i >> 5) * 34;
         return ((float)(int8_t)b[2 + (i & 31)] * h2f_at(b));
     }
+    case GGML_Q2_K: {  // DK:8-41 (the reference's layout: scale/min byte pairs from byte 4, 2-bit q from byte 20)
+        const uint8_t* b = row + (i >> 8) * 84;
+        int j = i & 255, g = j >> 6, sub = (j & 63) >> 4, scIdx = g * 4 + sub;
+        float d = h2f_at(b), dmin = h2f_at(b + 2);
+        int sc = b[4 + scIdx * 2] & 0x0F, mi = b[4 + scIdx * 2 + 1] & 0x0F;
+        int q = (b[20 + (j >> 2)] >> ((j & 3) * 2)) & 0x3;
+        return (((d * (float)sc) * ((float)q - 0.5f)) - (dmin * (float)mi));
+    }
+    case GGML_Q3_K: {  // DK:43-74: 6-bit group scales from byte 4, high-bit mask from 16, 2-bit q from 48
+        // (the q field runs to byte 111 of a 110-byte block: the last 8 elements
+        // read the next block's first two bytes, as the reference does; past the
+        // tensor's end the device buffer's zero padding)
+        const uint8_t* b = row + (i >> 8) * 110;
+        int j = i & 255, g = j >> 4;
+        float d = h2f_at(b);
+        int sc = extract6(b + 4, g * 6);
+        int q = (b[48 + (j >> 2)] >> ((j & 3) * 2)) & 0x3;
+        int m = (b[16 + (j >> 3)] >> (j & 7)) & 0x1;
+        int value = q - (m << 2);
+        return ((d * (float)sc) * (float)value);
+    }
     case GGML_Q4_K: {  // DK:76-106
         const uint8_t* b = row + (i >> 8) * 144;
         int j = i & 255, g = j >> 5;

@@ -282,6 +282,81 @@ struct TQ6K {
     }
 };
 
+// Reference Q2_K, 84 B / 256 (DequantizeK.cs:8-41): unit = 32 elements, two
+// sub-blocks of 16 with a (scale, min) byte pair each (low nibbles, bytes 4 +
+// 4 (u & 7) ..), 2-bit q at byte 20 + 8 (u & 7) + e / 4, shift 2 (e % 4).
+// value = d sc (q - 1/2) - dmin mi.  Blocks and rows are 4-byte aligned.
+struct TQ2K {
+    static constexpr int RB = 8, NS = 2, RUN = 32, PRE = 2, DEPTH = 2;
+    struct Raw { uint32_t h, s, q0, q1; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const uint8_t* blk = row + (u >> 3) * 84;
+        const int g = u & 7;
+        r.h = ld4_a4(blk);
+        r.s = ld4_a4(blk + 4 + 4 * g);
+        r.q0 = ld4_a4(blk + 20 + 8 * g);
+        r.q1 = ld4_a4(blk + 24 + 8 * g);
+    }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
+        const uint32_t Q[2] = {r.q0, r.q1};
+        float s[2] = {0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t qt = (Q[h] >> (2 * t)) & 0x03030303u;   // byte k: element 16 h + 4 k + t
+#pragma unroll
+                for (int k = 0; k < 4; k++) s[h] += x.v[16 * h + 4 * k + t] * ub(qt, k);
+            }
+        const float d = h16(r.h & 0xFFFFu), dm = h16(r.h >> 16);
+        const float sc0 = (float)(r.s & 15u), mi0 = (float)((r.s >> 8) & 15u);
+        const float sc1 = (float)((r.s >> 16) & 15u), mi1 = (float)((r.s >> 24) & 15u);
+        return ((d * sc0) * (s[0] - 0.5f * x.s[0]) - (dm * mi0) * x.s[0]) +
+               ((d * sc1) * (s[1] - 0.5f * x.s[1]) - (dm * mi1) * x.s[1]);
+    }
+};
+
+// Reference Q3_K, 110 B / 256 (DequantizeK.cs:43-74, TensorOps.cs:331-362):
+// unit = 32 elements, two groups of 16 whose 6-bit scales sit at bits 12 (u & 7)
+// and 12 (u & 7) + 6 of the stream from byte 4; the high-bit mask at byte 16 +
+// 4 (u & 7) (bit e), 2-bit q at byte 48 + 8 (u & 7) + e / 4.  value = q - 4 m,
+// scaled by d sc.  The q field of unit 7 ends 2 bytes past the block, in the
+// next block (as the reference reads it) or, for the tensor's last block, in
+// the device buffer's zero padding.  Blocks are 2-byte aligned.
+struct TQ3K {
+    static constexpr int RB = 4, NS = 2, RUN = 32, PRE = 2, DEPTH = 2;
+    struct Raw { RawW<4> H; RawW<1> M; RawW<2> Q; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const uint8_t* blk = row + (u >> 3) * 110;
+        const int g = u & 7;
+        r.H.load(blk);
+        r.M.load(blk + 16 + 4 * g);
+        r.Q.load(blk + 48 + 8 * g);
+    }
+    __device__ static float dot(const Raw& r, int u, const XF<NS>& x) {
+        float sc0, sc1;
+        kscale(r.H[1], r.H[2], r.H[3], u & 7, sc0, sc1);
+        const float d = h16(r.H[0] & 0xFFFFu);
+        const uint32_t M = r.M[0];
+        const uint32_t Q[2] = {r.Q[0], r.Q[1]};
+        float s[2] = {0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int e = 16 * h + 4 * k + t;
+                    const int q = (int)((Q[h] >> (8 * k + 2 * t)) & 3u);
+                    const int m = (int)((M >> e) & 1u);
+                    s[h] += x.v[e] * (float)(q - (m << 2));
+                }
+        return d * (sc0 * s[0] + sc1 * s[1]);
+    }
+};
+
 struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block
     static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
     struct Raw { RawW<8> Q; uint32_t d; };
@@ -375,6 +450,8 @@ struct TF16 {
 };
 
 template <uint32_t T> struct TypeOf;
+template <> struct TypeOf<GGML_Q2_K> { using type = TQ2K; };
+template <> struct TypeOf<GGML_Q3_K> { using type = TQ3K; };
 template <> struct TypeOf<GGML_Q4_K> { using type = TQ4K; };
 template <> struct TypeOf<GGML_Q5_K> { using type = TQ5K; };
 template <> struct TypeOf<GGML_Q6_K> { using type = TQ6K; };
@@ -690,6 +767,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* w, uin
 int type_rb(uint32_t t) {
     switch (t) {
     case GGML_Q6_K: return TQ6K::RB;
+    case GGML_Q3_K: return TQ3K::RB;
     case GGML_Q8_0: return TQ8_0::RB;
     case GGML_Q4_K: return TQ4K::RB;
     case GGML_F32: return TF32::RB;
@@ -741,7 +819,7 @@ bool generic_shape(uint32_t type, int cols) { return (type == GGML_F32 || type =
 
 bool gemv_supported(uint32_t type) {
     return type == GGML_Q4_K || type == GGML_Q5_K || type == GGML_Q6_K || type == GGML_Q8_0 ||
-           type == GGML_Q4_0 || type == GGML_F32 || type == GGML_F16;
+           type == GGML_Q4_0 || type == GGML_Q2_K || type == GGML_Q3_K || type == GGML_F32 || type == GGML_F16;
 }
 
 bool gemv_width_ok(uint32_t type, int cols) {
@@ -875,6 +953,8 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     case GGML_Q6_K: e = launch_t<GGML_Q6_K>(epi, a, nb, grid, threads, s); break;
     case GGML_Q8_0: e = launch_t<GGML_Q8_0>(epi, a, nb, grid, threads, s); break;
     case GGML_Q4_0: e = launch_t<GGML_Q4_0>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q2_K: e = launch_t<GGML_Q2_K>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q3_K: e = launch_t<GGML_Q3_K>(epi, a, nb, grid, threads, s); break;
     case GGML_F32: e = launch_t<GGML_F32>(epi, a, nb, grid, threads, s); break;
     case GGML_F16: e = launch_t<GGML_F16>(epi, a, nb, grid, threads, s); break;
     default: return hipErrorInvalidValue;

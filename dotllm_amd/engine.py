@@ -100,6 +100,10 @@ class InferenceEngine:
             raise NotImplementedError("only separate Q/K/V and SwiGLU FFN tensors are supported")
         if cfg.sliding_window:
             raise NotImplementedError("sliding-window attention is not supported")
+        if cfg.qk_norm:
+            raise NotImplementedError("Q/K norms are not supported")
+        if any(h != cfg.head_count_kv for h in cfg.kv_heads_per_layer):
+            raise NotImplementedError("per-layer KV head counts are not supported")
         self.model = model
         self.backend = backend or HipBackend()
         self._own_backend = backend is None
@@ -162,10 +166,42 @@ class InferenceEngine:
         return self._m
 
     # -- Generate ------------------------------------------------------------
-    def generate(self, prompt_tokens, options: GenerationOptions | None = None):
-        """InferenceEngine.Generate (IE:74-132): yields the token ids."""
-        tokens, _ = self.generate_all(prompt_tokens, options or GenerationOptions())
-        yield from tokens
+    def generate(self, prompt_tokens, options: GenerationOptions | None = None, chunk: int = 1, draws=None):
+        """InferenceEngine.Generate (IE:74-132) as a stream: yields each token id
+        as soon as the device has it (llmdot_hip_generate_begin / _next, `chunk`
+        tokens per device round trip; the step for the next token is already
+        running while the caller handles this one).  Stopping the iteration is
+        the cancellation: nothing further is computed."""
+        options = options or GenerationOptions()
+        if options.stop_sequences:
+            raise NotImplementedError("stop sequences need the tokenizer")
+        if chunk < 1:
+            raise ValueError("chunk must be at least 1")
+        prompt = np.ascontiguousarray(np.asarray(prompt_tokens, dtype=np.int32))
+        n = int(options.max_tokens)
+        pp = prompt.ctypes.data_as(C.POINTER(C.c_int32))
+        eos = int(self.model.config.eos_token_id)
+        if options.sampling.temperature > 0:
+            from .backend import sampling_struct
+            d = np.ascontiguousarray(draws if draws is not None else self.draws_for(options.sampling, n),
+                                     dtype=np.float32)
+            if d.size < n:
+                raise ValueError("one uniform draw per generated token is needed")
+            opt = sampling_struct(options.sampling)
+            _call(lib().llmdot_hip_generate_begin(self._m, pp, prompt.size, n, eos, C.byref(opt),
+                                                  d.ctypes.data_as(C.POINTER(C.c_float))))
+        else:
+            _call(lib().llmdot_hip_generate_begin(self._m, pp, prompt.size, n, eos, None, None))
+        out = np.zeros(chunk, dtype=np.int32)
+        n_out, done = C.c_int32(0), C.c_int32(0)
+        while not done.value:
+            rc = lib().llmdot_hip_generate_next(self._m, chunk, out.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                C.byref(n_out), C.byref(done), None)
+            if rc == _lib.E_RANGE:   # the KV cache ended: these tokens, then stop
+                yield from out[:n_out.value].tolist()
+                return
+            _call(rc)
+            yield from out[:n_out.value].tolist()
 
     @staticmethod
     def draws_for(sampling: SamplingOptions, n: int) -> np.ndarray:

@@ -177,6 +177,8 @@ class TransformerConfig:
     eos_token_id: int = 2
     qkv_fused: bool = False
     ffn_type: str = "swiglu"
+    qk_norm: bool = False            # attn_q_norm / attn_k_norm tensors (IE:354-365)
+    kv_heads_per_layer: tuple = ()   # HeadCountKvPerLayer when the metadata gives a list
     extra: dict = field(default_factory=dict)
 
     @property
@@ -238,6 +240,8 @@ def resolve(model: GgufModel) -> TransformerConfig:
         eos_token_id=int(meta.get("tokenizer.ggml.eos_token_id", 2)),
         qkv_fused=any("attn_qkv" in n for n in names),
         ffn_type="swiglu" if any("ffn_gate" in n for n in names) else "standard",
+        qk_norm=any("attn_q_norm" in n or "attn_k_norm" in n for n in names),
+        kv_heads_per_layer=tuple(int(v) for v in hkv_raw) if isinstance(hkv_raw, list) else (),
     )
 
 

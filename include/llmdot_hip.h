@@ -232,6 +232,24 @@ int32_t llmdot_hip_generate(llmdot_hip_model* model, const int32_t* prompt, int3
 int32_t llmdot_hip_generate_sampled(llmdot_hip_model* model, const int32_t* prompt, int32_t n_prompt,
                                     int32_t max_tokens, int32_t eos, const llmdot_hip_sampling* opt,
                                     const float* draws, int32_t* tokens_out, int32_t* n_out, float* logits_out);
+/* Streaming Generate: the IAsyncEnumerable of IE:74-132, a batch of tokens per
+ * call.  begin resets the cache, processes the prompt and computes token 0
+ * (greedy when opt_or_null is NULL or Temperature <= 0, else sampled with
+ * draws[i] for token i, as llmdot_hip_generate_sampled).  Each next call
+ * returns up to max_k (>= 1) further tokens in tokens_out (and, when
+ * logits_out_or_null is given, [n][vocab] logits they were taken from), sets
+ * *done once max_tokens tokens or eos (included, IE:112-115) have been
+ * returned, and enqueues the step for the following token before it returns,
+ * so the device computes while the caller consumes.  A caller that stops early
+ * (cancellation, stop sequences) simply stops calling.  The last batch before
+ * the end of the KV cache returns its tokens with LLMDOT_E_RANGE.  Any other
+ * call that changes the model's state (decode_step, prefill, reset, a new
+ * begin) ends the session; next then fails with LLMDOT_E_INVALID. */
+int32_t llmdot_hip_generate_begin(llmdot_hip_model* model, const int32_t* prompt, int32_t n_prompt,
+                                  int32_t max_tokens, int32_t eos, const llmdot_hip_sampling* opt_or_null,
+                                  const float* draws_or_null);
+int32_t llmdot_hip_generate_next(llmdot_hip_model* model, int32_t max_k, int32_t* tokens_out, int32_t* n_out,
+                                 int32_t* done, float* logits_out_or_null);
 /* Reads KV slot (layer, position) as fp32, kv_heads*head_dim floats each. */
 int32_t llmdot_hip_kv_read(llmdot_hip_model* model, int32_t layer, int32_t position, float* k,
                            float* v);

@@ -112,8 +112,23 @@ def byte_count(t: int, n: int) -> int:
     return lib().orc_byte_count(t, n)
 
 
+Q3_K = 11
+
+
+def _blocks(b: np.ndarray, ggml_type: int) -> np.ndarray:
+    """The block bytes as one uint8 vector; for Q3_K with two zero bytes after
+    them.  The reference's Q3_K reads its 2-bit values up to byte 111 of a
+    110-byte block (DequantizeK.cs:64, TensorOps.cs:353): inside a tensor that
+    is the next block's first two bytes, after the last block the reference's
+    span check throws; here, as on the device, those two bytes read zero."""
+    b = np.ascontiguousarray(b).reshape(-1).view(np.uint8)
+    if ggml_type == Q3_K:
+        b = np.concatenate([b, np.zeros(2, np.uint8)])
+    return b
+
+
 def dequantize(src: np.ndarray, ggml_type: int, num_rows: int, row_elements: int) -> np.ndarray:
-    src = np.ascontiguousarray(src).reshape(-1).view(np.uint8)
+    src = _blocks(src, ggml_type)
     dst = np.zeros(num_rows * row_elements, dtype=np.float32)
     if lib().orc_dequantize(_p(src), _p(dst), ggml_type, num_rows, row_elements) != 0:
         raise NotImplementedError(f"Dequantization for type {ggml_type} not yet implemented.")
@@ -122,7 +137,7 @@ def dequantize(src: np.ndarray, ggml_type: int, num_rows: int, row_elements: int
 
 def matmul(a: np.ndarray, b: np.ndarray, ggml_type: int, a_cols: int, b_cols: int, result_len: int | None = None):
     a = np.ascontiguousarray(a, dtype=np.float32)
-    b = np.ascontiguousarray(b).reshape(-1).view(np.uint8)
+    b = _blocks(b, ggml_type)
     n = result_len or b_cols
     out = np.zeros(n, dtype=np.float32)
     if lib().orc_matmul(_p(a), _p(b), _p(out), n, ggml_type, a_cols, b_cols) != 0:
@@ -134,7 +149,7 @@ def matmul_rows(a: np.ndarray, b: np.ndarray, ggml_type: int, a_cols: int, b_col
     """[rows][b_cols]: each activation row as its own single-row MatMul, through
     the batched path of the prompt processing (bitwise the same)."""
     a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1, a_cols)
-    b = np.ascontiguousarray(b).reshape(-1).view(np.uint8)
+    b = _blocks(b, ggml_type)
     out = np.zeros((a.shape[0], b_cols), dtype=np.float32)
     if lib().orc_matmul_rows(_p(a), a.shape[0], _p(b), ggml_type, a_cols, b_cols, _p(out)) != 0:
         raise NotImplementedError(f"MatMul for type {ggml_type}")

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from dotllm_amd import F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, BF16, byte_count, synth
+from dotllm_amd._lib import Q2_K, Q3_K
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -30,10 +31,11 @@ def random_blocks(t, rows, cols, seed):
     """Random block bytes with finite fp16 scale fields (exercises every bit pattern of q/scales)."""
     rng = np.random.default_rng(seed)
     b = rng.integers(0, 256, size=rows * byte_count(t, cols), dtype=np.uint8)
-    be, bb = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18)}[t]
+    be, bb = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18),
+              Q2_K: (256, 84), Q3_K: (256, 110)}[t]
     blocks = b.reshape(-1, bb)
     halves = rng.uniform(-2, 2, size=(blocks.shape[0], 2)).astype(np.float16).view(np.uint8)
-    if t in (Q4_K, Q5_K):
+    if t in (Q4_K, Q5_K, Q2_K, Q3_K):
         blocks[:, 0:4] = halves.reshape(-1, 4)
     elif t == Q6_K:
         blocks[:, 208:210] = halves[:, :2]
@@ -47,6 +49,20 @@ def random_blocks(t, rows, cols, seed):
 def test_dequantize_bit_exact(hip, t, kind):
     rows, cols = 7, 1024
     src = weights(t, rows, cols, 11) if kind == "quantized" else random_blocks(t, rows, cols, 12)
+    ref = O.dequantize(src, t, rows, cols)
+    out = np.zeros(rows * cols, dtype=np.float32)
+    hip.dequantize_to_float(src, out, t, rows, cols)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q2_K, Q3_K])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (7, 1024), (33, 4096)])
+def test_dequantize_lowbit_kquants_bit_exact(hip, t, rows, cols):
+    """Reference-layout Q2_K / Q3_K (DequantizeK.cs:8-74) over random blocks:
+    every element bit for bit, including Q3_K's last 8 values of each block,
+    which the reference reads from the next block's first two bytes (zeros
+    after the tensor's last block)."""
+    src = random_blocks(t, rows, cols, 40 + rows)
     ref = O.dequantize(src, t, rows, cols)
     out = np.zeros(rows * cols, dtype=np.float32)
     hip.dequantize_to_float(src, out, t, rows, cols)
@@ -91,6 +107,30 @@ def test_gemv_matches_reference(hip, t, rows, cols):
     y = np.zeros(rows, dtype=np.float32)
     hip.mat_mul(x, w, y, t, cols, rows)
     assert rel_err(y, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("t,rows,cols", [(Q2_K, 300, 2048), (Q2_K, 4096, 4096), (Q3_K, 257, 4096),
+                                         (Q3_K, 1024, 14336), (Q3_K, 3, 256)])
+def test_lowbit_kquant_gemv(hip, t, rows, cols):
+    """Q2_K / Q3_K GEMV (TensorOps.cs:293-362) on random blocks within 1e-3 of
+    the oracle's MatMul, and of the fp64 product of the oracle's dequantised
+    rows; with a resident weight key as well as host bytes."""
+    w = random_blocks(t, rows, cols, rows + 7)
+    blocks = w.reshape(-1, 84 if t == Q2_K else 110)
+    blocks[:, 0:4] = np.random.default_rng(rows).uniform(-0.05, 0.05, size=(blocks.shape[0], 2)).astype(
+        np.float16).view(np.uint8)
+    x = np.random.default_rng(cols).normal(0, 1, size=cols).astype(np.float32)
+    ref = O.matmul(x, w, t, cols, rows)
+    wd = O.dequantize(w, t, rows, cols).reshape(rows, cols).astype(np.float64)
+    exact = wd @ x.astype(np.float64)
+    y = np.zeros(rows, dtype=np.float32)
+    hip.mat_mul(x, w, y, t, cols, rows)
+    assert rel_err(y, ref) <= GEMV_TOL and rel_err(y, exact) <= GEMV_TOL
+    key = f"lowbit.{t}.{rows}.{cols}"
+    y2 = np.zeros(rows, dtype=np.float32)
+    hip.mat_mul(x, w, y2, t, cols, rows, weight_key=key)
+    hip.release_weight(key)
+    assert np.array_equal(y, y2)
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (14336, 4096), (4096, 14336)])
@@ -257,4 +297,4 @@ def test_argmax_ties_first_index(hip):
 
 def test_unsupported_type_raises(hip):
     with pytest.raises(NotImplementedError):
-        hip.mat_mul(np.zeros(256, np.float32), np.zeros(84, np.uint8), np.zeros(1, np.float32), 10, 256, 1)
+        hip.mat_mul(np.zeros(256, np.float32), np.zeros(176, np.uint8), np.zeros(1, np.float32), 6, 256, 1)   # Q5_0

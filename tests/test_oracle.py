@@ -209,7 +209,131 @@ def test_q6k_layout_and_scales():
         assert np.array_equal(x, want.astype(np.float32)), trial
 
 
+# ------------------------------------------------- reference-layout Q2_K / Q3_K --
+# No reference test covers these formats; the blocks below are written field by
+# field from DequantizeK.cs:8-74 and the expected values are closed forms.
+
+Q2_K, Q3_K = 10, 11
+
+
+def _q2block(d, dmin, sc, mi, q):
+    """Reference Q2_K (84 B): d, dmin; scale/min of sub-block s (16 elements,
+    s = 4 (i / 64) + (i % 64) / 16) in the low nibbles of bytes 4 + 2s and
+    5 + 2s; 2-bit q of element i at bits 2 (i % 4) of byte 20 + i / 4.  The two
+    fields overlap in bytes 20..35: q is written last, so the scale/min nibbles
+    of sub-blocks 8..15 are whatever q leaves there (sc/mi for s >= 8 are
+    ignored)."""
+    b = np.zeros(84, dtype=np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    for s in range(8):
+        b[4 + 2 * s] = sc[s] & 0xF
+        b[5 + 2 * s] = mi[s] & 0xF
+    for i in range(256):
+        b[20 + i // 4] &= ~(3 << (2 * (i % 4))) & 0xFF
+        b[20 + i // 4] |= (q[i] & 3) << (2 * (i % 4))
+    return b
+
+
+def test_q2k_scales_and_values():
+    """q = 0 everywhere: sub-blocks 0..7 give -sc/2 - (dmin/4) mi (d = 1,
+    dmin = 0.25); sub-blocks 8..15 read their scale/min nibbles from the zero q
+    bytes, so they give d*0*(0 - 1/2) - dmin*0 = -0.0."""
+    sc, mi = [1, 2, 3, 5, 7, 11, 13, 15], [0, 1, 2, 3, 4, 8, 12, 15]
+    x = O.dequantize(_q2block(1.0, 0.25, sc, mi, [0] * 256), Q2_K, 1, 256)
+    for s in range(8):
+        assert np.array_equal(x[16 * s:16 * s + 16], np.full(16, -sc[s] / 2 - 0.25 * mi[s], np.float32)), s
+    assert np.array_equal(x[128:].view(np.uint32), np.full(128, 0x80000000, np.uint32))
+
+
+def test_q2k_every_q_value_and_the_overlap():
+    """Elements 64..127 (q bytes 36..51, clear of the scale bytes) walk every q
+    value; elements 0..15 set bytes 20..23, whose low nibbles are the scale and
+    min of sub-blocks 8 and 9 (elements 128..159): q0 | q1 << 2."""
+    q = [0] * 256
+    for i in range(64, 128):
+        q[i] = (i * 3) % 4
+    q[0], q[1] = 3, 2      # byte 20 low nibble = 3 | 2 << 2 = 11: sub-block 8's scale
+    q[4], q[5] = 1, 1      # byte 21: 1 | 1 << 2 = 5: sub-block 8's min
+    q[8], q[9] = 2, 0      # byte 22: 2: sub-block 9's scale
+    q[12], q[13] = 0, 3    # byte 23: 12: sub-block 9's min
+    sc = [0, 0, 0, 0, 4, 6, 9, 15]
+    mi = [0, 0, 0, 0, 1, 0, 3, 2]
+    x = O.dequantize(_q2block(0.5, 0.125, sc, mi, q), Q2_K, 1, 256).astype(np.float64)
+    for i in range(64, 128):
+        s = i // 16
+        assert x[i] == np.float32(0.5 * sc[s] * (q[i] - 0.5) - 0.125 * mi[s]), i
+    assert np.all(x[128:144] == np.float32(0.5 * 11 * (0 - 0.5) - 0.125 * 5))
+    assert np.all(x[144:160] == np.float32(0.5 * 2 * (0 - 0.5) - 0.125 * 12))
+
+
+def _q3block(d, sc, m, q, size=110):
+    """Reference Q3_K (110 B): d; 6-bit scale of group g (16 elements) at bits 6g
+    of the stream at byte 4; high-bit mask of element i at bit i % 8 of byte
+    16 + i / 8; 2-bit q at bits 2 (i % 4) of byte 48 + i / 4.  The q field needs
+    112 bytes: elements 248..255 live in bytes 110 and 111, which belong to the
+    next block, so the buffer returned is 112 bytes (the caller overlaps it)."""
+    b = np.zeros(112, dtype=np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    for g in range(16):
+        _put_bits(b, 4, 6 * g, sc[g], 6)
+    for i in range(256):
+        b[16 + i // 8] |= (m[i] & 1) << (i % 8)
+        b[48 + i // 4] |= (q[i] & 3) << (2 * (i % 4))
+    return b
+
+
+def test_q3k_values_scales_and_mask():
+    """value = d * sc[g] * (q - 4 m) for every q and mask bit; the scale field of
+    each group at every bit position of its 6."""
+    rng = np.random.default_rng(8)
+    for trial in range(6):
+        q = rng.integers(0, 4, 256)
+        m = rng.integers(0, 2, 256)
+        sc = [1 << (trial % 6)] * 16 if trial < 6 else rng.integers(0, 64, 16)
+        sc = list(sc)
+        sc[trial] = 63
+        b = _q3block(0.25, sc, m, q)
+        q[248:] = 0  # bytes 110..111 are not part of the block: zero after the tensor
+        x = O.dequantize(b[:110], Q3_K, 1, 256).astype(np.float64)
+        want = np.array([0.25 * sc[i // 16] * (q[i] - 4 * m[i]) for i in range(256)])
+        assert np.array_equal(x, want.astype(np.float32)), trial
+
+
+def test_q3k_reads_two_bytes_of_the_next_block():
+    """Two blocks: the first's last 8 values take their q bits from the second
+    block's d bytes (DK:64 reads byte 48 + 63 = 111 of a 110-byte block)."""
+    q = np.zeros(256, np.int64)
+    q[248:] = [1, 2, 3, 0, 3, 3, 1, 0]
+    b0 = _q3block(1.0, [2] * 16, [0] * 256, q)
+    tail = b0[110:112].copy()
+    b1 = _q3block(0.0, [0] * 16, [0] * 256, np.zeros(256, np.int64))
+    b1[0:2] = tail   # the second block's d: its bytes are the first block's q tail
+    src = np.concatenate([b0[:110], b1[:110]])
+    x = O.dequantize(src, Q3_K, 2, 256)
+    assert np.array_equal(x[248:256], (2.0 * q[248:]).astype(np.float32))
+    d1 = float(np.frombuffer(tail.tobytes(), np.float16)[0])
+    assert np.array_equal(x[256:], np.zeros(256, np.float32) * d1)   # scales 0: zeros of the block's sign
+
+
 # ------------------------------------------------------------------------ GEMV --
+
+@pytest.mark.parametrize("t", [Q2_K, Q3_K])
+def test_kquant_lowbit_gemv_equals_fp64_brute_force(t):
+    """Q2_K / Q3_K MatMul (TO:293-362) over random blocks (finite d) against the
+    fp64 dot product of the oracle's dequantised rows."""
+    rng = np.random.default_rng(t)
+    rows, cols = 40, 1024
+    bb = 84 if t == Q2_K else 110
+    w = rng.integers(0, 256, size=rows * cols // 256 * bb, dtype=np.uint8)
+    blocks = w.reshape(-1, bb)
+    blocks[:, 0:4] = rng.uniform(-0.05, 0.05, size=(blocks.shape[0], 2)).astype(np.float16).view(np.uint8)
+    x = rng.normal(0, 1, size=cols).astype(np.float32)
+    wd = O.dequantize(w, t, rows, cols).reshape(rows, cols).astype(np.float64)
+    ref = wd @ x.astype(np.float64)
+    y = O.matmul(x, w, t, cols, rows)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 2e-6
+
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, F16])
 def test_gemv_equals_fp64_brute_force(t):
