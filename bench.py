@@ -22,17 +22,33 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_q4k_mistral7b_traffic.md")
+GEMV_SOURCE = os.path.join(ROOT, "dotllm_amd", "csrc", "gemv.hip")
+
+
+def gemv_source_hash() -> str:
+    import hashlib
+    with open(GEMV_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
 
 
 def measured_traffic(config: str):
     """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (counters cannot be read inside a normal run)."""
+    WRITE_SIZE summary (counters cannot be read inside a normal run), with the
+    reason when there is none.  The summary names the gemv.hip it measured
+    (`gemv_source_sha256:`); a figure from another build of the kernel is
+    refused rather than reported."""
     if config != "mistral7b" or not os.path.exists(TRAFFIC_PROFILE):
-        return None
+        return None, "no counter profile for this workload"
+    fields = {}
     for line in open(TRAFFIC_PROFILE):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        if ":" in line and not line.startswith((" ", "|", "#", "`")):
+            k, v = line.split(":", 1)
+            fields[k.strip()] = v.strip()
+    cur = gemv_source_hash()
+    if fields.get("gemv_source_sha256") != cur:
+        return None, (f"stale: the profile measured gemv.hip {fields.get('gemv_source_sha256', '?')}, "
+                      f"this build is {cur}")
+    return float(fields["traffic_bytes_per_launch"]), f"rocprofv3 FETCH_SIZE + WRITE_SIZE of gemv.hip {cur}"
 
 
 def log(msg: str) -> None:
@@ -40,7 +56,9 @@ def log(msg: str) -> None:
 
 
 def cpu_baseline(img, ctx: int, steps: int, threads: int) -> dict:
-    """The reference CPU path (oracle restatement) on the same weights."""
+    """The reference CPU path (oracle restatement) on the same weights; with
+    threads = 1 the reference's own execution model (no Parallel, Thread or
+    Task in its src/)."""
     from oracle import oracle as O
     O.set_threads(threads)
     m = O.Model(img, kv_fp16=False, context=ctx + steps + 2)
@@ -81,8 +99,10 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--config", default="mistral7b")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--cpu-steps", type=int, default=6)
-    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cpu-steps", type=int, default=2,
+                    help="timed oracle steps of the single-thread baseline (about 5 s each at the 7B shape)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the second, parallel oracle figure (0: up to 16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=8)
     ap.add_argument("--contexts", default="512,2048",
@@ -173,6 +193,9 @@ def main() -> int:
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
     log(f"gate/up GEMV: {per_launch_ms * 1e3:.1f} us/launch, {per_launch_bytes / 1e6:.1f} MB, {achieved:.0f} GB/s")
 
+    traffic, traffic_note = measured_traffic(args.config)
+    if traffic is None:
+        log(f"roofline.traffic: none ({traffic_note})")
     out = {
         "metric": "decode tok/s @batch 1, 7B-shape Q4_K_M; achieved HBM GB/s vs peak",
         "value": round(value, 2),
@@ -196,7 +219,7 @@ def main() -> int:
                      "peak_gbps": HBM_PEAK_GBPS, "frac": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBPS, 4)},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<Q4_K, SWIGLU, RmsNorm> (ffn gate+up, 14336x4096 x2)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.config),
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_note,
                      "bytes_per_launch": per_launch_bytes, "us_per_launch": round(per_launch_ms * 1e3, 2),
                      "stream_probe_gbps": {k: round(v, 1) for k, v in stream.items()}},
         "decode_by_context": by_ctx,
@@ -206,10 +229,16 @@ def main() -> int:
     eng.dispose()
     be.dispose()
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # the faithful figure: one thread, as the reference runs
         t0 = time.perf_counter()
-        out["cpu_baseline"] = cpu_baseline(img, args.ctx, args.cpu_steps, threads)
-        log(f"cpu baseline: {out['cpu_baseline']['value']:.3f} tok/s ({time.perf_counter() - t0:.1f}s)")
+        out["cpu_baseline"] = cpu_baseline(img, args.ctx, args.cpu_steps, 1)
+        log(f"cpu baseline (1 thread): {out['cpu_baseline']['value']:.4f} tok/s ({time.perf_counter() - t0:.1f}s)")
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        if threads > 1:
+            t0 = time.perf_counter()
+            par = cpu_baseline(img, args.ctx, 3 * args.cpu_steps, threads)
+            out["cpu_baseline"]["parallel"] = par
+            log(f"cpu baseline ({threads} threads): {par['value']:.3f} tok/s ({time.perf_counter() - t0:.1f}s)")
     print(json.dumps(out), flush=True)
     return 0
 

@@ -15,7 +15,7 @@
 //    |x s - hi - lo| <= 2^-23 |x s| -- 22-23 significant bits.
 //  * Weights: every supported format is (scale) * (small integer) per block
 //    (Q4_K/Q5_K: d * sc_g * (q - 8|16) - dmin * m_g; Q6_K: d * sc_16 * (q - 32);
-//    Q8_0: d * q; Q4_0: d * (q - 8), DequantizeK.cs / DequantizeBasic.cs).  The
+//    Q8_0: d * q; Q4_0: d * (q - 8), DequantizeK.cs / DequantizeBlock.cs).  The
 //    integer part v = sc * (q - c) is exact in fp16 (|v| <= 1008), except Q6_K
 //    (|v| <= 4096), which is split into v_hi + v_lo with v_lo in {-1, 0, 1}.
 //    Products of fp16 planes are exact in fp32, so a block's partial sum
