@@ -55,7 +55,7 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(img, ctx: int, steps: int, threads: int) -> dict:
+def cpu_baseline(img, ctx: int, steps: int, threads: int, warmup: bool = True) -> dict:
     """The reference CPU path (oracle restatement) on the same weights; with
     threads = 1 the reference's own execution model (no Parallel, Thread or
     Task in its src/)."""
@@ -64,7 +64,8 @@ def cpu_baseline(img, ctx: int, steps: int, threads: int) -> dict:
     m = O.Model(img, kv_fp16=False, context=ctx + steps + 2)
     m.kv_fill_random(ctx, seed=3)
     tok = 1
-    m.process_token(tok, ctx)            # warm-up step
+    if warmup:
+        m.process_token(tok, ctx)        # warm-up step
     t0 = time.perf_counter()
     for i in range(steps):
         lg = m.process_token(tok, ctx + 1 + i)
@@ -72,7 +73,7 @@ def cpu_baseline(img, ctx: int, steps: int, threads: int) -> dict:
     dt = time.perf_counter() - t0
     m.close()
     return {"value": steps / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"1 warm-up + {steps} greedy decode steps of the same model at position {ctx}+ "
+            "sample": f"{'1 warm-up + ' if warmup else ''}{steps} greedy decode step(s) of the same model at position {ctx}+ "
                       f"(KV filled synthetically), oracle restatement, {threads} OpenMP threads of "
                       f"{os.cpu_count()} host cores"}
 
@@ -91,6 +92,39 @@ def prefill_flops(spec: dict, n: int) -> float:
     return 2.0 * params * n + attn + 2.0 * d * spec["vocab"]
 
 
+# The other full-size workloads, measured after the headline run: name ->
+# (model, prompt tokens, KV format).  Decode is timed from the end of the prompt.
+EXTRA = {"c3": ("llama1b", 512, True), "c5": ("phi3mini", 2048, True)}
+
+
+def extra_config(be, key: str, seed: int, steps: int) -> dict:
+    """Prefill of the workload's prompt (batched MFMA path, HIP events) and the
+    greedy decode loop right after it, for one of EXTRA's shapes."""
+    from dotllm_amd import synth
+    from dotllm_amd.engine import InferenceEngine, LoadedModel
+    name, n, kv16 = EXTRA[key]
+    spec = synth.SPECS[name]
+    ctx = n + steps + 16
+    img = synth.build_image(name, seed=seed, context=ctx)
+    eng = InferenceEngine(LoadedModel.load(img), be, kv_fp16=kv16, context=ctx)
+    try:
+        prompt = synth.prompt(spec["vocab"], n, seed=7)
+        eng.time_prefill(prompt[:min(256, n)], 0)   # warm-up
+        pf_ms = eng.time_prefill(prompt, 0)
+        _, tok = eng.prefill(prompt, 0)
+        r = eng.time_decode(tok, n, steps)
+        dec = 1000.0 * steps / r["total_ms"]
+        fl = prefill_flops(spec, n)
+        return {"workload": f"{name}-shape, {n}-token prompt then greedy decode, batch 1, "
+                            f"{'fp16' if kv16 else 'fp32'} KV",
+                "prefill_tokens": n, "prefill_ms": round(pf_ms, 3), "prefill_tok_s": round(n / (pf_ms * 1e-3), 1),
+                "prefill_mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                "decode_tok_s": round(dec, 2), "decode_from_position": n, "decode_steps": steps,
+                "decode_step_gbps": round(eng.step_bytes(n + steps // 2) * dec / 1e9, 1)}
+    finally:
+        eng.dispose()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -99,8 +133,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--config", default="mistral7b")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--cpu-steps", type=int, default=2,
-                    help="timed oracle steps of the single-thread baseline (about 5 s each at the 7B shape)")
+    ap.add_argument("--cpu-steps", type=int, default=1,
+                    help="timed oracle steps of the single-thread baseline (about 23 s each at the 7B shape)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads of the second, parallel oracle figure (0: up to 16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -112,6 +146,8 @@ def main() -> int:
     ap.add_argument("--synthetic-kv", action="store_true",
                     help="fill the KV cache of the first --ctx positions with random values instead of "
                          "processing a --ctx-token prompt (same decode-step work; for short profiling runs)")
+    ap.add_argument("--extra", default="c3,c5",
+                    help="other full-size workloads timed after the headline run (prefill + decode); '' for none")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernel by kernel instead of replaying the captured HIP graph "
                          "(rocprofv3 cannot trace graph launches on this image)")
@@ -227,16 +263,23 @@ def main() -> int:
         "cpu_baseline": None,
     }
     eng.dispose()
+    extra = {}
+    for key in [k.strip() for k in args.extra.split(",") if k.strip()]:
+        t0 = time.perf_counter()
+        extra[key] = extra_config(be, key, args.seed, args.steps)
+        log(f"{key}: prefill {extra[key]['prefill_tok_s']:.0f} tok/s, decode {extra[key]['decode_tok_s']:.1f} tok/s "
+            f"({time.perf_counter() - t0:.1f}s)")
+    out["other_workloads"] = extra or None
     be.dispose()
     if not args.no_cpu_baseline:
         # the faithful figure: one thread, as the reference runs
         t0 = time.perf_counter()
-        out["cpu_baseline"] = cpu_baseline(img, args.ctx, args.cpu_steps, 1)
+        out["cpu_baseline"] = cpu_baseline(img, args.ctx, args.cpu_steps, 1, warmup=False)
         log(f"cpu baseline (1 thread): {out['cpu_baseline']['value']:.4f} tok/s ({time.perf_counter() - t0:.1f}s)")
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         if threads > 1:
             t0 = time.perf_counter()
-            par = cpu_baseline(img, args.ctx, 3 * args.cpu_steps, threads)
+            par = cpu_baseline(img, args.ctx, 6, threads)
             out["cpu_baseline"]["parallel"] = par
             log(f"cpu baseline ({threads} threads): {par['value']:.3f} tok/s ({time.perf_counter() - t0:.1f}s)")
     print(json.dumps(out), flush=True)
