@@ -350,22 +350,31 @@ def _fresh_engine_env(img, env, context, kv_fp16=True):
     return be, eng
 
 
-def test_attention_one_launch_matches_three(tiny_image):
+ATTN_PATHS = {"one launch + combine launch": {"LLMDOT_HIP_ATTN_FUSED": "1"},
+              "three launches": {"LLMDOT_HIP_ATTN_FUSED": "0"}}
+
+
+@pytest.mark.parametrize("model,cached", [("tiny", 448), ("tiny", 30), ("small5", 200)])
+def test_attention_one_launch_matches_three(model, cached):
     """The one-launch attention (chunk maxima exchanged between workgroups)
     and the three-launch form compute the same sums in different orders (the
     dot products are split over two threads per key instead of four): over
-    decode steps at a 448-position seeded cache, logits within fp32 noise of
-    each other on the 4-layer tiny model (fp32 KV)."""
-    outs = []
-    for fused in ("1", "0"):
-        be, eng = _fresh_engine_env(tiny_image, {"LLMDOT_HIP_ATTN_FUSED": fused}, 464, kv_fp16=False)
-        eng.kv_fill_random(448, seed=3)
-        outs.append([eng.process_token(t, 448 + i) for i, t in enumerate((5, 77, 901))])
+    decode steps from a seeded cache of 448 positions (7 chunks per kv head),
+    30 (one chunk) and 200 (query groups of 2), logits within fp32 noise of
+    each other (fp32 KV)."""
+    img = synth.build_image(model, seed=1234)
+    outs = {}
+    for name, env in ATTN_PATHS.items():
+        be, eng = _fresh_engine_env(img, env, cached + 16, kv_fp16=False)
+        eng.kv_fill_random(cached, seed=3)
+        outs[name] = [eng.process_token(t, cached + i) for i, t in enumerate((5, 77, 901))]
         eng.dispose()
         be.dispose()
-    errs = [float(np.max(np.abs(a - b))) for a, b in zip(*outs)]
-    print(f"tiny: one launch vs three, max |dlogit| per step {['%.2e' % e for e in errs]}")
-    assert max(errs) <= 1e-4
+    ref = outs["three launches"]
+    for name, got in outs.items():
+        errs = [float(np.max(np.abs(a - b))) for a, b in zip(got, ref)]
+        print(f"{model} at {cached}: {name} vs three launches, max |dlogit| per step {['%.2e' % e for e in errs]}")
+        assert max(errs) <= 1e-4, name
 
 
 @pytest.mark.parametrize("fused", ["1", "0"])
