@@ -549,8 +549,8 @@ extern "C" int32_t llmdot_hip_scale(llmdot_hip_ctx* ctx, const float* input, flo
 extern "C" int32_t llmdot_hip_dequantize(llmdot_hip_ctx* ctx, const void* src, float* dst, uint32_t type, int32_t num_rows,
                                          int32_t row_elements) {
     if (!ctx || !src || !dst || num_rows < 0 || row_elements <= 0) return fail(LLMDOT_E_INVALID, "bad DequantizeToFloat arguments");
-    if (block_elems(type) == 0 || type == GGML_Q4_1 || type == GGML_Q5_0 || type == GGML_Q5_1)
-        return fail(LLMDOT_E_UNSUPPORTED, "Dequantization for type " + std::to_string(type) + " not implemented.");
+    if (block_elems(type) == 0)   // TensorOps.DequantizeGeneric's NotSupportedException (TO:647-648)
+        return fail(LLMDOT_E_UNSUPPORTED, "Dequantization for type " + std::to_string(type) + " not yet implemented.");
     if (row_elements % block_elems(type) != 0) return fail(LLMDOT_E_INVALID, "row not a whole number of blocks");
     if (num_rows == 0) return 0;
     if (int rc = ensure_device(ctx)) return rc;

@@ -34,6 +34,34 @@ __device__ float deq_elem(uint32_t type, const uint8_t* row, int i) {
         int q = j < 16 ? (qs & 0x0F) : ((qs >> 4) & 0x0F);
         return ((float)(q - 8) * d);
     }
+    case GGML_Q4_1: {  // TO:586-603: d * q + m, low nibbles -> j, high -> j + 16
+        const uint8_t* b = row + (i >> 5) * 20;
+        int j = i & 31;
+        float d = h2f_at(b), m = h2f_at(b + 2);
+        int qs = b[4 + (j & 15)];
+        int q = j < 16 ? (qs & 0x0F) : ((qs >> 4) & 0x0F);
+        return ((d * (float)q) + m);
+    }
+    case GGML_Q5_0: {  // TO:604-622: (q | high bit from qh) - 16, times d
+        const uint8_t* b = row + (i >> 5) * 22;
+        int j = i & 31, jj = j & 15;
+        float d = h2f_at(b);
+        uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+        int qs = b[6 + jj];
+        int x = j < 16 ? (((qs & 0x0F) | (int)(((qh >> jj) << 4) & 0x10u)) - 16)
+                       : ((((qs >> 4) & 0x0F) | (int)((qh >> (jj + 12)) & 0x10u)) - 16);
+        return ((float)x * d);
+    }
+    case GGML_Q5_1: {  // TO:623-641: d * (q | high bit from qh) + m
+        const uint8_t* b = row + (i >> 5) * 24;
+        int j = i & 31, jj = j & 15;
+        float d = h2f_at(b), m = h2f_at(b + 2);
+        uint32_t qh = (uint32_t)b[4] | ((uint32_t)b[5] << 8) | ((uint32_t)b[6] << 16) | ((uint32_t)b[7] << 24);
+        int qs = b[8 + jj];
+        int x = j < 16 ? ((qs & 0x0F) | (int)(((qh >> jj) << 4) & 0x10u))
+                       : (((qs >> 4) & 0x0F) | (int)((qh >> (jj + 12)) & 0x10u));
+        return ((d * (float)x) + m);
+    }
     case GGML_Q8_0: {  // DB:36-59
         const uint8_t* b = row + (i >> 5) * 34;
         return ((float)(int8_t)b[2 + (i & 31)] * h2f_at(b));

@@ -406,6 +406,71 @@ struct TQ4_0 {   // Q4_0, 18 B / 32: unit = block; low nibbles -> j, high -> j +
     }
 };
 
+// Q4_1 (20 B / 32): d, m, 16 nibble bytes (low -> j, high -> j + 16); d q + m
+// (TO:586-603, reached through MatMul's dequantise-then-dot path TO:92-111).
+struct TQ4_1 {
+    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 1, DEPTH = 2;
+    struct Raw { u32x4 Q; uint32_t h; };
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) {
+        const uint8_t* blk = row + u * 20;   // 4-byte aligned (20-byte blocks, 4-aligned rows)
+        r.h = ld4_a4(blk);
+        r.Q = ld16_a4(blk + 4);
+    }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
+        const uint32_t q[4] = {r.Q.x, r.Q.y, r.Q.z, r.Q.w};
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = (q[j] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s0 += x.v[4 * j + k] * ub(lo, k);
+                s1 += x.v[16 + 4 * j + k] * ub(hi, k);
+            }
+        }
+        return h16(r.h & 0xFFFFu) * (s0 + s1) + h16(r.h >> 16) * x.s[0];
+    }
+};
+
+// Q5_0 (22 B / 32, 2-byte aligned) and Q5_1 (24 B / 32): d [, m], the 32 high
+// bits qh, 16 nibble bytes; element j < 16 is (nibble | bit j of qh << 4),
+// j + 16 the high nibble with bit j + 16; Q5_0: d (x - 16), Q5_1: d x + m
+// (TO:604-641).
+template <bool ONE>
+struct TQ5_01 {
+    static constexpr int BB = ONE ? 24 : 22, OQ = ONE ? 8 : 6, OH = ONE ? 4 : 2;
+    static constexpr int RB = 8, NS = 1, RUN = 32, PRE = 1, DEPTH = 2;
+    struct Raw { RawW<6> W; };   // bytes [0, 24) of the block: header, qh, the 16 quant bytes
+    __device__ static int xoff(int u, int) { return u * 32; }
+    __device__ static void load(Raw& r, const uint8_t* row, int u) { r.W.load(row + u * BB); }
+    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
+        // qh at byte OH, quants at byte OQ (both even): realign by 2 bytes when needed
+        const uint32_t w0 = r.W[0];
+        const uint32_t qh = OH == 4 ? r.W[1] : __builtin_amdgcn_alignbyte(r.W[1], w0, 2);
+        uint32_t q[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            q[j] = OQ == 8 ? r.W[2 + j] : __builtin_amdgcn_alignbyte(r.W[2 + j], r.W[1 + j], 2);
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // bits 4j .. 4j + 3 of qh -> bit 4 of bytes 0..3 (low half), bits 16 + 4j .. of qh (high half)
+            const uint32_t hl = (((qh >> (4 * j)) & 15u) * 0x00204081u) & 0x01010101u;
+            const uint32_t hh = (((qh >> (16 + 4 * j)) & 15u) * 0x00204081u) & 0x01010101u;
+            const uint32_t lo = (q[j] & 0x0F0F0F0Fu) | (hl << 4), hi = ((q[j] >> 4) & 0x0F0F0F0Fu) | (hh << 4);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s0 += x.v[4 * j + k] * ub(lo, k);
+                s1 += x.v[16 + 4 * j + k] * ub(hi, k);
+            }
+        }
+        const float d = h16(w0 & 0xFFFFu);
+        if constexpr (ONE) return d * (s0 + s1) + h16(w0 >> 16) * x.s[0];
+        else return d * ((s0 + s1) - 16.f * x.s[0]);
+    }
+};
+
 struct TF32 {
     static constexpr int RB = 2, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
     struct Raw { float4 f[8]; };
@@ -457,6 +522,9 @@ template <> struct TypeOf<GGML_Q5_K> { using type = TQ5K; };
 template <> struct TypeOf<GGML_Q6_K> { using type = TQ6K; };
 template <> struct TypeOf<GGML_Q8_0> { using type = TQ8_0; };
 template <> struct TypeOf<GGML_Q4_0> { using type = TQ4_0; };
+template <> struct TypeOf<GGML_Q4_1> { using type = TQ4_1; };
+template <> struct TypeOf<GGML_Q5_0> { using type = TQ5_01<false>; };
+template <> struct TypeOf<GGML_Q5_1> { using type = TQ5_01<true>; };
 template <> struct TypeOf<GGML_F32> { using type = TF32; };
 template <> struct TypeOf<GGML_F16> { using type = TF16; };
 
@@ -819,7 +887,8 @@ bool generic_shape(uint32_t type, int cols) { return (type == GGML_F32 || type =
 
 bool gemv_supported(uint32_t type) {
     return type == GGML_Q4_K || type == GGML_Q5_K || type == GGML_Q6_K || type == GGML_Q8_0 ||
-           type == GGML_Q4_0 || type == GGML_Q2_K || type == GGML_Q3_K || type == GGML_F32 || type == GGML_F16;
+           type == GGML_Q4_0 || type == GGML_Q4_1 || type == GGML_Q5_0 || type == GGML_Q5_1 ||
+           type == GGML_Q2_K || type == GGML_Q3_K || type == GGML_F32 || type == GGML_F16;
 }
 
 bool gemv_width_ok(uint32_t type, int cols) {
@@ -953,6 +1022,9 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     case GGML_Q6_K: e = launch_t<GGML_Q6_K>(epi, a, nb, grid, threads, s); break;
     case GGML_Q8_0: e = launch_t<GGML_Q8_0>(epi, a, nb, grid, threads, s); break;
     case GGML_Q4_0: e = launch_t<GGML_Q4_0>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q4_1: e = launch_t<GGML_Q4_1>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q5_0: e = launch_t<GGML_Q5_0>(epi, a, nb, grid, threads, s); break;
+    case GGML_Q5_1: e = launch_t<GGML_Q5_1>(epi, a, nb, grid, threads, s); break;
     case GGML_Q2_K: e = launch_t<GGML_Q2_K>(epi, a, nb, grid, threads, s); break;
     case GGML_Q3_K: e = launch_t<GGML_Q3_K>(epi, a, nb, grid, threads, s); break;
     case GGML_F32: e = launch_t<GGML_F32>(epi, a, nb, grid, threads, s); break;

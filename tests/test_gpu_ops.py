@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from dotllm_amd import F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, BF16, byte_count, synth
-from dotllm_amd._lib import Q2_K, Q3_K
+from dotllm_amd._lib import Q2_K, Q3_K, Q4_1, Q5_0, Q5_1
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -32,10 +32,10 @@ def random_blocks(t, rows, cols, seed):
     rng = np.random.default_rng(seed)
     b = rng.integers(0, 256, size=rows * byte_count(t, cols), dtype=np.uint8)
     be, bb = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18),
-              Q2_K: (256, 84), Q3_K: (256, 110)}[t]
+              Q2_K: (256, 84), Q3_K: (256, 110), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24)}[t]
     blocks = b.reshape(-1, bb)
     halves = rng.uniform(-2, 2, size=(blocks.shape[0], 2)).astype(np.float16).view(np.uint8)
-    if t in (Q4_K, Q5_K, Q2_K, Q3_K):
+    if t in (Q4_K, Q5_K, Q2_K, Q3_K, Q4_1, Q5_1):
         blocks[:, 0:4] = halves.reshape(-1, 4)
     elif t == Q6_K:
         blocks[:, 208:210] = halves[:, :2]
@@ -67,6 +67,34 @@ def test_dequantize_lowbit_kquants_bit_exact(hip, t, rows, cols):
     out = np.zeros(rows * cols, dtype=np.float32)
     hip.dequantize_to_float(src, out, t, rows, cols)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q4_1, Q5_0, Q5_1])
+@pytest.mark.parametrize("rows,cols", [(1, 32), (7, 1024), (33, 4128)])
+def test_dequantize_generic_types_bit_exact(hip, t, rows, cols):
+    """Q4_1, Q5_0, Q5_1 (TensorOps.DequantizeGeneric, TO:580-652) over random
+    blocks with finite scales, every element bit for bit; 4128 columns give
+    rows of an odd number of 22-byte blocks (2-byte aligned rows)."""
+    src = random_blocks(t, rows, cols, 60 + rows)
+    ref = O.dequantize(src, t, rows, cols)
+    out = np.zeros(rows * cols, dtype=np.float32)
+    hip.dequantize_to_float(src, out, t, rows, cols)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q4_1, Q5_0, Q5_1])
+@pytest.mark.parametrize("rows,cols", [(300, 2048), (257, 4128), (1024, 4096)])
+def test_generic_type_gemv(hip, t, rows, cols):
+    """MatMul of Q4_1 / Q5_0 / Q5_1 weights (the reference dequantises the row
+    and takes the 8-lane dot product, TO:92-111, 510-531) within 1e-3 of the
+    oracle's MatMul and of the fp64 product of the dequantised rows."""
+    w = random_blocks(t, rows, cols, rows + 11)
+    x = np.random.default_rng(cols + 1).normal(0, 1, size=cols).astype(np.float32)
+    ref = O.matmul(x, w, t, cols, rows)
+    exact = O.dequantize(w, t, rows, cols).reshape(rows, cols).astype(np.float64) @ x.astype(np.float64)
+    y = np.zeros(rows, dtype=np.float32)
+    hip.mat_mul(x, w, y, t, cols, rows)
+    assert rel_err(y, ref) <= GEMV_TOL and rel_err(y, exact) <= GEMV_TOL
 
 
 @pytest.mark.parametrize("t", [F16, BF16, F32])
@@ -297,4 +325,4 @@ def test_argmax_ties_first_index(hip):
 
 def test_unsupported_type_raises(hip):
     with pytest.raises(NotImplementedError):
-        hip.mat_mul(np.zeros(256, np.float32), np.zeros(176, np.uint8), np.zeros(1, np.float32), 6, 256, 1)   # Q5_0
+        hip.mat_mul(np.zeros(256, np.float32), np.zeros(40 * 8, np.uint8), np.zeros(1, np.float32), 9, 256, 1)   # Q8_1

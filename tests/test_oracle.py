@@ -316,6 +316,58 @@ def test_q3k_reads_two_bytes_of_the_next_block():
     assert np.array_equal(x[256:], np.zeros(256, np.float32) * d1)   # scales 0: zeros of the block's sign
 
 
+# ---------------------------------------------------------- Q4_1 / Q5_0 / Q5_1 --
+# TensorOps.DequantizeGeneric (TO:580-652): blocks of 32 written field by field.
+
+Q4_1, Q5_0, Q5_1 = 3, 6, 7
+
+
+def _q45block(t, d, m, q):
+    """Q4_1 (20 B: d, m, nibbles), Q5_0 (22 B: d, qh, nibbles), Q5_1 (24 B: d,
+    m, qh, nibbles); element j < 16 in the low nibble of quant byte j, j + 16
+    in its high nibble; the fifth bit of element e is bit e of qh."""
+    size, oq, oh = {Q4_1: (20, 4, None), Q5_0: (22, 6, 2), Q5_1: (24, 8, 4)}[t]
+    b = np.zeros(size, dtype=np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    if t != Q5_0:
+        b[2:4] = np.array([m], np.float16).view(np.uint8)
+    qh = 0
+    for e in range(32):
+        b[oq + (e & 15)] |= (q[e] & 15) << (4 * (e >> 4))
+        qh |= ((q[e] >> 4) & 1) << e
+    if oh is not None:
+        b[oh:oh + 4] = np.array([qh], np.uint32).view(np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("t", [Q4_1, Q5_0, Q5_1])
+def test_generic_types_every_value(t):
+    """Every quant value at every position (a rotating pattern), with the
+    closed forms d q + m (Q4_1), d (q - 16) (Q5_0), d q + m (Q5_1)."""
+    top = 16 if t == Q4_1 else 32
+    for shift in range(top):
+        q = [(e + shift) % top for e in range(32)]
+        d, m = 0.5, -1.25
+        x = O.dequantize(_q45block(t, d, m, q), t, 1, 32).astype(np.float64)
+        if t == Q5_0:
+            want = [d * (v - 16) for v in q]
+        else:
+            want = [d * v + m for v in q]
+        assert np.array_equal(x, np.asarray(want, np.float32)), shift
+
+
+def test_q5_high_bit_walk():
+    """One set bit of qh at a time moves exactly that element by 16 d."""
+    for t in (Q5_0, Q5_1):
+        base = O.dequantize(_q45block(t, 0.25, 0.0, [3] * 32), t, 1, 32)
+        for e in range(32):
+            q = [3] * 32
+            q[e] = 19
+            x = O.dequantize(_q45block(t, 0.25, 0.0, q), t, 1, 32)
+            diff = np.nonzero(x != base)[0]
+            assert list(diff) == [e] and x[e] - base[e] == np.float32(4.0), (t, e)
+
+
 # ------------------------------------------------------------------------ GEMV --
 
 @pytest.mark.parametrize("t", [Q2_K, Q3_K])
