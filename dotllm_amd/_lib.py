@@ -98,6 +98,10 @@ SIGNATURES = {
     "llmdot_hip_apply_rope_base": [_P, _P, _P, _I32, _I32, _F, _I32, _I32],
     "llmdot_hip_softmax": [_P, _P, _I32, _I32, _F],
     "llmdot_hip_silu": [_P, _P, _P, _I32],
+    "llmdot_hip_layer_norm": [_P, _P, _P, _P, _P, _I32, _F],
+    "llmdot_hip_gelu": [_P, _P, _P, _I32],
+    "llmdot_hip_softcap": [_P, _P, _I32, _F],
+    "llmdot_hip_conv1d": [_P, _P, _P, _P, _I32, _I32],
     "llmdot_hip_add": [_P, _P, _P, _P, _I32],
     "llmdot_hip_scale": [_P, _P, _F, _P, _I32],
     "llmdot_hip_mul": [_P, _P, _P, _P, _I32],

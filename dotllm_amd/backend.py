@@ -9,10 +9,10 @@ cache, src/Llmdot.Metal/MetalBackend.cs:92-100, does the same per key).
 
 Errors surface as exceptions with the reference's types: ValueError for
 ArgumentException, NotImplementedError for NotSupportedException, KeyError for
-KeyNotFoundException, IndexError for ArgumentOutOfRangeException.  Members that
-the LLaMA decode path never calls (LayerNorm, Gelu, Softcap, Conv1D) raise
-NotImplementedError; an adapter delegates those to the CPU backend, as
-VulkanBackend does for every op (src/Llmdot.Vulkan/VulkanBackend.cs:32-88).
+KeyNotFoundException, IndexError for ArgumentOutOfRangeException (and for
+spans shorter than the reference would index).  Every member runs on the
+device, including those the LLaMA-like decode path never calls (LayerNorm,
+Gelu, GeluScalar, Softcap, Conv1D).
 """
 from __future__ import annotations
 
@@ -206,18 +206,49 @@ class HipBackend:
                                       C.byref(tok)))
         return tok.value
 
-    # Members off the LLaMA decode path (ICB:12, 18, 19, 25, 26).
-    def layer_norm(self, *args, **kw):
-        raise NotImplementedError("LayerNorm is not on the LLaMA-like decode path")
+    # Members the LLaMA-like decode path does not call (other templates), on
+    # the device like the rest (ICB:12, 18, 19, 25, 26).
+    def layer_norm(self, inp, weights, bias, output, epsilon: float) -> None:
+        """ICB:12 LayerNorm(input, weights, bias, output, epsilon); bias None or
+        empty is the reference's empty bias span."""
+        inp, weights, output = _f32(inp, "input"), _f32(weights, "weights"), _f32(output, "output")
+        n = inp.size
+        if weights.size < n or output.size < n:
+            raise IndexError("weights and output must hold input.Length elements")
+        bp = None
+        if bias is not None and np.asarray(bias).size > 0:
+            bias = _f32(bias, "bias")
+            if bias.size < n:
+                raise IndexError("bias must be empty or hold input.Length elements")
+            bp = ptr(bias)
+        _call(lib().llmdot_hip_layer_norm(self._ctx, ptr(inp), ptr(weights), bp, ptr(output), n, epsilon))
 
-    def gelu(self, *args, **kw):
-        raise NotImplementedError("Gelu is not on the LLaMA-like decode path")
+    def gelu(self, inp, result) -> None:
+        """ICB:18 Gelu(input, result)."""
+        inp, result = _f32(inp, "input"), _f32(result, "result")
+        if result.size < inp.size:
+            raise IndexError("result must hold input.Length elements")
+        _call(lib().llmdot_hip_gelu(self._ctx, ptr(inp), ptr(result), inp.size))
 
     def gelu_scalar(self, x: float) -> float:
-        raise NotImplementedError("GeluScalar is not on the LLaMA-like decode path")
+        """ICB:19 GeluScalar(x): the one-element Gelu (its scalar form)."""
+        a = np.array([x], dtype=np.float32)
+        out = np.zeros(1, dtype=np.float32)
+        _call(lib().llmdot_hip_gelu(self._ctx, ptr(a), ptr(out), 1))
+        return float(out[0])
 
-    def softcap(self, *args, **kw):
-        raise NotImplementedError("Softcap is not on the LLaMA-like decode path")
+    def softcap(self, inp, cap: float) -> None:
+        """ICB:25 Softcap(input, cap) in place."""
+        inp = _f32(inp, "input")
+        _call(lib().llmdot_hip_softcap(self._ctx, ptr(inp), inp.size, cap))
 
-    def conv1d(self, *args, **kw):
-        raise NotImplementedError("Conv1D is not on the LLaMA-like decode path")
+    def conv1d(self, inp, weights, output, kernel_size: int, input_dim: int) -> None:
+        """ICB:26 Conv1D(input, weights, output, kernelSize, inputDim): input and
+        weights [inputDim][kernelSize], output [inputDim]."""
+        inp, weights, output = _f32(inp, "input"), _f32(weights, "weights"), _f32(output, "output")
+        if kernel_size < 1 or input_dim < 0:
+            raise ValueError("kernel_size must be positive and input_dim non-negative")
+        need = kernel_size * input_dim
+        if inp.size < need or weights.size < need or output.size < input_dim:
+            raise IndexError("input and weights must hold kernelSize * inputDim elements, output inputDim")
+        _call(lib().llmdot_hip_conv1d(self._ctx, ptr(inp), ptr(weights), ptr(output), kernel_size, input_dim))

@@ -4,7 +4,6 @@ using Llmdot.Hip.Native;
 using Llmdot.Inference;
 using Llmdot.Loading;
 using Llmdot.Tensors;
-using Llmdot.Tensors.Numeric;
 
 namespace Llmdot.Hip;
 
@@ -12,16 +11,14 @@ namespace Llmdot.Hip;
 /// IComputeBackend (src/Llmdot.Core/Inference/Backends/IComputeBackend.cs:7-29)
 /// on one AMD Instinct MI355X through libllmdot_hip.so.
 ///
-/// Op level: every member on the LLaMA-like decode path (MatMul, MatMulF32,
-/// RmsNorm, both ApplyRoPE overloads, Softmax, Silu, SiluInPlace, both Add
-/// overloads, both Scale overloads, Mul, DequantizeToFloat, ArgMax) runs on the
-/// device with the reference's arithmetic (bit-exact where the C header says
-/// so); MatMul keeps a weight uploaded once under its weightKey resident in
-/// HBM.  Spans are host memory, so each call copies its operands over PCIe:
-/// correct and useful for validation, not fast.  LayerNorm, Gelu, GeluScalar,
-/// Softcap and Conv1D belong to other model templates (GPT-2/Phi-2, Gemma,
-/// LFM2) and run on the host with the reference's own VectorMath/TensorOps,
-/// as VulkanBackend does for the members it does not accelerate.
+/// Op level: every member runs on the device with the reference's arithmetic
+/// (bit-exact where the C header says so): those on the LLaMA-like decode path
+/// (MatMul, MatMulF32, RmsNorm, both ApplyRoPE overloads, Softmax, Silu,
+/// SiluInPlace, both Add overloads, both Scale overloads, Mul,
+/// DequantizeToFloat, ArgMax) and those of other model templates (LayerNorm,
+/// Gelu, GeluScalar, Softcap, Conv1D); MatMul keeps a weight uploaded once
+/// under its weightKey resident in HBM.  Spans are host memory, so each call
+/// copies its operands over PCIe: correct and useful for validation, not fast.
 ///
 /// Fast path: <see cref="TryCreateDecoder"/> (IDeviceDecodeBackend) gives
 /// InferenceEngine a <see cref="HipDecoder"/> that keeps weights, KV cache and
@@ -117,7 +114,17 @@ public sealed unsafe class HipBackend : IComputeBackend, IDeviceDecodeBackend
     }
 
     public void LayerNorm(ReadOnlySpan<float> input, ReadOnlySpan<float> weights, ReadOnlySpan<float> bias, Span<float> output, float epsilon)
-        => VectorMath.LayerNorm(input, weights, bias, output, epsilon);
+    {
+        var n = input.Length;
+        if (n == 0) return;
+        if (weights.Length < n || output.Length < n) throw new ArgumentException("weights and output must hold input.Length values");
+        if (bias.Length > 0 && bias.Length < n) throw new ArgumentException("bias must be empty or hold input.Length values");
+        fixed (float* pi = input)
+        fixed (float* pw = weights)
+        fixed (float* pb = bias)
+        fixed (float* po = output)
+            HipNative.Check(HipNative.llmdot_hip_layer_norm(Handle, pi, pw, bias.Length > 0 ? pb : null, po, n, epsilon));
+    }
 
     // ---- ICB:13-14 rotary embedding (one head of query and key) --------------------------
 
@@ -166,9 +173,22 @@ public sealed unsafe class HipBackend : IComputeBackend, IDeviceDecodeBackend
             HipNative.Check(HipNative.llmdot_hip_silu(Handle, p, p, input.Length));
     }
 
-    public void Gelu(ReadOnlySpan<float> input, Span<float> result) => VectorMath.Gelu(input, result);
+    public void Gelu(ReadOnlySpan<float> input, Span<float> result)
+    {
+        if (input.IsEmpty) return;
+        if (result.Length < input.Length) throw new ArgumentException("result shorter than input");
+        fixed (float* pi = input)
+        fixed (float* pr = result)
+            HipNative.Check(HipNative.llmdot_hip_gelu(Handle, pi, pr, input.Length));
+    }
 
-    public float GeluScalar(float x) => VectorMath.Gelu(x);
+    /// <summary>VectorMath.Gelu(float): the one-element Gelu, which takes the scalar form.</summary>
+    public float GeluScalar(float x)
+    {
+        float r;
+        HipNative.Check(HipNative.llmdot_hip_gelu(Handle, &x, &r, 1));
+        return r;
+    }
 
     // ---- ICB:20-24 elementwise ------------------------------------------------------------
 
@@ -217,12 +237,26 @@ public sealed unsafe class HipBackend : IComputeBackend, IDeviceDecodeBackend
             HipNative.Check(HipNative.llmdot_hip_mul(Handle, pa, pb, pr, a.Length));
     }
 
-    // ---- ICB:25-26 other templates' operators (host, the reference's code) ---------------
+    // ---- ICB:25-26 other templates' operators -------------------------------------------
 
-    public void Softcap(Span<float> input, float cap) => VectorMath.Softcap(input, cap);
+    public void Softcap(Span<float> input, float cap)
+    {
+        if (input.IsEmpty) return;
+        fixed (float* p = input)
+            HipNative.Check(HipNative.llmdot_hip_softcap(Handle, p, input.Length, cap));
+    }
 
     public void Conv1D(ReadOnlySpan<float> input, ReadOnlySpan<float> weights, Span<float> output, int kernelSize, int inputDim)
-        => TensorOps.Conv1D(input, weights, output, kernelSize, inputDim);
+    {
+        if (inputDim == 0) return;
+        var need = (long)kernelSize * inputDim;
+        if (input.Length < need || weights.Length < need || output.Length < inputDim)
+            throw new IndexOutOfRangeException("input and weights must hold kernelSize * inputDim values, output inputDim");
+        fixed (float* pi = input)
+        fixed (float* pw = weights)
+        fixed (float* po = output)
+            HipNative.Check(HipNative.llmdot_hip_conv1d(Handle, pi, pw, po, kernelSize, inputDim));
+    }
 
     // ---- ICB:27-28 ------------------------------------------------------------------------------
 

@@ -91,6 +91,10 @@ internal static unsafe partial class HipNative
     [DllImport(Lib)] public static extern int llmdot_hip_apply_rope_base(nint ctx, float* query, float* key, int headDim, int position, float freqBase, int rotaryDim, int sameSpan);
     [DllImport(Lib)] public static extern int llmdot_hip_softmax(nint ctx, float* input, int n, int hasSoftcap, float softcap);
     [DllImport(Lib)] public static extern int llmdot_hip_silu(nint ctx, float* input, float* result, int n);
+    [DllImport(Lib)] public static extern int llmdot_hip_layer_norm(nint ctx, float* input, float* weights, float* biasOrNull, float* output, int n, float epsilon);
+    [DllImport(Lib)] public static extern int llmdot_hip_gelu(nint ctx, float* input, float* result, int n);
+    [DllImport(Lib)] public static extern int llmdot_hip_softcap(nint ctx, float* input, int n, float cap);
+    [DllImport(Lib)] public static extern int llmdot_hip_conv1d(nint ctx, float* input, float* weights, float* output, int kernelSize, int inputDim);
     [DllImport(Lib)] public static extern int llmdot_hip_add(nint ctx, float* a, float* b, float* result, int n);
     [DllImport(Lib)] public static extern int llmdot_hip_scale(nint ctx, float* input, float scale, float* result, int n);
     [DllImport(Lib)] public static extern int llmdot_hip_mul(nint ctx, float* a, float* b, float* result, int n);

@@ -515,6 +515,58 @@ extern "C" int32_t llmdot_hip_silu(llmdot_hip_ctx* ctx, const float* input, floa
     return copy_out(ctx, result, dy, sizeof(float) * (size_t)n);
 }
 
+extern "C" int32_t llmdot_hip_layer_norm(llmdot_hip_ctx* ctx, const float* input, const float* weights,
+                                         const float* bias_or_null, float* output, int32_t n, float epsilon) {
+    if (!ctx || n < 0 || (n > 0 && (!input || !weights || !output))) return fail(LLMDOT_E_INVALID, "bad LayerNorm arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float *dx, *dw, *db = nullptr, *dy;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    if (int rc = stage_in(ctx, 1, weights, (size_t)n, &dw)) return rc;
+    if (bias_or_null)
+        if (int rc = stage_in(ctx, 2, bias_or_null, (size_t)n, &db)) return rc;
+    if (int rc = stage_in<float>(ctx, 3, nullptr, (size_t)n, &dy)) return rc;
+    HIPCHK(launch_layernorm(dx, dw, db, dy, n, epsilon, ctx->stream));
+    return copy_out(ctx, output, dy, sizeof(float) * (size_t)n);
+}
+
+extern "C" int32_t llmdot_hip_gelu(llmdot_hip_ctx* ctx, const float* input, float* result, int32_t n) {
+    if (!ctx || n < 0 || (n > 0 && (!input || !result))) return fail(LLMDOT_E_INVALID, "bad Gelu arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float *dx, *dy;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    if (int rc = stage_in<float>(ctx, 1, nullptr, (size_t)n, &dy)) return rc;
+    HIPCHK(launch_gelu(dx, dy, n, ctx->stream));
+    return copy_out(ctx, result, dy, sizeof(float) * (size_t)n);
+}
+
+extern "C" int32_t llmdot_hip_softcap(llmdot_hip_ctx* ctx, float* input, int32_t n, float cap) {
+    if (!ctx || n < 0 || (n > 0 && !input)) return fail(LLMDOT_E_INVALID, "bad Softcap arguments");
+    if (n == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    float* dx;
+    if (int rc = stage_in(ctx, 0, input, (size_t)n, &dx)) return rc;
+    HIPCHK(launch_softcap(dx, n, cap, ctx->stream));
+    return copy_out(ctx, input, dx, sizeof(float) * (size_t)n);
+}
+
+extern "C" int32_t llmdot_hip_conv1d(llmdot_hip_ctx* ctx, const float* input, const float* weights, float* output,
+                                     int32_t kernel_size, int32_t input_dim) {
+    if (!ctx || kernel_size < 1 || input_dim < 0 || (input_dim > 0 && (!input || !weights || !output)))
+        return fail(LLMDOT_E_INVALID, "bad Conv1D arguments");
+    if ((int64_t)kernel_size * input_dim > INT32_MAX) return fail(LLMDOT_E_RANGE, "Conv1D input too large");
+    if (input_dim == 0) return 0;
+    if (int rc = ensure_device(ctx)) return rc;
+    const size_t n = (size_t)kernel_size * (size_t)input_dim;
+    float *dx, *dw, *dy;
+    if (int rc = stage_in(ctx, 0, input, n, &dx)) return rc;
+    if (int rc = stage_in(ctx, 1, weights, n, &dw)) return rc;
+    if (int rc = stage_in<float>(ctx, 2, nullptr, (size_t)input_dim, &dy)) return rc;
+    HIPCHK(launch_conv1d(dx, dw, dy, kernel_size, input_dim, ctx->stream));
+    return copy_out(ctx, output, dy, sizeof(float) * (size_t)input_dim);
+}
+
 namespace {
 int binary_common(llmdot_hip_ctx* ctx, int op, const float* a, const float* b, float* result, int n) {
     if (!ctx || !a || !b || !result || n < 0) return fail(LLMDOT_E_INVALID, "bad elementwise arguments");

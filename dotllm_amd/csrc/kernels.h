@@ -80,6 +80,11 @@ hipError_t launch_rope(float* q, float* k, const float* cosv, const float* sinv,
                        hipStream_t s);
 hipError_t launch_softmax(float* x, int n, int has_softcap, float cap, hipStream_t s);
 hipError_t launch_silu(const float* in, float* out, int n, hipStream_t s);
+hipError_t launch_layernorm(const float* in, const float* w, const float* b, float* out, int n, float eps,
+                            hipStream_t s);
+hipError_t launch_gelu(const float* in, float* out, int n, hipStream_t s);
+hipError_t launch_softcap(float* x, int n, float cap, hipStream_t s);
+hipError_t launch_conv1d(const float* in, const float* w, float* out, int kernel_size, int input_dim, hipStream_t s);
 hipError_t launch_binary(int op, const float* a, const float* b, float* out, int n, hipStream_t s);  // 0 add, 1 mul
 hipError_t launch_scale(const float* in, float sc, float* out, int n, hipStream_t s);
 // ArgMax over n floats (two launches); st.cand_* sized for argmax_grid(n).

@@ -1,6 +1,6 @@
 // ops.hip -- op-level IComputeBackend members (src/Llmdot.Core/Inference/Backends/
-// IComputeBackend.cs:7-29) that are not GEMVs: RmsNorm, ApplyRoPE, Softmax,
-// Silu, Add, Mul, Scale, ArgMax.  Each reproduces the arithmetic of the
+// IComputeBackend.cs:7-29) that are not GEMVs: RmsNorm, LayerNorm, ApplyRoPE,
+// Softmax, Silu, Gelu, Add, Mul, Scale, Softcap, Conv1D, ArgMax.  Each reproduces the arithmetic of the
 // reference's VectorMath (src/Llmdot.Core/Tensors/Numeric/VectorMath.cs) per
 // element: the 8-lane Vector<float> part and the scalar tail use their own
 // formulas where the reference's differ.
@@ -96,6 +96,74 @@ __global__ __launch_bounds__(WG_BIG) void softmax_kernel(float* x, int n, int ha
     s = block_sum<WG_BIG>(s, red);
     const float inv = (1.0f / (s));
     for (int i = threadIdx.x; i < n; i += WG_BIG) x[i] = (x[i] * inv);
+}
+
+// VectorMath.LayerNorm, VM:342-405 (one workgroup): mean and population
+// variance by block sums, then w (x - mean) invStd, plus the bias when given
+// (the vector lanes and the tail round alike).
+__global__ __launch_bounds__(WG_BIG) void layernorm_kernel(const float* in, const float* w, const float* b, float* out,
+                                                           int n, float eps) {
+    __shared__ float red[16];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n; i += WG_BIG) s += in[i];
+    const float mean = (block_sum<WG_BIG>(s, red) / (float)n);
+    float v = 0.f;
+    for (int i = threadIdx.x; i < n; i += WG_BIG) {
+        const float d = (in[i] - mean);
+        v += (d * d);
+    }
+    const float var = (block_sum<WG_BIG>(v, red) / (float)n);
+    const float inv = (1.0f / sqrtf((var + eps)));
+    for (int i = threadIdx.x; i < n; i += WG_BIG) {
+        const float val = ((w[i] * (in[i] - mean)) * inv);
+        out[i] = b ? (val + b[i]) : val;
+    }
+}
+
+// GELU constants of VM:170 and VM:178-180.
+constexpr float GELU_C = 0.7978845608028654f, GELU_C3 = 0.044715f;
+
+// VectorMath.Gelu, VM:169-193: the vector lanes take TanhApproxVector of
+// x c (1 + c3 x x x), grouped as the reference writes it; the tail (and the
+// scalar GeluScalar, a one-element call) 0.5 x (1 + tanh(c (x + c3 x x x))).
+__global__ void gelu_kernel(const float* in, float* out, int n) {
+    const int n8 = n & ~7;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float x = in[i];
+        const float x3 = (((GELU_C3 * x) * x) * x);
+        out[i] = i < n8 ? ((0.5f * x) * (1.0f + tanh_approx(((x * GELU_C) * (1.0f + x3)))))
+                        : ((0.5f * x) * (1.0f + tanhf((GELU_C * (x + x3)))));
+    }
+}
+
+// VectorMath.Softcap, VM:286-302, in place.
+__global__ void softcap_kernel(float* x, int n, float cap) {
+    const int n8 = n & ~7;
+    const float inv_cap = (1.0f / cap);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        x[i] = i < n8 ? (cap * tanh_approx((x[i] * inv_cap))) : (cap * tanhf((x[i] / cap)));
+}
+
+// TensorOps.Conv1D, TO:745-775: one thread per channel over its kernelSize
+// taps in the reference's order (8 lane sums, their horizontal sum as
+// Vector.Dot forms it, then the tail), so the result is bit-exact.
+__global__ void conv1d_kernel(const float* in, const float* w, float* out, int ks, int dim) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= dim) return;
+    const float* x = in + (int64_t)c * ks;
+    const float* y = w + (int64_t)c * ks;
+    if (ks == 1) {
+        out[c] = (x[0] * y[0]);
+        return;
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int k = 0;
+    for (; k <= ks - 8; k += 8)
+#pragma unroll
+        for (int l = 0; l < 8; l++) acc[l] = (acc[l] + (x[k + l] * y[k + l]));
+    float s = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])));
+    for (; k < ks; k++) s = (s + (x[k] * y[k]));
+    out[c] = s;
 }
 
 // VectorMath.Silu / SiluInPlace, VM:99-135.
@@ -233,6 +301,31 @@ hipError_t launch_softmax(float* x, int n, int has_softcap, float cap, hipStream
     softmax_kernel<<<1, WG_BIG, 0, s>>>(x, n, has_softcap, cap);
     return hipGetLastError();
 }
+hipError_t launch_layernorm(const float* in, const float* w, const float* b, float* out, int n, float eps,
+                            hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    layernorm_kernel<<<1, WG_BIG, 0, s>>>(in, w, b, out, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu(const float* in, float* out, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    gelu_kernel<<<grid_for(n, WG), WG, 0, s>>>(in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_softcap(float* x, int n, float cap, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    softcap_kernel<<<grid_for(n, WG), WG, 0, s>>>(x, n, cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv1d(const float* in, const float* w, float* out, int kernel_size, int input_dim, hipStream_t s) {
+    if (input_dim <= 0) return hipSuccess;
+    conv1d_kernel<<<(input_dim + WG - 1) / WG, WG, 0, s>>>(in, w, out, kernel_size, input_dim);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu(const float* in, float* out, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     silu_kernel<<<grid_for(n, WG), WG, 0, s>>>(in, out, n);

@@ -106,6 +106,19 @@ int32_t llmdot_hip_softmax(llmdot_hip_ctx* ctx, float* input, int32_t n, int32_t
                            float softcap);
 /* ICB:16 Silu(input, result) and ICB:17 SiluInPlace(input) (pass input == result). */
 int32_t llmdot_hip_silu(llmdot_hip_ctx* ctx, const float* input, float* result, int32_t n);
+/* ICB:12 LayerNorm(input, weights, bias, output, epsilon); bias_or_null NULL is
+ * the reference's empty bias span. */
+int32_t llmdot_hip_layer_norm(llmdot_hip_ctx* ctx, const float* input, const float* weights,
+                              const float* bias_or_null, float* output, int32_t n, float epsilon);
+/* ICB:18 Gelu(input, result); ICB:19 GeluScalar(x) is the one-element call
+ * (a single element takes the scalar form, as in VectorMath.Gelu). */
+int32_t llmdot_hip_gelu(llmdot_hip_ctx* ctx, const float* input, float* result, int32_t n);
+/* ICB:25 Softcap(input, cap) in place. */
+int32_t llmdot_hip_softcap(llmdot_hip_ctx* ctx, float* input, int32_t n, float cap);
+/* ICB:26 Conv1D(input, weights, output, kernelSize, inputDim): input and
+ * weights are [input_dim][kernel_size], output [input_dim]; bit-exact. */
+int32_t llmdot_hip_conv1d(llmdot_hip_ctx* ctx, const float* input, const float* weights, float* output,
+                          int32_t kernel_size, int32_t input_dim);
 /* ICB:20 Add(a, b) in place (result == a) and ICB:21 Add(a, b, result). */
 int32_t llmdot_hip_add(llmdot_hip_ctx* ctx, const float* a, const float* b, float* result, int32_t n);
 /* ICB:22/23 Scale(input, scale[, result]) */

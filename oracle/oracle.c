@@ -760,6 +760,83 @@ static float tanh_approx(float x) {
     return approx;
 }
 
+/* The GELU constants of VM:170 / VM:178-180: sqrt(2/pi) and the cubic term. */
+#define GELU_C 0.7978845608028654f
+#define GELU_C3 0.044715f
+
+/* VectorMath.Gelu(float), VM:169-170 (CpuBackend.GeluScalar): the libm tanh. */
+float orc_gelu_scalar(float x) {
+    return 0.5f * x * (1.0f + tanhf(GELU_C * (x + GELU_C3 * x * x * x)));
+}
+
+/* VectorMath.Gelu(input, result), VM:172-193: the vector lanes take
+ * TanhApproxVector of x*c*(1 + c3*x*x*x) (grouped as written there: x^3, not
+ * GELU's x^2, inside the bracket), the tail the scalar form.  Parity
+ * unpinned for the vector lanes away from x in {0, 1} and the clamp: no
+ * reference output or independent form fixes the x^3 term. */
+void orc_gelu(const float* in, float* out, int n) {
+    int i = 0;
+    for (; i <= n - VEC; i += VEC)
+        for (int l = 0; l < VEC; l++) {
+            const float x = in[i + l];
+            const float t = tanh_approx(x * GELU_C * (1.0f + GELU_C3 * x * x * x));
+            out[i + l] = 0.5f * x * (1.0f + t);
+        }
+    for (; i < n; i++) out[i] = orc_gelu_scalar(in[i]);
+}
+
+/* VectorMath.Softcap, VM:286-302, in place: cap * tanh(x / cap), the vector
+ * lanes through TanhApproxVector(x * (1/cap)). */
+void orc_softcap(float* x, int n, float cap) {
+    const float inv = 1.0f / cap;
+    int i = 0;
+    for (; i <= n - VEC; i += VEC)
+        for (int l = 0; l < VEC; l++) x[i + l] = cap * tanh_approx(x[i + l] * inv);
+    for (; i < n; i++) x[i] = cap * tanhf(x[i] / cap);
+}
+
+/* VectorMath.LayerNorm, VM:342-405: mean and variance as lane sums (lanes,
+ * horizontal sum, tail), then w * (x - mean) * invStd (+ bias).  bias NULL is
+ * the reference's empty bias span. */
+void orc_layer_norm(const float* in, const float* w, const float* b, float* out, int n, float eps) {
+    float mean = lane_sum(in, n);
+    mean /= (float)n;
+    float* sq = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    for (int e = 0; e < n; e++) {
+        const float d = in[e] - mean;
+        sq[e] = d * d;
+    }
+    float variance = lane_sum(sq, n);
+    free(sq);
+    variance /= (float)n;
+    const float invStd = 1.0f / sqrtf(variance + eps);
+    for (int i = 0; i < n; i++) {
+        const float val = w[i] * (in[i] - mean) * invStd;
+        out[i] = b ? val + b[i] : val;
+    }
+}
+
+/* TensorOps.Conv1D, TO:745-775: input and weights are [inputDim][kernelSize];
+ * kernelSize 1 is the elementwise product, otherwise each channel's dot in
+ * lanes, horizontal sum, then the tail. */
+void orc_conv1d(const float* in, const float* w, float* out, int ks, int dim) {
+    if (ks == 1) {
+        for (int i = 0; i < dim; i++) out[i] = in[i] * w[i];
+        return;
+    }
+    for (int c = 0; c < dim; c++) {
+        const float* x = in + (size_t)c * ks;
+        const float* y = w + (size_t)c * ks;
+        float acc[VEC] = {0};
+        int k = 0;
+        for (; k <= ks - VEC; k += VEC)
+            for (int l = 0; l < VEC; l++) acc[l] = acc[l] + x[k + l] * y[k + l];
+        float sum = hsum8(acc);
+        for (; k < ks; k++) sum += x[k] * y[k];
+        out[c] = sum;
+    }
+}
+
 /* FindMax, VM:260-284 */
 static float find_max(const float* in, int n) {
     if (n >= VEC) {

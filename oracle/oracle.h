@@ -62,6 +62,13 @@ void orc_matmul_f32(const float* a, const float* b, float* result, int result_le
 void orc_rms_norm(const float* in, const float* w, float* out, int n, float eps); /* VM:308-340 */
 void orc_softmax(float* x, int n, int has_softcap, float softcap);           /* VM:215-258 */
 void orc_silu(const float* in, float* out, int n);            /* VM:99-116 */
+float orc_gelu_scalar(float x);                                /* VM:169-170 */
+void orc_gelu(const float* in, float* out, int n);            /* VM:172-193; vector lanes: parity unpinned */
+void orc_softcap(float* x, int n, float cap);                 /* VM:286-302 */
+void orc_layer_norm(const float* in, const float* w, const float* b, float* out,
+                    int n, float eps);                        /* VM:342-405 */
+void orc_conv1d(const float* in, const float* w, float* out, int kernel_size,
+                int input_dim);                               /* TO:745-775 */
 void orc_silu_inplace(float* x, int n);                       /* VM:118-135 */
 void orc_add_inplace(float* a, const float* b, int n);        /* VM:27-42 */
 void orc_add(const float* a, const float* b, float* out, int n);   /* VM:10-25 */

@@ -43,6 +43,11 @@ _SIG = {
     "orc_rms_norm": ([_P, _P, _P, _I, _F], None),
     "orc_softmax": ([_P, _I, _I, _F], None),
     "orc_silu": ([_P, _P, _I], None),
+    "orc_gelu_scalar": ([_F], _F),
+    "orc_gelu": ([_P, _P, _I], None),
+    "orc_softcap": ([_P, _I, _F], None),
+    "orc_layer_norm": ([_P, _P, _P, _P, _I, _F], None),
+    "orc_conv1d": ([_P, _P, _P, _I, _I], None),
     "orc_silu_inplace": ([_P, _I], None),
     "orc_add_inplace": ([_P, _P, _I], None),
     "orc_add": ([_P, _P, _P, _I], None),
@@ -183,6 +188,45 @@ def silu(x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.zeros_like(x)
     lib().orc_silu(_p(x), _p(out), x.size)
+    return out
+
+
+def gelu_scalar(x):
+    """VectorMath.Gelu(float), VM:169-170."""
+    return float(lib().orc_gelu_scalar(float(x)))
+
+
+def gelu(x):
+    """VectorMath.Gelu(input, result), VM:172-193."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros_like(x)
+    lib().orc_gelu(_p(x), _p(out), x.size)
+    return out
+
+
+def softcap(x, cap):
+    """VectorMath.Softcap, VM:286-302 (returns the capped copy)."""
+    x = np.array(x, dtype=np.float32)
+    lib().orc_softcap(_p(x), x.size, float(cap))
+    return x
+
+
+def layer_norm(x, w, b, eps):
+    """VectorMath.LayerNorm, VM:342-405; b None is the empty bias span."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.zeros_like(x)
+    bp = None if b is None else _p(np.ascontiguousarray(b, dtype=np.float32))
+    lib().orc_layer_norm(_p(x), _p(w), bp, _p(out), x.size, float(eps))
+    return out
+
+
+def conv1d(x, w, kernel_size, input_dim):
+    """TensorOps.Conv1D, TO:745-775: x and w are [input_dim][kernel_size]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.zeros(input_dim, dtype=np.float32)
+    lib().orc_conv1d(_p(x), _p(w), _p(out), int(kernel_size), int(input_dim))
     return out
 
 

@@ -20,7 +20,7 @@ def declared_functions():
 def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     names = declared_functions()
-    assert len(names) == 46
+    assert len(names) == 50
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) - {"llmdot_hip_last_error"} == set(_lib.SIGNATURES)

@@ -53,7 +53,7 @@ def test_native_declares_every_c_function():
     found = {m.group(1): _params(m.group(2))
              for m in re.finditer(r"static extern \w+ (llmdot_hip_\w+)\(([^)]*)\);", decl)}
     want = header_functions()
-    assert len(want) == 46
+    assert len(want) == 50
     assert found == want
 
 
