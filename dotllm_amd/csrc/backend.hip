@@ -953,23 +953,28 @@ int enqueue_step(llmdot_hip_model* m) {
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
         // Q, K, V projections over RmsNorm(h) (IE:185-186, IE:333-353) in one launch when the
-        // types allow (one type, or the Q4_K_M mix of Q4_K and Q6_K), else one per type.
+        // types allow (one type, or Q4_K or Q8_0 mixed with Q6_K, as the Q4_K_M and
+        // Q6_K/Q8_0 mixes give), else one per type.
         const Weight* mats[3] = {w.q, w.k, w.v};
         float* outs[3] = {m->q, m->k, m->v};
         int rows[3] = {qdim, kvdim, kvdim};
-        bool mixed_ok = true, any_q4k = false;
+        uint32_t prim = 0;   // the one type other than Q6_K, if Q4_K or Q8_0
+        bool mixed_ok = true;
         for (int i = 0; i < 3; i++) {
-            mixed_ok = mixed_ok && (mats[i]->type == GGML_Q4_K || mats[i]->type == GGML_Q6_K);
-            any_q4k = any_q4k || mats[i]->type == GGML_Q4_K;
+            const uint32_t t = mats[i]->type;
+            if (t == GGML_Q6_K) continue;
+            mixed_ok = mixed_ok && (t == GGML_Q4_K || t == GGML_Q8_0) && (prim == 0 || prim == t);
+            prim = t;
         }
+        mixed_ok = mixed_ok && prim != 0;
         bool done[3] = {false, false, false};
         for (int i = 0; i < 3; i++) {
             if (done[i]) continue;
             GemvArgs ga{};
             ga.cols = d.hidden; ga.x = m->xn; ga.ssq = m->xssq; ga.norm = 1;
-            const uint32_t lt = mixed_ok && any_q4k ? (uint32_t)GGML_Q4_K : mats[i]->type;
+            const uint32_t lt = mixed_ok ? prim : mats[i]->type;
             for (int j = i; j < 3; j++)
-                if (!done[j] && (mats[j]->type == mats[i]->type || (mixed_ok && any_q4k))) {
+                if (!done[j] && (mats[j]->type == mats[i]->type || mixed_ok)) {
                     ga.seg[ga.nseg++] = {mats[j]->dev, nullptr, outs[j], rows[j], 0, mats[j]->type};
                     done[j] = true;
                 }
