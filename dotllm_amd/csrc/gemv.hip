@@ -150,6 +150,37 @@ __device__ __forceinline__ void quantize32(const float* v, XQ& q) {
     }
 }
 
+// Q8_0 path: the same 24-bit X as three signed byte digits, X = 65536 d2 +
+// 256 d1 + d0 (X + 0x808080 has the bytes d_p + 128), so v_dot4_i32_i8 takes
+// the int8 weights against each digit plane.
+struct XB {
+    uint32_t pl[4 * XQ_PLANES];   // pl[8p + j]: byte k = digit p of X[4j + k] as a signed int8
+    float s, sum;                 // v ~= s * X;  sum = sum(v)
+};
+
+__device__ __forceinline__ void quantize32_b(const float* v, XB& q) {
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    const float scale = amax > 0.f ? XQ_MAX / amax : 0.f;
+    q.s = amax > 0.f ? amax / XQ_MAX : 0.f;
+    q.sum = sum;
+    uint32_t Y[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {   // as quantize32, with Y = X + 0x808080
+        const float f = v[i] * scale + 12582912.0f;
+        Y[i] = __float_as_uint(f) - (0x4B400000u - 0x808080u);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int b = 0; b < 3; b++)
+            q.pl[8 * b + j] = gather_bytes(Y[4 * j], Y[4 * j + 1], Y[4 * j + 2], Y[4 * j + 3], b) ^ 0x80808080u;
+}
+
 // fp32 path: the unit's 32 activations in its element order, and the sums
 // its offsets need.
 template <int NS>
@@ -163,7 +194,7 @@ struct XF {
 
 struct TQ4K {   // reference Q4_K, 144 B / 256: unit = sub-block g
     // 4 rows per batch keep the kernel near 100 VGPRs (4 wavefronts per SIMD)
-    static constexpr int RB = 4, NS = 1, PRE = 2, DEPTH = 2;
+    static constexpr int RB = 4, PRE = 2, DEPTH = 2;
     // h: the 16-byte block header (d | dmin << 16, then the 96-bit 6-bit
     // (sc, m) stream), one load shared by the block's 8 lanes; q: the
     // sub-block's 16 nibble bytes.
@@ -357,8 +388,8 @@ struct TQ3K {
     }
 };
 
-struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block
-    static constexpr int RB = 4, NS = 1, RUN = 32, PRE = 2, DEPTH = 2;
+struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block; int8 weights on v_dot4_i32_i8
+    static constexpr int RB = 4, PRE = 2, DEPTH = 2;
     struct Raw { RawW<8> Q; uint32_t d; };
     __device__ static int xoff(int u, int) { return u * 32; }
     __device__ static void load(Raw& r, const uint8_t* row, int u) {
@@ -366,18 +397,20 @@ struct TQ8_0 {   // Q8_0, 34 B / 32: unit = block
         r.d = ld_h16_bits(blk);
         r.Q.load(blk + 2);
     }
-    __device__ static float dot(const Raw& r, int, const XF<NS>& x) {
-        float s0 = 0.f, s1 = 0.f;
+    __device__ static float dot(const Raw& r, int, const XB& x) {
+        // S = sum q X exactly in two int32 parts: the top two digits by Horner
+        // (|hi| <= 32 * 128 * (64 * 256 + 128) < 2^27), the low digit apart
+        // (|lo| <= 2^19); S = 256 hi + lo in fp32.
+        int hi = 0, lo = 0;
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-            const uint32_t a = r.Q[j], b = r.Q[j + 1];
+        for (int j = 0; j < 8; j++) hi = __builtin_amdgcn_sdot4((int)r.Q[j], (int)x.pl[16 + j], hi, false);
+        hi <<= 8;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                s0 += x.v[4 * j + k] * sb(a, k);
-                s1 += x.v[4 * j + 4 + k] * sb(b, k);
-            }
-        }
-        return h16(r.d) * (s0 + s1);
+        for (int j = 0; j < 8; j++) hi = __builtin_amdgcn_sdot4((int)r.Q[j], (int)x.pl[8 + j], hi, false);
+#pragma unroll
+        for (int j = 0; j < 8; j++) lo = __builtin_amdgcn_sdot4((int)r.Q[j], (int)x.pl[j], lo, false);
+        const float S = (float)hi * 256.0f + (float)lo;
+        return h16(r.d) * (x.s * S);
     }
 };
 
@@ -584,6 +617,12 @@ __device__ __forceinline__ void run_sums(XF<NS>& x) {
     }
 }
 
+// The activation form a row unit takes: 24-bit nibble planes (Q4_K, sdot8),
+// 24-bit byte planes (Q8_0, sdot4) or fp32 values with run sums.
+template <typename TT> struct ActOf { using type = XF<TT::NS>; static constexpr int kind = 0; };
+template <> struct ActOf<TQ4K> { using type = XQ; static constexpr int kind = 1; };
+template <> struct ActOf<TQ8_0> { using type = XB; static constexpr int kind = 2; };
+
 // One workgroup's rows.  Issue order: the activations, then the first PRE
 // batches of weights; a scheduling barrier keeps the activation arithmetic
 // (quantisation) after those issues, so it overlaps the weight loads.  DEPTH
@@ -599,7 +638,8 @@ template <typename TT, int NB, int HV = 1, typename RowPtr>
 __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, RowPtr&& row_ptr, float (*red_w)[4],
                                           bool own_x = true, uint32_t* xq_s = nullptr, int units = 0) {
     constexpr int RB = TT::RB;
-    constexpr bool INT = std::is_same<TT, TQ4K>::value;
+    constexpr int AK = ActOf<TT>::kind;
+    constexpr bool INT = AK != 0;
     static_assert(HV == 1 || INT, "shared activations are quantised ones");
     const int lane = threadIdx.x & 63;
     XRaw xr;
@@ -620,9 +660,12 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int uu, bool has, R
     for (int k = TT::PRE; k < NB && k < D; k++)
 #pragma unroll
         for (int i = 0; i < RB; i++) TT::load(buf[k][i], row_ptr(k * RB + i), uu);
-    typename std::conditional<INT, XQ, XF<INT ? 1 : TT::NS>>::type x;
+    typename ActOf<TT>::type x;
     if constexpr (INT) {
-        if (own_x) quantize32(v, x);
+        if (own_x) {
+            if constexpr (AK == 1) quantize32(v, x);
+            else quantize32_b(v, x);
+        }
         if constexpr (HV > 1) {
             constexpr int XW = 4 * XQ_PLANES + 2;   // dwords per unit: planes, s, sum
             if (own_x && has) {
