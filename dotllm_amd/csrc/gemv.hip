@@ -1035,10 +1035,10 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     const int rwg1 = gemv_rows_per_wg(type, epi, nb);
     const int hv = gemv_halves(type, epi, a.cols, t2 != type, (rows_total + rwg1 - 1) / rwg1);
     const int rwg = hv * rwg1;
-    // Q6_K segments of a mixed launch: with Q4_K, half the batches per
-    // workgroup (a Q6_K row costs about twice a Q4_K row), so their workgroups
-    // end with the rest; with Q8_0 (a row of about the same cost), as many
-    const int nb2 = type == GGML_Q4_K && nb > 1 ? nb / 2 : nb;
+    // Q6_K segments of a mixed launch: half the batches per workgroup (a Q6_K
+    // row costs about twice a Q4_K or Q8_0 row), so their workgroups end with
+    // the rest
+    const int nb2 = nb > 1 ? nb / 2 : 1;
     const int rwg2 = gemv_rows_per_wg(t2, epi, nb2);
     int grid = 0;
     for (int i = 0; i < a.nseg; i++) {
@@ -1053,9 +1053,9 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
     if (t2 != type && type == GGML_Q8_0) {   // Q8_0 with Q6_K segments (Q/K/V of the Q6_K/Q8_0 mixes)
         switch (nb) {
         case 1: gemv_kernel<GGML_Q8_0, EPI_STORE, 1, true, GGML_Q6_K, 1><<<grid, threads, 0, s>>>(a); break;
-        case 2: gemv_kernel<GGML_Q8_0, EPI_STORE, 2, true, GGML_Q6_K, 2><<<grid, threads, 0, s>>>(a); break;
-        case 4: gemv_kernel<GGML_Q8_0, EPI_STORE, 4, true, GGML_Q6_K, 4><<<grid, threads, 0, s>>>(a); break;
-        case 8: gemv_kernel<GGML_Q8_0, EPI_STORE, 8, true, GGML_Q6_K, 8><<<grid, threads, 0, s>>>(a); break;
+        case 2: gemv_kernel<GGML_Q8_0, EPI_STORE, 2, true, GGML_Q6_K, 1><<<grid, threads, 0, s>>>(a); break;
+        case 4: gemv_kernel<GGML_Q8_0, EPI_STORE, 4, true, GGML_Q6_K, 2><<<grid, threads, 0, s>>>(a); break;
+        case 8: gemv_kernel<GGML_Q8_0, EPI_STORE, 8, true, GGML_Q6_K, 4><<<grid, threads, 0, s>>>(a); break;
         default: return hipErrorInvalidValue;
         }
         return hipGetLastError();
