@@ -164,6 +164,7 @@ def main() -> int:
     from dotllm_amd.engine import InferenceEngine, LoadedModel
 
     spec = synth.SPECS[args.config]
+    ffn_type = {v: k.upper() for k, v in synth.QUANT_NAMES.items()}[synth.tensor_type(spec["mix"], "blk.0.ffn_gate.weight")]
     total_ctx = args.ctx + args.warmup + 2 * args.steps + args.kernel_steps + 8
     t0 = time.perf_counter()
     img = synth.build_image(args.config, seed=args.seed, context=total_ctx)
@@ -253,7 +254,8 @@ def main() -> int:
                    "vocab": spec["vocab"], "context": args.ctx, "batch": 1},
         "step_hbm": {"bytes_per_token": step_bytes, "achieved_gbps": round(step_bytes / ms_step / 1e6, 1),
                      "peak_gbps": HBM_PEAK_GBPS, "frac": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBPS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<Q4_K, SWIGLU, RmsNorm> (ffn gate+up, 14336x4096 x2)",
+        "roofline": {"bound": "hbm",
+                     "kernel": f"gemv_kernel<{ffn_type}, SWIGLU, RmsNorm> (ffn gate+up, {spec['ffn']}x{spec['hidden']} x2)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_note,
                      "bytes_per_launch": per_launch_bytes, "us_per_launch": round(per_launch_ms * 1e3, 2),
