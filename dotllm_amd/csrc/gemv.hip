@@ -940,8 +940,12 @@ bool gemv_width_ok(uint32_t type, int cols) {
     return cols % block_elems(type) == 0 && cols / 32 <= MAXW * 64;
 }
 
-// Wavefronts a launch should have at least (4 per CU: fewer, longer
-// workgroups amortise the activation loads); LLMDOT_GEMV_WAVES overrides it.
+// Wavefronts a launch should have at least: 6 per CU for workgroups of two or
+// more wavefronts, 4 per CU for one-wavefront workgroups (fewer, longer
+// workgroups amortise the activation loads; measured: the Phi-3 Q/K/V and
+// gate/up launches gained 1.9% of the step at 1536, the 7B launches were
+// unchanged, 1B's one-wavefront gate/up lost 0.3%); LLMDOT_GEMV_WAVES
+// overrides both.
 // LLMDOT_GEMV_HALVES=0 keeps one half per workgroup (A/B timing and tests).
 static bool env_halves_off() {
     static const bool off = [] {
@@ -951,13 +955,12 @@ static bool env_halves_off() {
     return off;
 }
 
-static int target_waves() {
+static int target_waves(int nw) {
     static const int w = [] {
         const char* e = getenv("LLMDOT_GEMV_WAVES");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 1024;
+        return e ? atoi(e) : 0;
     }();
-    return w;
+    return w > 0 ? w : (nw > 1 ? 1536 : 1024);
 }
 
 int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
@@ -969,7 +972,7 @@ int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
     // (14336 rows: 1024 workgroups, 4 per CU, instead of 896)
     if (epi == EPI_SWIGLU && rows_total % (7 * opb) == 0 && (rows_total / (7 * opb)) % 256 == 0) return 7;
     int nb = 8;
-    while (nb > 1 && ((rows_total + nb * opb - 1) / (nb * opb)) * nw < target_waves()) nb /= 2;
+    while (nb > 1 && ((rows_total + nb * opb - 1) / (nb * opb)) * nw < target_waves(nw)) nb /= 2;
     // the ADD epilogue packs rows in groups of 8
     while (epi == EPI_ADD && nb < 8 && (nb * opb) % 8) nb *= 2;
     return nb;
