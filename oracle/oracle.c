@@ -771,9 +771,8 @@ float orc_gelu_scalar(float x) {
 
 /* VectorMath.Gelu(input, result), VM:172-193: the vector lanes take
  * TanhApproxVector of x*c*(1 + c3*x*x*x) (grouped as written there: x^3, not
- * GELU's x^2, inside the bracket), the tail the scalar form.  Parity
- * unpinned for the vector lanes away from x in {0, 1} and the clamp: no
- * reference output or independent form fixes the x^3 term. */
+ * GELU's x^2, inside the bracket, so the lanes return x for x <= -4), the
+ * tail the scalar form. */
 void orc_gelu(const float* in, float* out, int n) {
     int i = 0;
     for (; i <= n - VEC; i += VEC)

@@ -63,7 +63,7 @@ void orc_rms_norm(const float* in, const float* w, float* out, int n, float eps)
 void orc_softmax(float* x, int n, int has_softcap, float softcap);           /* VM:215-258 */
 void orc_silu(const float* in, float* out, int n);            /* VM:99-116 */
 float orc_gelu_scalar(float x);                                /* VM:169-170 */
-void orc_gelu(const float* in, float* out, int n);            /* VM:172-193; vector lanes: parity unpinned */
+void orc_gelu(const float* in, float* out, int n);            /* VM:172-193 */
 void orc_softcap(float* x, int n, float cap);                 /* VM:286-302 */
 void orc_layer_norm(const float* in, const float* w, const float* b, float* out,
                     int n, float eps);                        /* VM:342-405 */

@@ -114,22 +114,29 @@ def test_gelu_tail_is_the_tanh_formula():
         assert abs(O.gelu_scalar(v) - float(_gelu64(v))) <= 4e-7 * max(1.0, abs(v))
 
 
-def test_gelu_vector_lanes_where_pinned():
-    """The vector lanes (VM:183-187) take TanhApproxVector of the argument as
-    written there, x c (1 + c3 x x x), which is not GELU's c (x + c3 x^3)
-    except at x = 0 and x = 1.  Pinned: x = 0 gives exactly 0; at x = 1 the
-    lane is 0.5 (1 + P(c (1 + c3))), within 0.5 * 0.0236 (the Pade form's
-    largest distance from tanh on [-4, 4], see the softcap test) of GELU(1);
-    for x >= 8 the argument is past 4 and the clamp gives exactly x.  The x^3
-    term elsewhere is restated as written with no independent check (parity
-    unpinned there); it puts the lanes up to 0.13 away from GELU near x = -1.9
-    and returns x (not 0) for large negative x."""
+def test_gelu_vector_lanes():
+    """The vector lanes (VM:183-187) take TanhApproxVector (the Pade form and
+    its clamp to exactly +-1 past |4|, pinned by the softcap test) of the
+    argument as written there, x c (1 + c3 x x x) -- not GELU's c (x + c3 x^3).
+    Pinned independently of the oracle's expression:
+      * x = 0 gives exactly 0, and x >= 8 exactly x (argument past the clamp);
+      * x <= -4 gives exactly x: 1 + c3 x^3 < 0 there, so the argument is
+        positive and past the clamp.  GELU's x^2 form, a dropped cubic term or
+        a flipped sign all give exactly 0 instead (negative argument);
+      * at x = 1 (where x^3 = x^2) the lane is within 0.5 * 0.0236 of GELU(1),
+        fixing c and c3 to the Pade bound; the tail test fixes them exactly,
+        and the oracle shares the constants between the two forms."""
     x = np.array([0, 1, 8, 10, 20, 50, 1, 0], np.float32)
     g = O.gelu(x)
     assert g[0] == 0.0 and g[7] == 0.0
     assert abs(float(g[1]) - float(_gelu64(1.0))) <= 0.5 * 0.0236
     assert g[1] == g[6]
     assert np.array_equal(g[2:6], x[2:6])
+    neg = np.array([-4, -5, -6, -8, -10, -20, -50, -100], np.float32)
+    assert np.array_equal(O.gelu(neg), neg)
+    # the same values on the scalar tail are GELU's (about 0 for x <= -4)
+    tail = O.gelu(neg[:4])
+    assert np.all(np.abs(tail) < 1e-3)
 
 
 def test_softcap_tail_and_lanes():
