@@ -550,7 +550,7 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(AttnArgs a) {
     const int nch = (n + CHP - 1) / CHP;
     const int hq = blockIdx.x, g = threadIdx.x / HD, d = threadIdx.x - g * HD;
     float acc = 0.f, z = 0.f;
-#pragma unroll 4
+#pragma unroll 8
     for (int i = g; i < nch; i += NG) {
         acc += a.part_out[((int64_t)i * a.heads + hq) * HD + d];
         z += a.part_sum[(int64_t)i * a.heads + hq];
