@@ -83,12 +83,15 @@ def _run(hip, key):
             forced.append(_err(row, z, s))
             if int(np.argmax(row)) != ref[s] and not tie[s]:
                 flips.append(s)
-        kv_err, kv_bound = [], []
+        kv_err, kv_bound, kv_mag = [], [], []
         for i, layer in enumerate(z["kv_layers"]):
             for j, pos in enumerate(z["kv_positions"]):
                 k, v = eng.kv_read(int(layer), int(pos))
                 kv_err.append(max(float(np.max(np.abs(k - z["k"][i, j]))), float(np.max(np.abs(v - z["v"][i, j])))))
                 kv_bound.append(max(KV_TOL, 2 * float(z["k_floor"][i, j]), 2 * float(z["v_floor"][i, j])))
+                dk, dv = np.abs(k - z["k"][i, j]), np.abs(v - z["v"][i, j])
+                at = (z["k"][i, j], int(np.argmax(dk))) if dk.max() >= dv.max() else (z["v"][i, j], int(np.argmax(dv)))
+                kv_mag.append((int(layer), int(pos), float(at[0][at[1]])))
     finally:
         eng.dispose()
     forced, free = np.asarray(forced), np.asarray(free)
@@ -102,7 +105,8 @@ def _run(hip, key):
     assert np.all(free <= bound[:len(free)])
     assert np.all(forced <= bound), [(s, forced[s], bound[s]) for s in np.where(forced > bound)[0][:5]]
     assert not flips, flips
-    assert all(e <= b for e, b in zip(kv_err, kv_bound)), list(zip(kv_err, kv_bound))
+    assert all(e <= b for e, b in zip(kv_err, kv_bound)), [
+        (i, e, b, kv_mag[i]) for i, (e, b) in enumerate(zip(kv_err, kv_bound)) if e > b]
 
 
 def test_c3_llama1b_512_prompt_256_tokens(hip):
