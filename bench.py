@@ -150,7 +150,7 @@ def main() -> int:
                     help="other full-size workloads timed after the headline run (prefill + decode); '' for none")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernel by kernel instead of replaying the captured HIP graph "
-                         "(rocprofv3 cannot trace graph launches on this image)")
+                         "(the committed rocprofv3 summaries are of eager runs, one record per kernel)")
     args = ap.parse_args()
     if args.eager:
         os.environ["LLMDOT_HIP_NO_GRAPH"] = "1"
