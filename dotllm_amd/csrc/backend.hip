@@ -120,10 +120,26 @@ int ensure_device(llmdot_hip_ctx* ctx) {
     return 0;
 }
 
+// Fresh device memory is zeroed, and host bytes are copied in, on the context
+// stream, which is then waited for.  A plain hipMemset / hipMemcpy runs on the
+// null stream, which the context stream (created non-blocking) and the side
+// streams forked from it do not wait for: work enqueued right after could read
+// or write the buffer before the zeros or the bytes land.
+int zero_fresh(llmdot_hip_ctx* ctx, void* p, size_t n) {
+    HIPCHK(hipMemsetAsync(p, 0, n, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+int copy_in(llmdot_hip_ctx* ctx, void* dst, const void* src, size_t n) {
+    HIPCHK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
 int ensure_argmax(llmdot_hip_ctx* ctx, int n) {
     if (!ctx->am_ints) {
         HIPCHK(hipMalloc(&ctx->am_ints, 64));
-        HIPCHK(hipMemset(ctx->am_ints, 0, 64));
+        if (int rc = zero_fresh(ctx, ctx->am_ints, 64)) return rc;
     }
     if (n > ctx->am_cap) {
         if (ctx->am_val) (void)hipFree(ctx->am_val);
@@ -152,7 +168,7 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
             if (old.type != type || old.rows != rows || old.cols != cols)
                 return fail(LLMDOT_E_INVALID, "weight '" + key + "' is in use by a model with another shape or type");
             HIPCHK(hipStreamSynchronize(ctx->stream));
-            HIPCHK(hipMemcpy(old.dev, bytes, (size_t)need, hipMemcpyHostToDevice));
+            if (int rc = copy_in(ctx, old.dev, bytes, (size_t)need)) return rc;
             for (const auto& c : ctx->norm_copies)   // models reading an fp32 copy of this norm
                 if (c.key == key) HIPCHK(launch_dequant(old.dev, c.dst, type, 1, c.n, ctx->stream));
             HIPCHK(hipStreamSynchronize(ctx->stream));
@@ -165,8 +181,8 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
     Weight w;
     w.type = type; w.rows = rows; w.cols = cols; w.nbytes = (size_t)need;
     HIPCHK(hipMalloc(&w.dev, (size_t)need + WEIGHT_PAD));
-    HIPCHK(hipMemcpy(w.dev, bytes, (size_t)need, hipMemcpyHostToDevice));
-    HIPCHK(hipMemset(w.dev + need, 0, WEIGHT_PAD));
+    if (int rc = zero_fresh(ctx, w.dev + need, WEIGHT_PAD)) { (void)hipFree(w.dev); return rc; }
+    if (int rc = copy_in(ctx, w.dev, bytes, (size_t)need)) { (void)hipFree(w.dev); return rc; }
     auto& slot = ctx->weights[key];
     slot = w;
     if (out) *out = &slot;
@@ -703,8 +719,7 @@ extern "C" int32_t llmdot_hip_device_alloc(llmdot_hip_ctx* ctx, size_t nbytes, v
     if (int rc = ensure_device(ctx)) return rc;
     hipError_t e = hipMalloc(dptr, nbytes + WEIGHT_PAD);
     if (e != hipSuccess) return fail(LLMDOT_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
-    HIPCHK(hipMemset(*dptr, 0, nbytes + WEIGHT_PAD));
-    return 0;
+    return zero_fresh(ctx, *dptr, nbytes + WEIGHT_PAD);
 }
 extern "C" int32_t llmdot_hip_device_free(llmdot_hip_ctx* ctx, void* dptr) {
     if (!ctx) return fail(LLMDOT_E_INVALID, "null ctx");
@@ -866,8 +881,7 @@ int dalloc(llmdot_hip_model* m, size_t n, void** p) {
     hipError_t e = hipMalloc(p, n + WEIGHT_PAD);
     if (e != hipSuccess) return fail(LLMDOT_E_NOMEM, "device allocation of " + std::to_string(n) + " bytes failed: " + hipGetErrorString(e));
     m->owned.push_back(*p);
-    HIPCHK(hipMemset(*p, 0, n + WEIGHT_PAD));
-    return 0;
+    return zero_fresh(m->ctx, *p, n + WEIGHT_PAD);
 }
 
 // A context weight the model reads; it stays pinned (no release, no
@@ -1290,9 +1304,8 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
         void *pc, *ps;
         if ((rc = dalloc(m, n * sizeof(float), &pc)) || (rc = dalloc(m, n * sizeof(float), &ps))) return bail(rc);
         m->cos_tab = (float*)pc; m->sin_tab = (float*)ps;
-        if (hipMemcpy(pc, cs.data(), n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemcpy(ps, sn.data(), n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
-            return bail(fail(LLMDOT_E_DEVICE, "RoPE table upload failed"));
+        if ((rc = copy_in(ctx, pc, cs.data(), n * sizeof(float))) || (rc = copy_in(ctx, ps, sn.data(), n * sizeof(float))))
+            return bail(rc);
     }
     void* p;
     auto A = [&](size_t n, void** dst) { return dalloc(m, n, dst); };
