@@ -231,13 +231,14 @@ __device__ __forceinline__ void lds_bytes8(const unsigned char* p, int o, uint32
 }
 
 // K-quant B fragment: elements 8 lk .. 8 lk + 7 of group g for the row whose
-// header (16 bytes) is at hdr and whose quant chunk(s) start at qs (next chunk
-// 2048 bytes further): fp16 sc * (q - 8|16), exact.
+// header words 1..3 (bytes 4..15, the packed scales) are hw and whose quant
+// chunk(s) start at qs (next chunk 2048 bytes further): fp16 sc * (q - 8|16),
+// exact.  The header comes from registers: an 8-byte LDS read of it would sit
+// at a 4-byte-aligned address for 5 of the 8 groups, which the LDS serves an
+// order of magnitude slower than an aligned one.
 template <uint32_t FMT>
-__device__ __forceinline__ h8 kq_frag(const unsigned char* hdr, const unsigned char* qs, int g, int lk) {
-    const int b = 12 * g;   // scale field bit offset in bytes 4..15 (wave-uniform)
-    const uint2 fw = *reinterpret_cast<const uint2*>(hdr + 4 + 4 * (b >> 5));
-    const _Float16 sc = (_Float16)(float)(__builtin_amdgcn_alignbit(fw.y, fw.x, (uint32_t)(b & 31)) & 63u);
+__device__ __forceinline__ h8 kq_frag(v4u hw, const unsigned char* qs, int g, int lk) {
+    const _Float16 sc = (_Float16)(float)(k_field12(hw[1], hw[2], hw[3], 12 * g) & 63u);
     const uint32_t w = reinterpret_cast<const uint32_t*>(qs)[lk];
     const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
     uint32_t n0 = perm(hi, lo, 0x05010400u), n1 = perm(hi, lo, 0x07030602u);
@@ -325,9 +326,11 @@ __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" :
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // LDS rows of 32 halves (64 bytes) hold 4 chunks of 8; chunk c of row r sits
-// at position c ^ swz(r), which spreads an MFMA fragment read (16 rows x 4
-// chunks) over distinct banks whether the LDS serves 16 or 32 lanes of a
-// 16-byte read per cycle.  swz(16 i + l) = swz(l) ^ 2 (i & 1).
+// at position c ^ swz(r).  swz(16 i + l) = swz(l) ^ 2 (i & 1).  An MFMA
+// fragment read (16 rows x 4 chunks) still takes two passes of the LDS (as
+// does the unswizzled [row][chunk] order); the conflict-free order, chunk-major
+// per 16-row tile, makes the global -> LDS copies slower by more than it saves
+// (a lane quad no longer covers one token's 64 contiguous bytes).
 __device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ r ^ ((r >> 3) & 2)) & 3; }
 
 template <uint32_t FMT, int EPI>
@@ -435,6 +438,9 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     for (int i = 0; i < TI; i++)
 #pragma unroll
         for (int j = 0; j < TJ; j++) acc[i][j] = cs[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    v4u hdr[TJ];   // K-quants: the current superblock's 16-byte header per weight row
+#pragma unroll
+    for (int j = 0; j < TJ; j++) hdr[j] = v4u{0u, 0u, 0u, 0u};
 
     issue(0);
     if (NS == 3 && nsteps > 1) issue(1);
@@ -452,11 +458,19 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         const unsigned char* raw = sb + XS1;
         h8 wf[TJ][NP];
         float d[TJ];
+        if constexpr (F::KQ) {
+            // the 16-byte header (d, dmin, packed scales) of the superblock, read
+            // aligned once at its first step (every step's stage holds a copy)
+            if ((st & 7) == 0) {
+#pragma unroll
+                for (int tj = 0; tj < TJ; tj++) hdr[tj] = *reinterpret_cast<const v4u*>(raw + rw[tj] * 16);
+            }
+        }
 #pragma unroll
         for (int tj = 0; tj < TJ; tj++) {
             if constexpr (F::KQ) {
-                wf[tj][0] = kq_frag<FMT>(raw + rw[tj] * 16, raw + 2048 + rw[tj] * 16, st & 7, lk);
-                d[tj] = (float)*reinterpret_cast<const _Float16*>(raw + rw[tj] * 16);
+                wf[tj][0] = kq_frag<FMT>(hdr[tj], raw + 2048 + rw[tj] * 16, st & 7, lk);
+                d[tj] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr[tj][0] & 0xFFFFu));
             } else {
                 win_frag<FMT>(raw + rw[tj] * R * 16, st, lk, frow[tj], wf[tj], &d[tj]);
             }
@@ -499,7 +513,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
                 const int sp = (st >> 3) & 1;
 #pragma unroll
                 for (int tj = 0; tj < TJ; tj++) {
-                    const uint32_t* hw = reinterpret_cast<const uint32_t*>(raw + rw[tj] * 16);
+                    const v4u hw = hdr[tj];
                     const float dm = 32.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(hw[0] >> 16));
                     h4 mq = h4{0, 0, 0, 0};
                     if (lk < 2) {
