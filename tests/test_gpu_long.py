@@ -17,6 +17,9 @@ decodes with the captured step.  Bars, per step s:
   * greedy tokens identical up to the oracle's first step whose top-2 gap is
     below max(1e-2, 4 floor(s)) (a near-tie at that error);
   * the same argmax, teacher-forced, wherever the gap is at least that;
+  * the fresh engine's first prefill (inside generate_all: workspace allocated
+    and zeroed just before) and the re-run after reset give bit-identical
+    last-token logits (both runs are deterministic);
   * the KV rows of the sampled (layer, position) pairs within
     max(1e-3, 2 floor_kv) (floor_kv: how far the same order change moves the
     oracle's row; a single sample has no running maximum to lean on, and the
@@ -73,10 +76,14 @@ def _run(hip, key):
         toks, logits = eng.generate_all(prompt, greedy(n_gen), return_logits=True)
         same = next((i for i, (a, b) in enumerate(zip(toks, ref)) if a != b), n_gen)
         free = [_err(logits[s], z, s) for s in range(min(well_posed + 1, n_gen))]
+        first_free = np.array(logits[0], copy=True)   # the fresh engine's first prefill
         del logits
         eng.reset()
         forced, flips = [], []
         row, _ = eng.prefill(prompt, 0)
+        # the same prompt again on the now warm engine: no allocation, same kernels,
+        # so the logits must agree bit for bit with the first (cold) prefill
+        cold_warm_same = np.array_equal(first_free, row)
         for s in range(n_gen):
             if s > 0:
                 row = eng.process_token(ref[s - 1], n_prompt + s - 1)
@@ -101,6 +108,7 @@ def _run(hip, key):
           f"{free.max():.3e}, teacher-forced max {forced.max():.3e} at step {int(forced.argmax())} "
           f"(bound there {bound[int(forced.argmax())]:.3e}, largest error/bound {ratio.max():.2f}, "
           f"floor max {z['floor'].max():.3e}); KV error max {max(kv_err):.3e} (bound {max(kv_bound):.3e})")
+    assert cold_warm_same, "the first prefill of a fresh engine differs from the warm re-run"
     assert same >= well_posed
     assert np.all(free <= bound[:len(free)])
     assert np.all(forced <= bound), [(s, forced[s], bound[s]) for s in np.where(forced > bound)[0][:5]]
