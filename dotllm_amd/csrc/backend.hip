@@ -207,6 +207,9 @@ constexpr size_t NOALLOC_CAND_IDX = NOALLOC_CAND_VAL + 4 * NOALLOC_CAND;   // in
 constexpr size_t NOALLOC_INTS = NOALLOC_CAND_IDX + 4 * NOALLOC_CAND;   // [0] draw counter, [1] draw bits
 constexpr size_t NOALLOC_BYTES = NOALLOC_INTS + 256;                   // 1 MiB + 768 B
 constexpr int NOALLOC_MAX_DEVICES = 64;
+// Elements of each prefill K-part buffer: a split keeps tiles (of 128 x 128)
+// x parts <= 512 (prefill_ksplit).
+constexpr int64_t PF_PARTS_MAX = 512LL * 128 * 128;
 
 __attribute__((used)) __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 
@@ -853,6 +856,9 @@ struct llmdot_hip_model {
     int pf_cap = 0;
     float *pf_h = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_qr = nullptr, *pf_attn = nullptr,
           *pf_act = nullptr, *pf_scores = nullptr, *pf_rowmax = nullptr;
+    // K parts of the narrow projections (prefill_ksplit): Q, then O and down
+    // (in stream order) share one buffer; K and V run at the same time as Q
+    float *pf_parts_q = nullptr, *pf_parts_k = nullptr, *pf_parts_v = nullptr;
     PfPlanes pf_planes{};
     int32_t* pf_tokens = nullptr;
     // sampled generation (allocated on first use): recent-token history
@@ -1112,6 +1118,10 @@ int ensure_prefill_ws(llmdot_hip_model* m) {
     if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_qr = (float*)p;
     if ((rc = A(4 * cap * qdim, &p))) return rc; m->pf_attn = (float*)p;
     if ((rc = A(4 * cap * (size_t)d.ffn, &p))) return rc; m->pf_act = (float*)p;
+    // a K split keeps tiles x parts <= 512, so parts x rows x cols <= 512 x 128 x 128
+    if ((rc = A(4 * PF_PARTS_MAX, &p))) return rc; m->pf_parts_q = (float*)p;
+    if ((rc = A(4 * PF_PARTS_MAX, &p))) return rc; m->pf_parts_k = (float*)p;
+    if ((rc = A(4 * PF_PARTS_MAX, &p))) return rc; m->pf_parts_v = (float*)p;
     if (!d.kv_fp16) {
         if ((rc = A(4 * (size_t)d.heads * cap * (size_t)d.context, &p))) return rc;
         m->pf_scores = (float*)p;
@@ -1135,6 +1145,26 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
     hipStream_t s = m->ctx->stream;
     const int qdim = d.heads * d.head_dim, kvdim = d.kv_heads * d.head_dim;
     const PfPlanes& pl = m->pf_planes;
+    const bool split_ok = !env_flag("LLMDOT_HIP_PF_NO_SPLIT");
+    // A STORE projection [T x N] over K columns, in K parts into `parts` when
+    // the launch has few tiles; returns the part count (1: written to out).
+    auto proj = [&](const Weight* w, int N, int K, float* out, float* parts, hipStream_t st, int* nparts) {
+        int sp = split_ok ? prefill_ksplit(w->type, T, N, K) : 1;
+        if ((int64_t)sp * T * N > PF_PARTS_MAX) sp = 1;
+        *nparts = sp;
+        if (sp == 1) return launch_prefill_gemm(w->type, 0, pl, w->dev, nullptr, T, N, K, out, N, st);
+        return launch_prefill_gemm(w->type, 0, pl, w->dev, nullptr, T, N, K, parts, N, st, sp, (int64_t)T * N);
+    };
+    // h += the [T x hidden] projection: in place, or its K parts then their sum
+    auto proj_add = [&](const Weight* w, int K) {
+        int sp = split_ok ? prefill_ksplit(w->type, T, d.hidden, K) : 1;
+        if ((int64_t)sp * T * d.hidden > PF_PARTS_MAX) sp = 1;
+        if (sp == 1) return launch_prefill_gemm(w->type, 1, pl, w->dev, nullptr, T, d.hidden, K, m->pf_h, d.hidden, s);
+        const int64_t n = (int64_t)T * d.hidden;
+        hipError_t e = launch_prefill_gemm(w->type, 0, pl, w->dev, nullptr, T, d.hidden, K, m->pf_parts_q, d.hidden, s,
+                                           sp, n);
+        return e != hipSuccess ? e : launch_prefill_add_parts(m->pf_h, m->pf_parts_q, sp, n, n, s);
+    };
     HIPCHK(launch_embed_rows(m->embd->dev, m->embd->type, d.hidden, m->pf_tokens, T, m->pf_h, s));
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
@@ -1142,18 +1172,24 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
         // Q, K and V read the same planes and write separate buffers: K and V
         // run on the side streams beside Q (K and V alone fill half the CUs)
         llmdot_hip_ctx* c = m->ctx;
+        int nq = 1, nk = 1, nv = 1;
         HIPCHK(hipEventRecord(c->fork, s));
         HIPCHK(hipStreamWaitEvent(c->side[0], c->fork, 0));
         HIPCHK(hipStreamWaitEvent(c->side[1], c->fork, 0));
-        HIPCHK(launch_prefill_gemm(w.k->type, 0, pl, w.k->dev, nullptr, T, kvdim, d.hidden, m->pf_k, kvdim, c->side[0]));
-        HIPCHK(launch_prefill_gemm(w.v->type, 0, pl, w.v->dev, nullptr, T, kvdim, d.hidden, m->pf_v, kvdim, c->side[1]));
+        HIPCHK(proj(w.k, kvdim, d.hidden, m->pf_k, m->pf_parts_k, c->side[0], &nk));
+        HIPCHK(proj(w.v, kvdim, d.hidden, m->pf_v, m->pf_parts_v, c->side[1], &nv));
         HIPCHK(hipEventRecord(c->join[0], c->side[0]));
         HIPCHK(hipEventRecord(c->join[1], c->side[1]));
-        HIPCHK(launch_prefill_gemm(w.q->type, 0, pl, w.q->dev, nullptr, T, qdim, d.hidden, m->pf_q, qdim, s));
+        HIPCHK(proj(w.q, qdim, d.hidden, m->pf_q, m->pf_parts_q, s, &nq));
         HIPCHK(hipStreamWaitEvent(s, c->join[0], 0));
         HIPCHK(hipStreamWaitEvent(s, c->join[1], 0));
         PfAttnArgs aa{};
-        aa.q = m->pf_q; aa.k = m->pf_k; aa.v = m->pf_v; aa.qr = m->pf_qr;
+        aa.q = nq > 1 ? m->pf_parts_q : m->pf_q;
+        aa.k = nk > 1 ? m->pf_parts_k : m->pf_k;
+        aa.v = nv > 1 ? m->pf_parts_v : m->pf_v;
+        aa.q_split = nq; aa.k_split = nk; aa.v_split = nv;
+        aa.q_part = (int64_t)T * qdim; aa.k_part = (int64_t)T * kvdim; aa.v_part = (int64_t)T * kvdim;
+        aa.qr = m->pf_qr;
         aa.kcache = m->kcache + (size_t)l * m->kv_layer_bytes;
         aa.vcache = m->vcache + (size_t)l * m->kv_layer_bytes;
         aa.cos_tab = m->cos_tab; aa.sin_tab = m->sin_tab;
@@ -1164,11 +1200,11 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
         HIPCHK(launch_prefill_rope_kv(aa, s));
         HIPCHK(launch_prefill_attention(aa, s));
         HIPCHK(launch_prefill_planes(m->pf_attn, T, qdim, nullptr, 0.f, pl, s));
-        HIPCHK(launch_prefill_gemm(w.o->type, 1, pl, w.o->dev, nullptr, T, d.hidden, qdim, m->pf_h, d.hidden, s));
+        HIPCHK(proj_add(w.o, qdim));
         HIPCHK(launch_prefill_planes(m->pf_h, T, d.hidden, w.ffn_norm_f, d.eps, pl, s));
         HIPCHK(launch_prefill_gemm(w.gate->type, 2, pl, w.gate->dev, w.up->dev, T, d.ffn, d.hidden, m->pf_act, d.ffn, s));
         HIPCHK(launch_prefill_planes(m->pf_act, T, d.ffn, nullptr, 0.f, pl, s));
-        HIPCHK(launch_prefill_gemm(w.down->type, 1, pl, w.down->dev, nullptr, T, d.hidden, d.ffn, m->pf_h, d.hidden, s));
+        HIPCHK(proj_add(w.down, d.ffn));
     }
     return 0;
 }

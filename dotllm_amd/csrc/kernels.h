@@ -182,15 +182,29 @@ struct PfAttnArgs {
     float* rowmax;            // [heads][T]
     float* out;               // [T][heads*head_dim]
     int T, pos0, ld_scores, heads, kv_heads, head_dim, rope_half, context, kv_fp16;
+    // q, k and v as sums of q_split (k_split, v_split) K parts, q_part elements apart
+    int q_split, k_split, v_split;
+    int64_t q_part, k_part, v_part;
 };
 bool prefill_gemm_supported(uint32_t type, int cols);
 // Optional RmsNorm (norm_w non-null) of each row of x, then its planes.
 hipError_t launch_prefill_planes(const float* x, int M, int K, const float* norm_w, float eps, const PfPlanes& p,
                                  hipStream_t s);
 // out[M][ldo] (=, += for epi 1, SiLU(gate) * up for epi 2 with w = gate, w2 = up)
-// of the planes times the [N][K] weight blocks, transposed.
+// of the planes times the [N][K] weight blocks, transposed.  ksplit > 1 (STORE
+// only): K in ksplit parts of whole blocks, part p written at out + p * part_stride.
 hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const uint8_t* w, const uint8_t* w2, int M,
-                               int N, int K, float* out, int ldo, hipStream_t s);
+                               int N, int K, float* out, int ldo, hipStream_t s, int ksplit = 1,
+                               int64_t part_stride = 0);
+// K parts for an [M x N x K] prefill GEMM: more than 1 only for launches of
+// fewer than 128 tiles, so that tiles x parts stays within 512 workgroups.
+// (Splitting the 128-tile K/V projections of a 7B-shape 2048-token prompt too
+// moved a deep-layer fp16 KV row one ulp past twice the oracle's reorder
+// floor.)
+int prefill_ksplit(uint32_t type, int M, int N, int K);
+// h[i] += sum over the nparts parts (stride elements apart) of parts[p][i], i < n.
+hipError_t launch_prefill_add_parts(float* h, const float* parts, int nparts, int64_t stride, int64_t n,
+                                    hipStream_t s);
 hipError_t launch_prefill_rope_kv(const PfAttnArgs& a, hipStream_t s);
 hipError_t launch_prefill_attention(const PfAttnArgs& a, hipStream_t s);
 // Embedding rows tokens[0..T) (device ids) into out[T][hidden].

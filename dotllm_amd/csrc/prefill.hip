@@ -149,9 +149,11 @@ struct PfGemmArgs {
     const float* xinv;                   // [M]
     const uint8_t* w;                    // [N][row bytes] GGUF blocks
     const uint8_t* w2;                   // SWIGLU: the up matrix (w = gate)
-    float* out;                          // [M][ldo]
+    float* out;                          // [M][ldo]; K part p (split) at out + p * part_stride
     int M, N, K, ldo;
     int tiles_n;                         // weight-row tiles (128 rows; SWIGLU: 64 gate + 64 up)
+    int ksplit;                          // K parts (STORE only): each a whole number of blocks
+    int64_t part_stride;
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -357,11 +359,14 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     // contiguous tile range [xcd * per, (xcd + 1) * per) in token-tile-major
     // order, so the workgroups resident on one XCD share a token tile and its
     // activation stream stays in that XCD's L2.
-    const int ntm = (a.M + BM - 1) / BM, ntn = a.tiles_n, per = (ntm * ntn + 7) / 8;
+    // With a K split, tile = (part * ntm + token tile) * ntn + row tile: the
+    // workgroups of one XCD still share one token tile and K range.
+    const int ntm = (a.M + BM - 1) / BM, ntn = a.tiles_n, per = (ntm * ntn * a.ksplit + 7) / 8;
     const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-    if (tile >= ntm * ntn) return;
-    const int tn = tile % ntn, m0 = (tile / ntn) * BM;
-    const int K = a.K, nsteps = K / 32;
+    if (tile >= ntm * ntn * a.ksplit) return;
+    const int tn = tile % ntn, m0 = ((tile / ntn) % ntm) * BM, part = tile / (ntn * ntm);
+    const int K = a.K, spp = K / 32 / a.ksplit;   // 32-element steps per part
+    const int st0 = part * spp, st1 = st0 + spp;
     const int64_t rbytes = (int64_t)(K / F::EPB) * F::BSZ;
     auto grow_of = [&](int r) {   // tile row -> weight row (SWIGLU: rows 0..63 gate, 64..127 up)
         const int g = EPI == PF_SWIGLU ? tn * 64 + (r & 63) : tn * BN + r;
@@ -442,18 +447,18 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TJ; j++) hdr[j] = v4u{0u, 0u, 0u, 0u};
 
-    issue(0);
-    if (NS == 3 && nsteps > 1) issue(1);
-    for (int st = 0; st < nsteps; st++) {
+    issue(st0);
+    if (NS == 3 && st0 + 1 < st1) issue(st0 + 1);
+    for (int st = st0; st < st1; st++) {
         // step st's copies are complete once at most the later step's remain
-        if (NS == 3 && st + 1 < nsteps) {
+        if (NS == 3 && st + 1 < st1) {
             if (F::MIN && ((st + 1) & 7) == 0) vm_wait<NX + NW + 1>();
             else vm_wait<NX + NW>();
         } else {
             vm_wait<0>();
         }
         lds_barrier();   // every wave's copies of step st landed; step st - 1's buffers are free
-        if (st + NS - 1 < nsteps) issue(st + NS - 1);
+        if (st + NS - 1 < st1) issue(st + NS - 1);
         const unsigned char* sb = smem + (st % NS) * ST1;
         const unsigned char* raw = sb + XS1;
         h8 wf[TJ][NP];
@@ -591,7 +596,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
                     const int row = tn * BN + wn * 16 * TJ + tj * 16 + lr;
                     if (t < a.M && row < a.N) {
                         const float y = acc[ti][tj][e] * xi[ti][e];
-                        float* o = a.out + (int64_t)t * a.ldo + row;
+                        float* o = a.out + part * a.part_stride + (int64_t)t * a.ldo + row;
                         if (EPI == PF_ADD) {
 #pragma clang fp contract(off)
                             *o = *o + y;
@@ -607,23 +612,50 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
 
 // One workgroup per token of the chunk (position pos0 + t): RoPE on every q
 // head (into qr) and k head, K and V written to their cache slots
-// (IE:362-381, same per-element arithmetic as the decode path).
+// (IE:362-381, same per-element arithmetic as the decode path).  A projection
+// computed in K parts is summed here, parts in order.
+__device__ __forceinline__ float sum_parts(const float* x, int64_t idx, int n, int64_t stride) {
+    float v = x[idx];
+    for (int p = 1; p < n; p++) v += x[p * stride + idx];
+    return v;
+}
+
 __global__ __launch_bounds__(WG) void pf_rope_kv_kernel(PfAttnArgs a) {
     const int t = blockIdx.x, p = a.pos0 + t;
     const int HD = a.head_dim, half = a.rope_half;
     const int qdim = a.heads * HD, kvdim = a.kv_heads * HD;
     const float* cs = a.cos_tab + (int64_t)p * half;
     const float* sn = a.sin_tab + (int64_t)p * half;
+    // element d's rotation partner and the pair's table index
+    auto partner = [&](int d) { return d < half ? d + half : (d < 2 * half ? d - half : d); };
+    auto pidx = [&](int d) { return d < half ? d : (d < 2 * half ? d - half : 0); };
     for (int i = threadIdx.x; i < qdim; i += WG) {
         const int h = i / HD, d = i - h * HD;
-        a.qr[(int64_t)t * qdim + i] = rope_elem(a.q + (int64_t)t * qdim + h * HD, d, half, cs, sn);
+        const int64_t r = (int64_t)t * qdim + h * HD;
+        const float x = sum_parts(a.q, r + d, a.q_split, a.q_part);
+        const float y = sum_parts(a.q, r + partner(d), a.q_split, a.q_part);
+        a.qr[(int64_t)t * qdim + i] = rope_pair(x, y, cs[pidx(d)], sn[pidx(d)], d, half);
     }
     for (int i = threadIdx.x; i < kvdim; i += WG) {
         const int h = i / HD, d = i - h * HD;
+        const int64_t r = (int64_t)t * kvdim + h * HD;
         const int64_t slot = ((int64_t)h * a.context + p) * HD + d;
-        store_kv(a.kcache, slot, rope_elem(a.k + (int64_t)t * kvdim + h * HD, d, half, cs, sn), a.kv_fp16);
-        store_kv(a.vcache, slot, a.v[(int64_t)t * kvdim + i], a.kv_fp16);
+        const float x = sum_parts(a.k, r + d, a.k_split, a.k_part);
+        const float y = sum_parts(a.k, r + partner(d), a.k_split, a.k_part);
+        store_kv(a.kcache, slot, rope_pair(x, y, cs[pidx(d)], sn[pidx(d)], d, half), a.kv_fp16);
+        store_kv(a.vcache, slot, sum_parts(a.v, (int64_t)t * kvdim + i, a.v_split, a.v_part), a.kv_fp16);
     }
+}
+
+// h[i] += parts[0][i] + parts[1][i] + ... (in part order) for i < n: the
+// residual add of an output projection computed in K parts.
+__global__ __launch_bounds__(WG) void pf_add_parts_kernel(float* __restrict__ h, const float* __restrict__ parts,
+                                                          int nparts, int64_t stride, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (i >= n) return;
+    float y = parts[i];
+    for (int p = 1; p < nparts; p++) y += parts[p * stride + i];
+    h[i] += y;
 }
 
 // ------------------------------------------------------------- attention --
@@ -1039,7 +1071,7 @@ __global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
 template <uint32_t FMT>
 hipError_t launch_gemm_fmt(int epi, PfGemmArgs a, hipStream_t s) {
     a.tiles_n = epi == PF_SWIGLU ? (a.N + 63) / 64 : (a.N + BN - 1) / BN;
-    const int tiles = a.tiles_n * ((a.M + BM - 1) / BM);
+    const int tiles = a.tiles_n * ((a.M + BM - 1) / BM) * a.ksplit;
     const dim3 grid(8 * ((tiles + 7) / 8));
     switch (epi) {
     case PF_STORE: pf_gemm_kernel<FMT, PF_STORE><<<grid, WG, 0, s>>>(a); break;
@@ -1081,13 +1113,18 @@ hipError_t launch_prefill_planes(const float* x, int M, int K, const float* norm
 }
 
 hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const uint8_t* w, const uint8_t* w2, int M,
-                               int N, int K, float* out, int ldo, hipStream_t s) {
+                               int N, int K, float* out, int ldo, hipStream_t s, int ksplit, int64_t part_stride) {
     if (M <= 0 || N <= 0 || !prefill_gemm_supported(type, K) || (epi == PF_SWIGLU && !w2) || ldo < N)
+        return hipErrorInvalidValue;
+    // parts of whole blocks (256-element superblocks for the K-quants), STORE only
+    const int gran = block_elems(type) == 256 ? 8 : 1;
+    if (ksplit < 1 || (ksplit > 1 && (epi != PF_STORE || (K / 32) % (ksplit * gran) != 0 ||
+                                      part_stride < (int64_t)(M - 1) * ldo + N)))
         return hipErrorInvalidValue;
     // the kernel addresses activations and weight rows with 32-bit byte offsets
     if ((int64_t)M * K * 2 >= (int64_t)1 << 31 || (int64_t)N * byte_count(type, K) >= ((int64_t)1 << 31) - 65536)
         return hipErrorInvalidValue;
-    PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, w2, out, M, N, K, ldo, 0};
+    PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, w2, out, M, N, K, ldo, 0, ksplit, part_stride};
     switch (type) {
     case GGML_Q4_K: return launch_gemm_fmt<GGML_Q4_K>(epi, a, s);
     case GGML_Q5_K: return launch_gemm_fmt<GGML_Q5_K>(epi, a, s);
@@ -1099,9 +1136,24 @@ hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const 
 }
 
 hipError_t launch_prefill_rope_kv(const PfAttnArgs& a, hipStream_t s) {
-    if (a.T <= 0) return hipErrorInvalidValue;
+    if (a.T <= 0 || a.q_split < 1 || a.k_split < 1 || a.v_split < 1) return hipErrorInvalidValue;
     pf_rope_kv_kernel<<<a.T, WG, 0, s>>>(a);
     return hipGetLastError();
+}
+
+hipError_t launch_prefill_add_parts(float* h, const float* parts, int nparts, int64_t stride, int64_t n, hipStream_t s) {
+    if (n <= 0 || nparts < 1 || stride < n) return hipErrorInvalidValue;
+    pf_add_parts_kernel<<<(unsigned)((n + WG - 1) / WG), WG, 0, s>>>(h, parts, nparts, stride, n);
+    return hipGetLastError();
+}
+
+int prefill_ksplit(uint32_t type, int M, int N, int K) {
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int gran = block_elems(type) == 256 ? 8 : 1;
+    int sp = 1;
+    if (tiles >= 128) return 1;
+    while (sp < 8 && tiles * sp * 2 <= 512 && (K / 32) % (sp * 2 * gran) == 0) sp *= 2;
+    return sp;
 }
 
 hipError_t launch_prefill_attention(const PfAttnArgs& a, hipStream_t s) {
