@@ -149,9 +149,19 @@ def _prompt_check(hip, img, prompt, ctx, kv_fp16, layers, split=None):
 
 @pytest.mark.parametrize("kv_fp16", [True, False])
 def test_prefill_tiny_multi_tile(hip, tiny_image, kv_fp16):
-    """tiny Q8_0, MHA head_dim 64: 200 tokens = 2 token tiles, 4 key tiles."""
+    """tiny Q8_0, MHA head_dim 64: 200 tokens = 2 token tiles, 4 key tiles.
+    Every projection launch has under 128 tiles, so Q, K, V and O run in 8 K
+    parts and down (44 steps) in 4, summed by the next kernel."""
     prompt = synth.prompt(32000, 200, seed=17)
     _prompt_check(hip, tiny_image, prompt, 256, kv_fp16, [0, 3])
+
+
+def test_prefill_tiny_no_split(hip, tiny_image, monkeypatch):
+    """The same prompt with the K split turned off: every projection one
+    launch walking all of K, ragged token and row tiles."""
+    monkeypatch.setenv("LLMDOT_HIP_PF_NO_SPLIT", "1")
+    prompt = synth.prompt(32000, 200, seed=17)
+    _prompt_check(hip, tiny_image, prompt, 256, True, [0, 3])
 
 
 @pytest.mark.parametrize("kv_fp16,split", [(True, None), (False, None), (True, 1500)])
