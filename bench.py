@@ -95,6 +95,8 @@ def prefill_flops(spec: dict, n: int) -> float:
 # The other full-size workloads, measured after the headline run: name ->
 # (model, prompt tokens, KV format).  Decode is timed from the end of the prompt.
 EXTRA = {"c3": ("llama1b", 512, True), "c5": ("phi3mini", 2048, True)}
+# weight mixes of the synthetic models, as named in the workload label
+MIX_LABELS = {"q4_k_m": "Q4_K_M", "q5_k_m": "Q5_K_M", "q8_0": "Q8_0", "phi3": "Q6_K/Q8_0"}
 
 
 def extra_config(be, key: str, seed: int, steps: int) -> dict:
@@ -115,7 +117,7 @@ def extra_config(be, key: str, seed: int, steps: int) -> dict:
         r = eng.time_decode(tok, n, steps)
         dec = 1000.0 * steps / r["total_ms"]
         fl = prefill_flops(spec, n)
-        return {"workload": f"{name}-shape, {n}-token prompt then greedy decode, batch 1, "
+        return {"workload": f"{name}-shape {MIX_LABELS.get(spec['mix'], spec['mix'])}, {n}-token prompt then greedy decode, batch 1, "
                             f"{'fp16' if kv16 else 'fp32'} KV",
                 "prefill_tokens": n, "prefill_ms": round(pf_ms, 3), "prefill_tok_s": round(n / (pf_ms * 1e-3), 1),
                 "prefill_mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
@@ -165,6 +167,7 @@ def main() -> int:
 
     spec = synth.SPECS[args.config]
     ffn_type = {v: k.upper() for k, v in synth.QUANT_NAMES.items()}[synth.tensor_type(spec["mix"], "blk.0.ffn_gate.weight")]
+    mix_label = MIX_LABELS.get(spec["mix"], spec["mix"])
     total_ctx = args.ctx + args.warmup + 2 * args.steps + args.kernel_steps + 8
     t0 = time.perf_counter()
     img = synth.build_image(args.config, seed=args.seed, context=total_ctx)
@@ -246,7 +249,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}-shape Q4_K_M greedy decode, batch 1, context {args.ctx}, fp16 KV",
+        "config": {"workload": f"{args.config}-shape {mix_label} greedy decode, batch 1, context {args.ctx}, fp16 KV",
                    "launch": "eager" if args.eager else "hip-graph",
                    "kv": "random fill" if args.synthetic_kv else "prompt processed on device",
                    "hidden": spec["hidden"], "layers": spec["layers"], "heads": spec["heads"],

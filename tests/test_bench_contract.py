@@ -66,3 +66,12 @@ def test_dominant_kernel_label_follows_the_weights():
     assert labels == {"mistral7b": "Q4_K", "phi3mini": "Q8_0"}
     src = open(os.path.join(ROOT, "bench.py")).read()
     assert "gemv_kernel<{ffn_type}, SWIGLU, RmsNorm>" in src
+
+
+def test_every_synthetic_mix_has_a_workload_label():
+    """The workload label names the model's real weight mix (the Phi-3-mini
+    shape is Q6_K/Q8_0, not Q4_K_M)."""
+    for name, spec in synth.SPECS.items():
+        assert spec["mix"] in bench.MIX_LABELS, name
+    assert bench.MIX_LABELS[synth.SPECS["phi3mini"]["mix"]] == "Q6_K/Q8_0"
+    assert bench.MIX_LABELS[synth.SPECS["mistral7b"]["mix"]] == "Q4_K_M"
