@@ -335,19 +335,23 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // (a lane quad no longer covers one token's 64 contiguous bytes).
 __device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ r ^ ((r >> 3) & 2)) & 3; }
 
-template <uint32_t FMT, int EPI>
+// TM tokens per workgroup: BM, or 64 for launches that would have only 128
+// to 255 tiles of BM (all CUs busy; each output's sum runs in the same order).
+template <uint32_t FMT, int EPI, int TM = BM>
 __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     using F = PfFmt<FMT>;
+    static_assert(TM == BM || (TM == 64 && EPI != PF_SWIGLU), "64-token tiles: STORE and ADD only");
     constexpr int NP = F::NP, R = F::R, NS = F::NS;
-    constexpr int TI = BM / 16, TJ = BN / 16 / 4;    // wave w: all BM tokens x rows 16 TJ w .. +16 TJ - 1
-    constexpr int XS1 = 2 * BM * 64;                 // activation stage: [plane][token][32 halves]
+    constexpr int TI = TM / 16, TJ = BN / 16 / 4;    // wave w: all TM tokens x rows 16 TJ w .. +16 TJ - 1
+    constexpr int XS1 = 2 * TM * 64;                 // activation stage: [plane][token][32 halves]
     constexpr int WS1 = BN * R * 16;                 // raw weight stage
     constexpr int ST1 = XS1 + WS1;
-    constexpr int SS_B = F::MIN ? 2 * 2 * BM * 16 : 0;   // [sb parity][plane][token][8] group sums
+    constexpr int SS_B = F::MIN ? 2 * 2 * TM * 16 : 0;   // [sb parity][plane][token][8] group sums
     constexpr int STAGE_B = NS * ST1 + SS_B;
-    constexpr int EX_B = 2 * BM * (16 * TJ + 1) * 4;     // SWIGLU exchange: [gate wave][token][rows + 1]
+    constexpr int EX_B = 2 * TM * (16 * TJ + 1) * 4;     // SWIGLU exchange: [gate wave][token][rows + 1]
     constexpr int SMEM = STAGE_B > EX_B ? STAGE_B : EX_B;
-    constexpr int NX = 4, NW = R / 2;                // DMA instructions per wave and step
+    constexpr int NX = TM / 32, NW = R / 2;          // DMA instructions per wave and step
+    constexpr int XPI = TM / 16;                     // activation DMA instructions per plane
     __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
     const uint32_t sm = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     unsigned char* const Ss = smem + NS * ST1;
@@ -361,10 +365,10 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     // activation stream stays in that XCD's L2.
     // With a K split, tile = (part * ntm + token tile) * ntn + row tile: the
     // workgroups of one XCD still share one token tile and K range.
-    const int ntm = (a.M + BM - 1) / BM, ntn = a.tiles_n, per = (ntm * ntn * a.ksplit + 7) / 8;
+    const int ntm = (a.M + TM - 1) / TM, ntn = a.tiles_n, per = (ntm * ntn * a.ksplit + 7) / 8;
     const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
     if (tile >= ntm * ntn * a.ksplit) return;
-    const int tn = tile % ntn, m0 = ((tile / ntn) % ntm) * BM, part = tile / (ntn * ntm);
+    const int tn = tile % ntn, m0 = ((tile / ntn) % ntm) * TM, part = tile / (ntn * ntm);
     const int K = a.K, spp = K / 32 / a.ksplit;   // 32-element steps per part
     const int st0 = part * spp, st1 = st0 + spp;
     const int64_t rbytes = (int64_t)(K / F::EPB) * F::BSZ;
@@ -375,13 +379,13 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     auto wsel = [&](int r) -> const uint8_t* { return EPI == PF_SWIGLU && r >= 64 ? a.w2 : a.w; };
 
     // DMA sources.  Activations: instruction i of wave wv covers stage slots
-    // q = (NX wv + i) 64 + lane: plane q >> 9, token (q >> 2) & 127, position
-    // q & 3 holding chunk (q & 3) ^ swz(token).
+    // q = (NX wv + i) 64 + lane: plane q / (4 TM), token (q >> 2) % TM,
+    // position q & 3 holding chunk (q & 3) ^ swz(token).
     uint32_t xoff[NX];
 #pragma unroll
     for (int i = 0; i < NX; i++) {
         const int q = (NX * wv + i) * 64 + lane;
-        const int tk = (q >> 2) & 127, c = (q & 3) ^ swz(tk);
+        const int tk = (q >> 2) & (TM - 1), c = (q & 3) ^ swz(tk);
         xoff[i] = (uint32_t)(((int64_t)min(m0 + tk, a.M - 1) * K + 8 * c) * 2);
     }
     // Weights: K-quants: slot q = ch * 128 + row (ch uniform per instruction);
@@ -396,13 +400,13 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         woff[j] = (uint32_t)wrow[j];
     }
     uint32_t soff = 0;
-    if (F::MIN) soff = (uint32_t)((int64_t)min(m0 + ((wv * 64 + lane) & 127), a.M - 1) * (K / 32) * 2);
+    if (F::MIN) soff = (uint32_t)((int64_t)min(m0 + ((wv * 64 + lane) & (TM - 1)), a.M - 1) * (K / 32) * 2);
 
     auto issue = [&](int st) __attribute__((always_inline)) {
         const uint32_t lb = sm + (uint32_t)((st % NS) * ST1);
 #pragma unroll
         for (int i = 0; i < NX; i++) {
-            const char* xb = reinterpret_cast<const char*>(((NX * wv + i) >> 3) ? a.xl : a.xh) + 64 * st;
+            const char* xb = reinterpret_cast<const char*>((NX * wv + i) >= XPI ? a.xl : a.xh) + 64 * st;
             dma16(xb, xoff[i], lb + (NX * wv + i) * 1024);
         }
 #pragma unroll
@@ -419,9 +423,9 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
                 dma16(wsel(q0 / R), o, lb + XS1 + (NW * wv + j) * 1024);
             }
         }
-        if (F::MIN && (st & 7) == 0) {
-            const char* sbase = reinterpret_cast<const char*>((wv >> 1) ? a.sl : a.sh) + 16 * (st >> 3);
-            dma16(sbase, soff, sm + (uint32_t)(NS * ST1 + ((st >> 3) & 1) * (2 * BM * 16) + wv * 1024));
+        if (F::MIN && (st & 7) == 0 && wv < TM / 32) {   // TM / 32 x 1 KB of group sums
+            const char* sbase = reinterpret_cast<const char*>(wv >= TM / 64 ? a.sl : a.sh) + 16 * (st >> 3);
+            dma16(sbase, soff, sm + (uint32_t)(NS * ST1 + ((st >> 3) & 1) * (2 * TM * 16) + wv * 1024));
         }
     };
     // fragment addresses: activation rows ti * 16 + lr (two swizzle patterns),
@@ -481,14 +485,14 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
             }
         }
         // activation fragments of tile ti + 1 are read while tile ti's MFMAs issue
-        h8 xn0 = *reinterpret_cast<const h8*>(sb + xo0), xn1 = *reinterpret_cast<const h8*>(sb + xo0 + BM * 64);
+        h8 xn0 = *reinterpret_cast<const h8*>(sb + xo0), xn1 = *reinterpret_cast<const h8*>(sb + xo0 + TM * 64);
 #pragma unroll
         for (int ti = 0; ti < TI; ti++) {
             const h8 x0 = xn0, x1 = xn1;
             if (ti + 1 < TI) {
                 const unsigned char* xr = sb + (ti + 1) * 1024 + (((ti + 1) & 1) ? xo1 : xo0);
                 xn0 = *reinterpret_cast<const h8*>(xr);
-                xn1 = *reinterpret_cast<const h8*>(xr + BM * 64);
+                xn1 = *reinterpret_cast<const h8*>(xr + TM * 64);
             }
 #pragma unroll
             for (int tj = 0; tj < TJ; tj++) {
@@ -532,8 +536,8 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
                         const int tl = ti * 16 + lr;
                         h4 s0 = h4{0, 0, 0, 0}, s1 = h4{0, 0, 0, 0};
                         if (lk < 2) {
-                            s0 = *reinterpret_cast<const h4*>(Ss + ((sp * 2 + 0) * BM + tl) * 16 + 8 * lk);
-                            s1 = *reinterpret_cast<const h4*>(Ss + ((sp * 2 + 1) * BM + tl) * 16 + 8 * lk);
+                            s0 = *reinterpret_cast<const h4*>(Ss + ((sp * 2 + 0) * TM + tl) * 16 + 8 * lk);
+                            s1 = *reinterpret_cast<const h4*>(Ss + ((sp * 2 + 1) * TM + tl) * 16 + 8 * lk);
                         }
                         f4 rr = __builtin_amdgcn_mfma_f32_16x16x16f16(s0, mq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                         rr = __builtin_amdgcn_mfma_f32_16x16x16f16(s1, mq, rr, 0, 0, 0);
@@ -555,7 +559,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         for (int e = 0; e < 4; e++) xi[ti][e] = a.xinv[min(m0 + ti * 16 + 4 * lk + e, a.M - 1)];
     if (EPI == PF_SWIGLU) {
         // waves 2, 3 hold the up rows matching the gate rows of waves 0, 1
-        float (*E)[BM][16 * TJ + 1] = reinterpret_cast<float (*)[BM][16 * TJ + 1]>(smem);
+        float (*E)[TM][16 * TJ + 1] = reinterpret_cast<float (*)[TM][16 * TJ + 1]>(smem);
         if (wn >= 2) {
 #pragma unroll
             for (int ti = 0; ti < TI; ti++)
@@ -1072,10 +1076,22 @@ template <uint32_t FMT>
 hipError_t launch_gemm_fmt(int epi, PfGemmArgs a, hipStream_t s) {
     a.tiles_n = epi == PF_SWIGLU ? (a.N + 63) / 64 : (a.N + BN - 1) / BN;
     const int tiles = a.tiles_n * ((a.M + BM - 1) / BM) * a.ksplit;
-    const dim3 grid(8 * ((tiles + 7) / 8));
+    // 128 to 255 tiles of BM tokens fill only part of the CUs: 64-token tiles
+    // (LLMDOT_HIP_PF_TM64=0 turns this off)
+    const char* env = getenv("LLMDOT_HIP_PF_TM64");
+    const bool tm64_off = env && env[0] == '0' && env[1] == 0;
+    const bool tm64 = !tm64_off && epi != PF_SWIGLU && a.ksplit == 1 && tiles >= 128 && tiles < 256;
+    const int t64 = a.tiles_n * ((a.M + 63) / 64);
+    const dim3 grid(8 * (((tm64 ? t64 : tiles) + 7) / 8));
     switch (epi) {
-    case PF_STORE: pf_gemm_kernel<FMT, PF_STORE><<<grid, WG, 0, s>>>(a); break;
-    case PF_ADD: pf_gemm_kernel<FMT, PF_ADD><<<grid, WG, 0, s>>>(a); break;
+    case PF_STORE:
+        if (tm64) pf_gemm_kernel<FMT, PF_STORE, 64><<<grid, WG, 0, s>>>(a);
+        else pf_gemm_kernel<FMT, PF_STORE><<<grid, WG, 0, s>>>(a);
+        break;
+    case PF_ADD:
+        if (tm64) pf_gemm_kernel<FMT, PF_ADD, 64><<<grid, WG, 0, s>>>(a);
+        else pf_gemm_kernel<FMT, PF_ADD><<<grid, WG, 0, s>>>(a);
+        break;
     case PF_SWIGLU: pf_gemm_kernel<FMT, PF_SWIGLU><<<grid, WG, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }

@@ -215,3 +215,32 @@ def test_prefill_mistral7b(hip, oracle_threads):
     img = synth.build_image("mistral7b", seed=1234, context=32)
     prompt = synth.prompt(32000, 12, seed=7)
     _prompt_check(hip, img, prompt, 32, True, [0, 31])
+
+
+def test_prefill_64_token_tiles_bit_identical(hip, monkeypatch):
+    """1B shape, 1024-token prompt: Q, O and down have 128 tiles of 128 tokens,
+    which run as 64-token tiles (Q STORE, O and down ADD into the residual),
+    with Q4_K, Q6_K and the min term.  Every output's sum runs in the same
+    order as with 128-token tiles, so the last logits and the KV cache must
+    be bit-identical with the 64-token tiles turned off."""
+    n, ctx = 1024, 1040
+    img = synth.build_image("llama1b", seed=1234, context=ctx)
+    prompt = synth.prompt(128256, n, seed=29)
+    runs = []
+    for off in (False, True):
+        if off:
+            monkeypatch.setenv("LLMDOT_HIP_PF_TM64", "0")
+        else:
+            monkeypatch.delenv("LLMDOT_HIP_PF_TM64", raising=False)
+        eng = InferenceEngine(LoadedModel.load(img), hip, kv_fp16=True, context=ctx)
+        try:
+            logits, am = eng.prefill(prompt, 0)
+            kv = [eng.kv_read(layer, pos) for layer in (0, 7, 15) for pos in (0, 511, 1023)]
+        finally:
+            eng.dispose()
+        runs.append((np.array(logits, copy=True), am, kv))
+    (l0, a0, kv0), (l1, a1, kv1) = runs
+    assert a0 == a1
+    assert np.array_equal(l0, l1), float(np.max(np.abs(l0 - l1)))
+    for (k0, v0), (k1, v1) in zip(kv0, kv1):
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
