@@ -187,19 +187,23 @@ __device__ __forceinline__ uint32_t k_field12(uint32_t w1, uint32_t w2, uint32_t
 // rows touches 256 contiguous bytes); the 2-byte aligned formats copy windows
 // starting at the block address rounded down to 4 bytes ([row][ch]).
 // Every step's partial sum is scaled by the row's block scale d; NP = weight
-// planes; NS = LDS stages (prefetch distance NS - 1).
+// planes; NS = LDS stages (prefetch distance NS - 1).  RH > 0 (Q6_K): the
+// weights are staged once per half superblock (4 steps) instead, RH chunks per
+// row: the 4 steps of a half read the same qh bytes and pairs of them the same
+// ql bytes, which a per-step copy fetched again each time (128 bytes per row
+// and step for ~68 used).
 template <uint32_t FMT>
 struct PfFmt;
 template <>
-struct PfFmt<GGML_Q4_K> { static constexpr int BSZ = 144, EPB = 256, R = 2, NP = 1, NS = 2; static constexpr bool MIN = true, KQ = true; };
+struct PfFmt<GGML_Q4_K> { static constexpr int BSZ = 144, EPB = 256, R = 2, NP = 1, NS = 2, RH = 0; static constexpr bool MIN = true, KQ = true; };
 template <>
-struct PfFmt<GGML_Q5_K> { static constexpr int BSZ = 176, EPB = 256, R = 4, NP = 1, NS = 2; static constexpr bool MIN = true, KQ = true; };
+struct PfFmt<GGML_Q5_K> { static constexpr int BSZ = 176, EPB = 256, R = 4, NP = 1, NS = 2, RH = 0; static constexpr bool MIN = true, KQ = true; };
 template <>
-struct PfFmt<GGML_Q6_K> { static constexpr int BSZ = 210, EPB = 256, R = 8, NP = 2, NS = 2; static constexpr bool MIN = false, KQ = false; };
+struct PfFmt<GGML_Q6_K> { static constexpr int BSZ = 210, EPB = 256, R = 8, NP = 2, NS = 2, RH = 10; static constexpr bool MIN = false, KQ = false; };
 template <>
-struct PfFmt<GGML_Q8_0> { static constexpr int BSZ = 34, EPB = 32, R = 4, NP = 1, NS = 2; static constexpr bool MIN = false, KQ = false; };
+struct PfFmt<GGML_Q8_0> { static constexpr int BSZ = 34, EPB = 32, R = 4, NP = 1, NS = 2, RH = 0; static constexpr bool MIN = false, KQ = false; };
 template <>
-struct PfFmt<GGML_Q4_0> { static constexpr int BSZ = 18, EPB = 32, R = 2, NP = 1, NS = 2; static constexpr bool MIN = false, KQ = false; };
+struct PfFmt<GGML_Q4_0> { static constexpr int BSZ = 18, EPB = 32, R = 2, NP = 1, NS = 2, RH = 0; static constexpr bool MIN = false, KQ = false; };
 
 // K-quants: byte offset of chunk ch of group g within a superblock.
 template <uint32_t FMT>
@@ -207,20 +211,24 @@ __device__ __forceinline__ int kq_chunk_off(int ch, int g) {
     if constexpr (FMT == GGML_Q4_K) return ch == 0 ? 0 : 16 + 16 * g;                          // header | quants of g
     else return ch == 0 ? 0 : ch == 1 ? 48 + 16 * g : 16 + 16 * (g >> 2);                   // header | low nibbles | high bits
 }
-// 2-byte aligned formats: byte offset (from the row start) of the window that
-// chunk ch of step st belongs to, and the chunk's index inside that window.
+// Q8_0 / Q4_0: byte offset (from the row start) of the window that chunk ch
+// of step st belongs to, and the chunk's index inside that window.
 template <uint32_t FMT>
 __device__ __forceinline__ void win_chunk(int st, int ch, int64_t* off, int* k) {
-    using F = PfFmt<FMT>;
-    if constexpr (FMT == GGML_Q6_K) {
-        const int g = st & 7, n = 128 * (g >> 2), qq = g & 3;
-        const int64_t blk = (int64_t)(st >> 3) * F::BSZ;
-        *off = blk + (ch < 3 ? n / 2 + (qq & 1) * 32 : ch < 6 ? 128 + n / 4 : 192);     // ql | qh | scales + d
-        *k = ch < 3 ? ch : ch < 6 ? ch - 3 : ch - 6;
-    } else {   // Q8_0, Q4_0: the block
-        *off = (int64_t)st * F::BSZ;
-        *k = ch < 2 ? ch : 2;
-    }
+    *off = (int64_t)st * PfFmt<FMT>::BSZ;   // Q8_0, Q4_0: the block
+    *k = ch < 2 ? ch : 2;
+}
+
+// Q6_K half-superblock stage (steps 4 h .. 4 h + 3 of a superblock share it):
+// chunks 0-4 cover the 64 ql bytes at 64 h, 5-7 the 32 qh bytes at 128 + 32 h,
+// 8-9 the scales and d at 192; each window starts at its offset rounded down
+// to 4 bytes.  Byte offset (from the row start) of chunk ch's window, and the
+// chunk's index inside it.
+__device__ __forceinline__ void q6_half_chunk(int st, int ch, int64_t* off, int* k) {
+    const int h = (st >> 2) & 1;
+    const int64_t blk = (int64_t)(st >> 3) * 210;
+    *off = blk + (ch < 5 ? 64 * h : ch < 8 ? 128 + 32 * h : 192);
+    *k = ch < 5 ? ch : ch < 8 ? ch - 5 : ch - 8;
 }
 
 // 8 bytes starting at byte offset o (any alignment) of an LDS array, as 2 words.
@@ -264,15 +272,16 @@ template <uint32_t FMT>
 __device__ __forceinline__ void win_frag(const unsigned char* raw, int st, int lk, int64_t rowoff, h8* out, float* d) {
     uint32_t pr[4];
     if constexpr (FMT == GGML_Q6_K) {
-        const int g = st & 7, n = 128 * (g >> 2), qq = g & 3;
+        // raw: this row's half-superblock stage (q6_half_chunk)
+        const int g = st & 7, h = g >> 2, qq = g & 3;
         const int64_t blk = rowoff + (int64_t)(st >> 3) * 210;
-        const int sA = (int)((blk + n / 2 + (qq & 1) * 32) & 3), sB = (int)((blk + 128 + n / 4) & 3);
+        const int sA = (int)((blk + 64 * h) & 3), sB = (int)((blk + 128 + 32 * h) & 3);
         const int sC = (int)((blk + 192) & 3);
         uint32_t ql[2], qh[2];
-        lds_bytes8(raw, sA + 8 * lk, ql);
-        lds_bytes8(raw + 48, sB + 8 * lk, qh);
-        const int scv = (int)(int8_t)raw[96 + sC + 2 * g + (lk >> 1)];
-        const uint32_t dw = reinterpret_cast<const uint32_t*>(raw + 96)[(sC + 16) >> 2];
+        lds_bytes8(raw, sA + (qq & 1) * 32 + 8 * lk, ql);
+        lds_bytes8(raw + 80, sB + 8 * lk, qh);
+        const int scv = (int)(int8_t)raw[128 + sC + 2 * g + (lk >> 1)];
+        const uint32_t dw = reinterpret_cast<const uint32_t*>(raw + 128)[(sC + 16) >> 2];
         *d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw >> (8 * ((sC + 16) & 3))));
         const h2 sc2 = {(_Float16)(float)scv, (_Float16)(float)scv};
         const h2 off = {(_Float16)1056.f, (_Float16)1056.f};
@@ -343,14 +352,16 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     static_assert(TM == BM || (TM == 64 && EPI != PF_SWIGLU), "64-token tiles: STORE and ADD only");
     constexpr int NP = F::NP, R = F::R, NS = F::NS;
     constexpr int TI = TM / 16, TJ = BN / 16 / 4;    // wave w: all TM tokens x rows 16 TJ w .. +16 TJ - 1
+    constexpr bool WH = F::RH > 0;                   // weights staged per half superblock (4 steps)
     constexpr int XS1 = 2 * TM * 64;                 // activation stage: [plane][token][32 halves]
-    constexpr int WS1 = BN * R * 16;                 // raw weight stage
+    constexpr int WS1 = WH ? 0 : BN * R * 16;        // raw weight stage (per step)
+    constexpr int WSH = WH ? BN * F::RH * 16 : 0;    // raw weight stage (per half superblock), two of them
     constexpr int ST1 = XS1 + WS1;
     constexpr int SS_B = F::MIN ? 2 * 2 * TM * 16 : 0;   // [sb parity][plane][token][8] group sums
-    constexpr int STAGE_B = NS * ST1 + SS_B;
+    constexpr int STAGE_B = NS * ST1 + SS_B + 2 * WSH;
     constexpr int EX_B = 2 * TM * (16 * TJ + 1) * 4;     // SWIGLU exchange: [gate wave][token][rows + 1]
     constexpr int SMEM = STAGE_B > EX_B ? STAGE_B : EX_B;
-    constexpr int NX = TM / 32, NW = R / 2;          // DMA instructions per wave and step
+    constexpr int NX = TM / 32, NW = WH ? BN * F::RH / 256 : R / 2;   // DMA instructions per wave (weights: per stage)
     constexpr int XPI = TM / 16;                     // activation DMA instructions per plane
     __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
     const uint32_t sm = (uint32_t)reinterpret_cast<uintptr_t>(smem);
@@ -395,7 +406,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NW; j++) {
         const int q = (NW * wv + j) * 64 + lane;
-        const int r = F::KQ ? (q & 127) : q / R;
+        const int r = F::KQ ? (q & 127) : q / (WH ? F::RH : R);
         wrow[j] = (int64_t)grow_of(r) * rbytes;
         woff[j] = (uint32_t)wrow[j];
     }
@@ -415,6 +426,15 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
             if constexpr (F::KQ) {
                 const uint8_t* wb = wsel(q0 & 127) + (int64_t)(st >> 3) * F::BSZ + kq_chunk_off<FMT>(q0 >> 7, st & 7);
                 dma16(wb, woff[j], lb + XS1 + (NW * wv + j) * 1024);
+            } else if constexpr (WH) {   // a new half superblock every 4 steps
+                if ((st & 3) == 0) {
+                    int64_t off;
+                    int k;
+                    q6_half_chunk(st, (q0 + lane) % F::RH, &off, &k);
+                    const uint32_t o = (uint32_t)(((wrow[j] + off) & ~int64_t(3)) + 16 * k);
+                    dma16(wsel(q0 / F::RH), o,
+                          sm + (uint32_t)(NS * ST1 + SS_B + ((st >> 2) & 1) * WSH + (NW * wv + j) * 1024));
+                }
             } else {
                 int64_t off;
                 int k;
@@ -464,7 +484,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         lds_barrier();   // every wave's copies of step st landed; step st - 1's buffers are free
         if (st + NS - 1 < st1) issue(st + NS - 1);
         const unsigned char* sb = smem + (st % NS) * ST1;
-        const unsigned char* raw = sb + XS1;
+        const unsigned char* raw = WH ? smem + NS * ST1 + SS_B + ((st >> 2) & 1) * WSH : sb + XS1;
         h8 wf[TJ][NP];
         float d[TJ];
         if constexpr (F::KQ) {
@@ -481,7 +501,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
                 wf[tj][0] = kq_frag<FMT>(hdr[tj], raw + 2048 + rw[tj] * 16, st & 7, lk);
                 d[tj] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr[tj][0] & 0xFFFFu));
             } else {
-                win_frag<FMT>(raw + rw[tj] * R * 16, st, lk, frow[tj], wf[tj], &d[tj]);
+                win_frag<FMT>(raw + rw[tj] * (WH ? F::RH : R) * 16, st, lk, frow[tj], wf[tj], &d[tj]);
             }
         }
         // activation fragments of tile ti + 1 are read while tile ti's MFMAs issue
