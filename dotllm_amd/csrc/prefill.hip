@@ -187,11 +187,12 @@ __device__ __forceinline__ uint32_t k_field12(uint32_t w1, uint32_t w2, uint32_t
 // rows touches 256 contiguous bytes); the 2-byte aligned formats copy windows
 // starting at the block address rounded down to 4 bytes ([row][ch]).
 // Every step's partial sum is scaled by the row's block scale d; NP = weight
-// planes; NS = LDS stages (prefetch distance NS - 1).  RH > 0 (Q6_K): the
-// weights are staged once per half superblock (4 steps) instead, RH chunks per
-// row: the 4 steps of a half read the same qh bytes and pairs of them the same
-// ql bytes, which a per-step copy fetched again each time (128 bytes per row
-// and step for ~68 used).
+// planes; NS = LDS stages (prefetch distance NS - 1).  RH > 0: the weights
+// are staged once per 4 steps instead, RH chunks per row.  Q6_K: the 4 steps
+// of a half superblock read the same qh bytes and pairs of them the same ql
+// bytes, which a per-step copy fetched again each time (128 bytes per row and
+// step for ~68 used); Q8_0: 4 blocks of 34 bytes in 10 chunks instead of 4
+// per block (the last a repeat).
 template <uint32_t FMT>
 struct PfFmt;
 template <>
@@ -201,7 +202,7 @@ struct PfFmt<GGML_Q5_K> { static constexpr int BSZ = 176, EPB = 256, R = 4, NP =
 template <>
 struct PfFmt<GGML_Q6_K> { static constexpr int BSZ = 210, EPB = 256, R = 8, NP = 2, NS = 2, RH = 10; static constexpr bool MIN = false, KQ = false; };
 template <>
-struct PfFmt<GGML_Q8_0> { static constexpr int BSZ = 34, EPB = 32, R = 4, NP = 1, NS = 2, RH = 0; static constexpr bool MIN = false, KQ = false; };
+struct PfFmt<GGML_Q8_0> { static constexpr int BSZ = 34, EPB = 32, R = 4, NP = 1, NS = 2, RH = 10; static constexpr bool MIN = false, KQ = false; };
 template <>
 struct PfFmt<GGML_Q4_0> { static constexpr int BSZ = 18, EPB = 32, R = 2, NP = 1, NS = 2, RH = 0; static constexpr bool MIN = false, KQ = false; };
 
@@ -211,11 +212,11 @@ __device__ __forceinline__ int kq_chunk_off(int ch, int g) {
     if constexpr (FMT == GGML_Q4_K) return ch == 0 ? 0 : 16 + 16 * g;                          // header | quants of g
     else return ch == 0 ? 0 : ch == 1 ? 48 + 16 * g : 16 + 16 * (g >> 2);                   // header | low nibbles | high bits
 }
-// Q8_0 / Q4_0: byte offset (from the row start) of the window that chunk ch
-// of step st belongs to, and the chunk's index inside that window.
+// Q4_0: byte offset (from the row start) of the window that chunk ch of step
+// st belongs to, and the chunk's index inside that window.
 template <uint32_t FMT>
 __device__ __forceinline__ void win_chunk(int st, int ch, int64_t* off, int* k) {
-    *off = (int64_t)st * PfFmt<FMT>::BSZ;   // Q8_0, Q4_0: the block
+    *off = (int64_t)st * PfFmt<FMT>::BSZ;   // the block
     *k = ch < 2 ? ch : 2;
 }
 
@@ -229,6 +230,20 @@ __device__ __forceinline__ void q6_half_chunk(int st, int ch, int64_t* off, int*
     const int64_t blk = (int64_t)(st >> 3) * 210;
     *off = blk + (ch < 5 ? 64 * h : ch < 8 ? 128 + 32 * h : 192);
     *k = ch < 5 ? ch : ch < 8 ? ch - 5 : ch - 8;
+}
+
+// Q8_0 stage: the 4 blocks of steps 4 j .. 4 j + 3 (136 bytes) in 10 chunks
+// from the first block's offset rounded down to 4 bytes.
+__device__ __forceinline__ void q8_quad_chunk(int st, int ch, int64_t* off, int* k) {
+    *off = (int64_t)(st & ~3) * 34;
+    *k = ch;
+}
+
+// Stage window of chunk ch for step st (formats with PfFmt::RH > 0).
+template <uint32_t FMT>
+__device__ __forceinline__ void staged_chunk(int st, int ch, int64_t* off, int* k) {
+    if constexpr (FMT == GGML_Q6_K) q6_half_chunk(st, ch, off, k);
+    else q8_quad_chunk(st, ch, off, k);
 }
 
 // 8 bytes starting at byte offset o (any alignment) of an LDS array, as 2 words.
@@ -300,21 +315,25 @@ __device__ __forceinline__ void win_frag(const unsigned char* raw, int st, int l
         }
         out[0] = __builtin_bit_cast(h8, v4u{ph[0], ph[1], ph[2], ph[3]});
         out[1] = __builtin_bit_cast(h8, v4u{pl[0], pl[1], pl[2], pl[3]});
-    } else {   // Q8_0, Q4_0: window shift s = block offset & 3; d at s, payload at s + 2
+    } else if constexpr (FMT == GGML_Q8_0) {   // raw: this row's 4-block stage (q8_quad_chunk)
+        const int o = (int)((rowoff + (int64_t)(st & ~3) * 34) & 3) + 34 * (st & 3);   // block start, even
+        const uint32_t dw = reinterpret_cast<const uint32_t*>(raw)[o >> 2];
+        *d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw >> (8 * (o & 3))));
+        uint32_t q[2];
+        lds_bytes8(raw, o + 2 + 8 * lk, q);
+        bytes_to_h2(q[0] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &pr[0]);
+        bytes_to_h2(q[1] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &pr[2]);
+        out[0] = __builtin_bit_cast(h8, v4u{pr[0], pr[1], pr[2], pr[3]});
+    } else {   // Q4_0: window shift s = block offset & 3; d at s, payload at s + 2
         const int sh = (int)((rowoff + (int64_t)st * PfFmt<FMT>::BSZ) & 3);
         const uint32_t dw = reinterpret_cast<const uint32_t*>(raw)[0];
         *d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw >> (8 * sh)));
         uint32_t q[2];
-        if constexpr (FMT == GGML_Q8_0) {
-            lds_bytes8(raw, sh + 2 + 8 * lk, q);
-            bytes_to_h2(q[0] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &pr[0]);
-            bytes_to_h2(q[1] ^ 0x80808080u, (_Float16)1152.f, (_Float16)1.f, &pr[2]);
-        } else {   // elements 0..15: low nibbles of bytes 0..15; 16..31: high nibbles
-            lds_bytes8(raw, sh + 2 + 8 * (lk & 1), q);
-            const uint32_t sft = lk < 2 ? 0u : 4u;
-            bytes_to_h2((q[0] >> sft) & 0x0F0F0F0Fu, (_Float16)1032.f, (_Float16)1.f, &pr[0]);
-            bytes_to_h2((q[1] >> sft) & 0x0F0F0F0Fu, (_Float16)1032.f, (_Float16)1.f, &pr[2]);
-        }
+        // elements 0..15: low nibbles of bytes 0..15; 16..31: high nibbles
+        lds_bytes8(raw, sh + 2 + 8 * (lk & 1), q);
+        const uint32_t sft = lk < 2 ? 0u : 4u;
+        bytes_to_h2((q[0] >> sft) & 0x0F0F0F0Fu, (_Float16)1032.f, (_Float16)1.f, &pr[0]);
+        bytes_to_h2((q[1] >> sft) & 0x0F0F0F0Fu, (_Float16)1032.f, (_Float16)1.f, &pr[2]);
         out[0] = __builtin_bit_cast(h8, v4u{pr[0], pr[1], pr[2], pr[3]});
     }
 }
@@ -352,10 +371,10 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     static_assert(TM == BM || (TM == 64 && EPI != PF_SWIGLU), "64-token tiles: STORE and ADD only");
     constexpr int NP = F::NP, R = F::R, NS = F::NS;
     constexpr int TI = TM / 16, TJ = BN / 16 / 4;    // wave w: all TM tokens x rows 16 TJ w .. +16 TJ - 1
-    constexpr bool WH = F::RH > 0;                   // weights staged per half superblock (4 steps)
+    constexpr bool WH = F::RH > 0;                   // weights staged once per 4 steps
     constexpr int XS1 = 2 * TM * 64;                 // activation stage: [plane][token][32 halves]
     constexpr int WS1 = WH ? 0 : BN * R * 16;        // raw weight stage (per step)
-    constexpr int WSH = WH ? BN * F::RH * 16 : 0;    // raw weight stage (per half superblock), two of them
+    constexpr int WSH = WH ? BN * F::RH * 16 : 0;    // raw weight stage (per 4 steps), two of them
     constexpr int ST1 = XS1 + WS1;
     constexpr int SS_B = F::MIN ? 2 * 2 * TM * 16 : 0;   // [sb parity][plane][token][8] group sums
     constexpr int STAGE_B = NS * ST1 + SS_B + 2 * WSH;
@@ -426,11 +445,11 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
             if constexpr (F::KQ) {
                 const uint8_t* wb = wsel(q0 & 127) + (int64_t)(st >> 3) * F::BSZ + kq_chunk_off<FMT>(q0 >> 7, st & 7);
                 dma16(wb, woff[j], lb + XS1 + (NW * wv + j) * 1024);
-            } else if constexpr (WH) {   // a new half superblock every 4 steps
-                if ((st & 3) == 0) {
+            } else if constexpr (WH) {   // a new stage every 4 steps (and at a part's first step)
+                if ((st & 3) == 0 || st == st0) {
                     int64_t off;
                     int k;
-                    q6_half_chunk(st, (q0 + lane) % F::RH, &off, &k);
+                    staged_chunk<FMT>(st, (q0 + lane) % F::RH, &off, &k);
                     const uint32_t o = (uint32_t)(((wrow[j] + off) & ~int64_t(3)) + 16 * k);
                     dma16(wsel(q0 / F::RH), o,
                           sm + (uint32_t)(NS * ST1 + SS_B + ((st >> 2) & 1) * WSH + (NW * wv + j) * 1024));
