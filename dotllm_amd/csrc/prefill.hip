@@ -443,8 +443,11 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         for (int j = 0; j < NW; j++) {
             const int q0 = (NW * wv + j) * 64;
             if constexpr (F::KQ) {
-                const uint8_t* wb = wsel(q0 & 127) + (int64_t)(st >> 3) * F::BSZ + kq_chunk_off<FMT>(q0 >> 7, st & 7);
-                dma16(wb, woff[j], lb + XS1 + (NW * wv + j) * 1024);
+                // chunk 0 (the header) is read only at a superblock's first step
+                if ((q0 >> 7) != 0 || (st & 7) == 0) {
+                    const uint8_t* wb = wsel(q0 & 127) + (int64_t)(st >> 3) * F::BSZ + kq_chunk_off<FMT>(q0 >> 7, st & 7);
+                    dma16(wb, woff[j], lb + XS1 + (NW * wv + j) * 1024);
+                }
             } else if constexpr (WH) {   // a new stage every 4 steps (and at a part's first step)
                 if ((st & 3) == 0 || st == st0) {
                     int64_t off;
