@@ -356,12 +356,14 @@ __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" :
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // LDS rows of 32 halves (64 bytes) hold 4 chunks of 8; chunk c of row r sits
-// at position c ^ swz(r).  swz(16 i + l) = swz(l) ^ 2 (i & 1).  An MFMA
-// fragment read (16 rows x 4 chunks) still takes two passes of the LDS (as
-// does the unswizzled [row][chunk] order); the conflict-free order, chunk-major
-// per 16-row tile, makes the global -> LDS copies slower by more than it saves
-// (a lane quad no longer covers one token's 64 contiguous bytes).
-__device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ r ^ ((r >> 3) & 2)) & 3; }
+// at position c ^ swz(r), swz(r) = (r >> 1) & 3 (the same for rows 16 i + l
+// and l).  An MFMA fragment read (16 rows x 4 chunks, lane 16 c + l reading
+// chunk c of row l) then takes one LDS pass: measured on gfx950, conflict-free
+// like a read of consecutive 16-byte words, where the unswizzled order and
+// other XOR patterns take two.  A copy instruction still covers 16 tokens'
+// contiguous 64 bytes, 4 lanes each (the chunk-major layout, also
+// conflict-free to read, made the copies slower than it saved).
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 
 // TM tokens per workgroup: BM, or 64 for launches that would have only 128
 // to 255 tiles of BM (all CUs busy; each output's sum runs in the same order).
@@ -470,9 +472,8 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
             dma16(sbase, soff, sm + (uint32_t)(NS * ST1 + ((st >> 3) & 1) * (2 * TM * 16) + wv * 1024));
         }
     };
-    // fragment addresses: activation rows ti * 16 + lr (two swizzle patterns),
-    // weight rows rw[tj]
-    const int xo0 = lr * 64 + ((lk ^ swz(lr)) << 4), xo1 = lr * 64 + ((lk ^ swz(lr) ^ 2) << 4);
+    // fragment addresses: activation rows ti * 16 + lr, weight rows rw[tj]
+    const int xo0 = lr * 64 + ((lk ^ swz(lr)) << 4);
     int rw[TJ];
     int64_t frow[TJ];
 #pragma unroll
@@ -532,7 +533,7 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
         for (int ti = 0; ti < TI; ti++) {
             const h8 x0 = xn0, x1 = xn1;
             if (ti + 1 < TI) {
-                const unsigned char* xr = sb + (ti + 1) * 1024 + (((ti + 1) & 1) ? xo1 : xo0);
+                const unsigned char* xr = sb + (ti + 1) * 1024 + xo0;
                 xn0 = *reinterpret_cast<const h8*>(xr);
                 xn1 = *reinterpret_cast<const h8*>(xr + TM * 64);
             }
