@@ -244,3 +244,20 @@ def test_prefill_64_token_tiles_bit_identical(hip, monkeypatch):
     assert np.array_equal(l0, l1), float(np.max(np.abs(l0 - l1)))
     for (k0, v0), (k1, v1) in zip(kv0, kv1):
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+@pytest.mark.parametrize("k", [96, 160])
+def test_batched_matmul_short_k(hip, t, k):
+    """32-element block formats with K not a multiple of 128: Q8_0 stages 4
+    blocks at a time, so the last stage of each row holds 1 or 3 blocks plus
+    bytes past the row (read, never used)."""
+    m, n = 130, 200
+    rng = np.random.default_rng(k + t)
+    w = synth.quantize(t, rng.normal(0, 0.02, size=(n, k)).astype(np.float32))
+    a = rng.normal(0, 1, size=(m, k)).astype(np.float32)
+    ref = O.matmul(a, w, t, k, n, result_len=m * n).reshape(m, n)
+    y = np.zeros(m * n, dtype=np.float32)
+    hip.mat_mul(a.reshape(-1), w, y, t, k, n)
+    err = row_rel_err(y.reshape(m, n), ref)
+    assert err <= FP32_LEVEL, err
