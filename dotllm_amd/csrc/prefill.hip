@@ -94,8 +94,25 @@ __global__ __launch_bounds__(WG) void pf_planes_kernel(const float* __restrict__
         if (!NORM) return v;
         return i < n8 ? ((w[i] * v) * inv) : (w[i] * (v * inv));
     };
+    // The thread's y values, 4 consecutive elements per 1024-element block,
+    // read once and kept in registers (K <= 16384), or re-read below.
+    constexpr int NB = 16;
+    const bool held = K <= NB * 4 * WG;
+    float yr[NB][4];
     float amax = 0.f;
-    for (int i = tid; i < K; i += WG) amax = fmaxf(amax, fabsf(yval(i)));
+    if (held) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int base = b * 4 * WG + 4 * tid;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                yr[b][j] = base < K ? yval(base + j) : 0.f;   // K % 32 == 0: whole quads
+                amax = fmaxf(amax, fabsf(yr[b][j]));
+            }
+        }
+    } else {
+        for (int i = tid; i < K; i += WG) amax = fmaxf(amax, fabsf(yval(i)));
+    }
     amax = wave_max(amax);
     if (lane == 0) red[wave] = amax;
     __syncthreads();
@@ -111,17 +128,12 @@ __global__ __launch_bounds__(WG) void pf_planes_kernel(const float* __restrict__
     const float s = ldexpf(1.0f, e), s32 = ldexpf(1.0f, e - 5);
     if (tid == 0) xinv[t] = ldexpf(1.0f, -e);
     // 4 consecutive elements per thread; 8 threads cover one 32-element group
-    for (int b0 = 0; b0 < K; b0 += 4 * WG) {
-        const int base = b0 + 4 * tid;
-        const bool ok = base < K;     // K % 32 == 0: a group's 8 lanes agree
-        float y[4], g = 0.f;
+    auto emit = [&](const int base, const float* y) __attribute__((always_inline)) {
+        float g = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            y[j] = ok ? yval(base + j) : 0.f;
-            g += y[j];
-        }
+        for (int j = 0; j < 4; j++) g += y[j];
         g = sum8(g);
-        if (ok) {
+        if (base < K) {
             h4 hv, lv;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -138,6 +150,19 @@ __global__ __launch_bounds__(WG) void pf_planes_kernel(const float* __restrict__
                 sh[(int64_t)t * (K / 32) + base / 32] = hi;
                 sl[(int64_t)t * (K / 32) + base / 32] = (_Float16)(gs - (float)hi);
             }
+        }
+    };
+    if (held) {
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            if (b * 4 * WG < K) emit(b * 4 * WG + 4 * tid, yr[b]);   // uniform: every lane calls sum8
+    } else {
+        for (int b0 = 0; b0 < K; b0 += 4 * WG) {
+            const int base = b0 + 4 * tid;
+            float y[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) y[j] = base < K ? yval(base + j) : 0.f;
+            emit(base, y);
         }
     }
 }
