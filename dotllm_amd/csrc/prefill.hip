@@ -31,8 +31,11 @@
 // all 128 tokens and rows 32 w .. 32 w + 31 as 8 x 2 MFMA tiles, so each
 // wave dequantises only its own 32 rows.  K advances 32 per step (one MFMA
 // K).  Each step's activation planes and raw weight blocks are copied
-// global -> LDS by the waves (global_load_lds, no registers) two steps ahead;
-// each wave then builds its weight fragments from the raw bytes in LDS.
+// global -> LDS by the waves (global_load_lds, no registers) one step ahead
+// into two LDS stages; each wave then builds its weight fragments from the
+// raw bytes in LDS.  Launches that would have few tiles use 64-token tiles
+// (128 to 255 tiles) or split K into parts summed by the next kernel (under
+// 128 tiles).
 #include "common.h"
 #include "kernels.h"
 
