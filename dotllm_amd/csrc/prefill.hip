@@ -629,36 +629,42 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) xi[ti][e] = a.xinv[min(m0 + ti * 16 + 4 * lk + e, a.M - 1)];
     if (EPI == PF_SWIGLU) {
-        // waves 2, 3 hold the up rows matching the gate rows of waves 0, 1
+        // waves 2, 3 hold the up rows matching the gate rows of waves 0, 1.
+        // The pair splits the tokens: the gate wave finishes the first half
+        // (up values through LDS), the up wave the second (gate values
+        // through LDS); each value crosses as the same fp32 number.
         float (*E)[TM][16 * TJ + 1] = reinterpret_cast<float (*)[TM][16 * TJ + 1]>(smem);
-        if (wn >= 2) {
+        const bool gate = wn < 2;
+        const int pw = gate ? wn : wn - 2;   // the pair's index
 #pragma unroll
-            for (int ti = 0; ti < TI; ti++)
+        for (int ti = 0; ti < TI; ti++) {
+            if ((ti < TI / 2) == gate) continue;   // the half the other wave finishes
 #pragma unroll
-                for (int tj = 0; tj < TJ; tj++)
+            for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) E[wn - 2][ti * 16 + 4 * lk + e][tj * 16 + lr] = acc[ti][tj][e] * xi[ti][e];
+                for (int e = 0; e < 4; e++) E[pw][ti * 16 + 4 * lk + e][tj * 16 + lr] = acc[ti][tj][e] * xi[ti][e];
         }
         __syncthreads();
-        if (wn < 2) {
-            const int n8 = a.N & ~7;
+        const int n8 = a.N & ~7;
 #pragma unroll
-            for (int ti = 0; ti < TI; ti++)
+        for (int ti = 0; ti < TI; ti++) {
+            if ((ti < TI / 2) != gate) continue;
 #pragma unroll
-                for (int tj = 0; tj < TJ; tj++)
+            for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int t = m0 + ti * 16 + 4 * lk + e;
-                        const int row = tn * 64 + wn * 16 * TJ + tj * 16 + lr;
-                        if (t < a.M && row < a.N) {
+                for (int e = 0; e < 4; e++) {
+                    const int t = m0 + ti * 16 + 4 * lk + e;
+                    const int row = tn * 64 + pw * 16 * TJ + tj * 16 + lr;
+                    if (t < a.M && row < a.N) {
 #pragma clang fp contract(off)
-                            const float g = acc[ti][tj][e] * xi[ti][e];
-                            const float u = E[wn][ti * 16 + 4 * lk + e][tj * 16 + lr];
-                            // SiluInPlace then Mul (IE:463-474): ExpApprox on the vector lanes
-                            const float sg = row < n8 ? silu_ref(g) : g / (1.0f + expf(-g));
-                            a.out[(int64_t)t * a.ldo + row] = sg * u;
-                        }
+                        const float own = acc[ti][tj][e] * xi[ti][e];
+                        const float other = E[pw][ti * 16 + 4 * lk + e][tj * 16 + lr];
+                        const float g = gate ? own : other, u = gate ? other : own;
+                        // SiluInPlace then Mul (IE:463-474): ExpApprox on the vector lanes
+                        const float sg = row < n8 ? silu_ref(g) : g / (1.0f + expf(-g));
+                        a.out[(int64_t)t * a.ldo + row] = sg * u;
                     }
+                }
         }
     } else {
 #pragma unroll
