@@ -193,7 +193,8 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
 
 // ======================================================= allocation-free ==
 // llmdot_hip_sample_noalloc keeps its scratch in this file-scope device array
-// instead of allocating: the sampler's work vector (one float per logit), the
+// instead of allocating: the sampler's work vector (sample_work_floats(n):
+// the probabilities and the top-p sort scratch, 9 floats per logit), the
 // argmax candidates (one per 4096 logits) and two words (the draw counter and
 // the uniform draw).  Each device holds its own copy until the process ends;
 // its address is looked up once per device (with that device current) when a
@@ -201,11 +202,13 @@ int upload(llmdot_hip_ctx* ctx, const std::string& key, uint32_t type, const voi
 namespace {
 constexpr int NOALLOC_MAX_N = 262144;                                  // logits per call
 constexpr int NOALLOC_CAND = NOALLOC_MAX_N / 4096;                     // argmax_grid(NOALLOC_MAX_N)
-constexpr size_t NOALLOC_WORK = sizeof(float) * (size_t)NOALLOC_MAX_N; // work[n]
+constexpr size_t NOALLOC_WORK = sizeof(float) * (((size_t)NOALLOC_MAX_N + 1) & ~(size_t)1) +
+                                sizeof(float) * 8 * (size_t)NOALLOC_MAX_N;  // sample_work_floats(NOALLOC_MAX_N)
+static_assert(NOALLOC_WORK == sizeof(float) * sample_work_floats(NOALLOC_MAX_N), "sampler work size");
 constexpr size_t NOALLOC_CAND_VAL = NOALLOC_WORK;                      // float[NOALLOC_CAND]
 constexpr size_t NOALLOC_CAND_IDX = NOALLOC_CAND_VAL + 4 * NOALLOC_CAND;   // int32[NOALLOC_CAND]
 constexpr size_t NOALLOC_INTS = NOALLOC_CAND_IDX + 4 * NOALLOC_CAND;   // [0] draw counter, [1] draw bits
-constexpr size_t NOALLOC_BYTES = NOALLOC_INTS + 256;                   // 1 MiB + 768 B
+constexpr size_t NOALLOC_BYTES = NOALLOC_INTS + 256;                   // 9 MiB + 768 B
 constexpr int NOALLOC_MAX_DEVICES = 64;
 // Elements of each prefill K-part buffer: a split keeps tiles (of 128 x 128)
 // x parts <= 512 (prefill_ksplit).
@@ -661,7 +664,7 @@ extern "C" int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, i
     float *dl, *dr;
     int32_t* dh;
     if (int rc = stage_in(ctx, 0, logits, (size_t)n, &dl)) return rc;
-    HIPCHK(ctx->scratch[1].ensure(sizeof(float) * (size_t)n));
+    HIPCHK(ctx->scratch[1].ensure(sizeof(float) * sample_work_floats(n)));
     if (int rc = stage_in(ctx, 2, recent, (size_t)n_recent, &dh)) return rc;
     if (int rc = stage_in(ctx, 3, &r, 1, &dr)) return rc;
     HIPCHK(launch_set_scalar(ctx->am_ints + 1, 1, ctx->stream));   // draw 0
@@ -1510,7 +1513,7 @@ int generate_begin(llmdot_hip_model* m, const int32_t* prompt, int32_t n_prompt,
             void *h, *r, *w;
             if (int rc = dalloc(m, sizeof(int32_t) * (size_t)(d.context + 1), &h)) return rc;
             if (int rc = dalloc(m, sizeof(float) * (size_t)(d.context + 1), &r)) return rc;
-            if (int rc = dalloc(m, sizeof(float) * (size_t)d.vocab, &w)) return rc;
+            if (int rc = dalloc(m, sizeof(float) * sample_work_floats(d.vocab), &w)) return rc;
             m->s_hist = (int32_t*)h; m->s_draws = (float*)r; m->s_work = (float*)w;
         }
         if (n_prompt > 0)

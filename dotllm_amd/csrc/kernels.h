@@ -152,13 +152,17 @@ struct SampleArgs {
     int hist_base;
     const int32_t* step;      // this is draw *step - 1 (the argmax pass has advanced it)
     const float* rvals;       // uniform draws: draw s uses rvals[s]
-    float* work;              // [n] scratch
+    float* work;              // [sample_work_floats(n)] scratch: probabilities, then the top-p scratch
     int32_t* token_out;       // the sampled token
     int32_t* token_log;       // optional: token_log[draw] = token while draw < log_cap
     int32_t log_cap;
     int32_t* hist_out;        // optional: hist_out[hist_base + draw] = token
 };
 bool sample_supported(int n, int top_k);
+// Floats of SampleArgs::work for n logits: the probabilities, then (8-byte
+// aligned) the top-p slow path's scratch: 3n 64-bit sort slots, n ids, n values.
+__host__ __device__ constexpr size_t sample_comp_offset(int n) { return ((size_t)n + 1) & ~(size_t)1; }
+__host__ __device__ constexpr size_t sample_work_floats(int n) { return sample_comp_offset(n) + 8 * (size_t)n; }
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
 
 // ---- prefill.hip (batched prompt processing) ----

@@ -10,17 +10,22 @@
 //             sorted by (value desc, index asc), VectorMath.Softmax over them in
 //             the reference's summation order, then the sequential draw
 //             (SampleFromProbabilities, Sampler.cs:158-170)
-//   softmax:  (otherwise) VectorMath.Softmax over all n (same maximum and
-//             exponentials; the sum is a workgroup reduction)
-//   top-p:    (TopP < 1, Sampler.cs:44-59, FindNucleus 129-156) the nucleus
-//             boundary and the draw inside it located by radix descent over
-//             the probabilities with fp64 mass sums, so no full sort is needed;
-//             without a proper nucleus the draw walks the probabilities in index
-//             order (Sampler.cs:61).
+//   softmax:  (otherwise) VectorMath.Softmax over all n in the reference's
+//             summation order: the probabilities bit for bit
+//   top-p:    (TopP < 1, Sampler.cs:44-61, FindNucleus 129-156) the reference
+//             as written: its selection-sort order (ties included), the values
+//             it writes into the buffer it still reads from, the sequential
+//             float running sum that closes the nucleus, the renormalised draw,
+//             and the fall-through draw over the rewritten buffer that returns
+//             a rank; candidates located by fp64 radix descent, so a full sort
+//             runs only when they do not suffice
+//   no top-p: the draw over the probabilities in index order (Sampler.cs:61),
+//             placed with fp64 running sums
 //
 // The uniform draw r (Random.NextSingle() in the reference, Sampler.cs:160-161)
 // is an input, read from rvals[step - 1], so the caller owns the generator.
-// Exact ties between values are resolved toward the smaller index.
+// In the top-k path exact ties between values are resolved toward the smaller
+// index.
 #include "common.h"
 #include "kernels.h"
 
@@ -323,16 +328,19 @@ __global__ __launch_bounds__(SWG) void samp_topk_kernel(SampleArgs a) {
     if (t == 0) publish(a, s_pick);
 }
 
-// VectorMath.Softmax over all n in place (VM:215-258): the same max and
-// exponentials (ExpApprox on the first 8 floor(n/8), expf on the tail); the sum
-// is a workgroup reduction, so it (and the probabilities) may differ from the
-// reference's interleaved sequential sum in the last bits.
+// VectorMath.Softmax over all n in place (VM:215-258) in the reference's
+// order: the maximum (FindMax, VM:260-284: the same value whatever the order),
+// the exponentials (ExpApprox on the first 8 floor(n/8), expf on the tail),
+// eight lane sums (lane l adds elements l, l + 8, ... in order), their
+// horizontal sum ((l0 + l1) + (l2 + l3)) + ((l4 + l5) + (l6 + l7)), the tail
+// added in order, then each probability times 1f / sum -- bit for bit the
+// reference's probabilities.
 __global__ __launch_bounds__(SWG) void samp_softmax_kernel(SampleArgs a) {
     __shared__ float red[NWAVE];
+    __shared__ float s_lane[8];
     __shared__ float s_inv;
     const int n = a.n, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     float* x = a.work;
-    // FindMax (VM:260-284) returns the maximum value whatever the order
     float m = -INFINITY;
     for (int i = t; i < n; i += SWG) m = fmaxf(m, x[i]);
     m = wave_max(m);
@@ -341,7 +349,6 @@ __global__ __launch_bounds__(SWG) void samp_softmax_kernel(SampleArgs a) {
     m = red[0];
     for (int w = 1; w < NWAVE; w++) m = fmaxf(m, red[w]);
     const int n8 = n & ~7;
-    float sum = 0.f;
     for (int i = t; i < n; i += SWG) {
         float ev;
         {
@@ -350,15 +357,26 @@ __global__ __launch_bounds__(SWG) void samp_softmax_kernel(SampleArgs a) {
             ev = i < n8 ? exp_approx(d) : expf(d);
         }
         x[i] = ev;
-        sum += ev;
     }
-    sum = wave_sum(sum);
     __syncthreads();
-    if (lane == 0) red[wave] = sum;
+    if (t < 8) {
+        // lane t's running sum; the loads run ahead of the dependent adds
+        float acc = 0.f;
+        int j = t;
+        for (; j + 8 * 15 < n8; j += 8 * 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = x[j + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc += v[u];
+        }
+        for (; j < n8; j += 8) acc += x[j];
+        s_lane[t] = acc;
+    }
     __syncthreads();
     if (t == 0) {
-        float z = 0.f;
-        for (int w = 0; w < NWAVE; w++) z += red[w];
+        float z = ((s_lane[0] + s_lane[1]) + (s_lane[2] + s_lane[3])) + ((s_lane[4] + s_lane[5]) + (s_lane[6] + s_lane[7]));
+        for (int j = n8; j < n; j++) z += x[j];
         s_inv = 1.0f / z;
     }
     __syncthreads();
@@ -366,63 +384,249 @@ __global__ __launch_bounds__(SWG) void samp_softmax_kernel(SampleArgs a) {
     for (int i = t; i < n; i += SWG) x[i] = x[i] * inv;
 }
 
-// Top-p nucleus and the draw (Sampler.cs:44-61) over the probabilities in work.
+// ---- top-p: FindNucleus (Sampler.cs:129-156) with the reference's buffers ----
+//
+// The reference sorts token ids by probability with a selection sort (strict
+// `>`, so among equal values the first in the array's current order wins) and
+// then writes values[i] = probabilities[indices[i]] into the same buffer the
+// probabilities live in (Sampler.cs:30, 48-50): a rank i whose id indices[i]
+// is below i reads the value rank indices[i] already wrote.  Following
+// a = indices[a] while indices[a] < a therefore gives rank i's value,
+// p[indices[a]] (each link lowers a, so the chain ends).  The running float sum
+// of those values, in rank order, closes the nucleus; when it never reaches
+// TopP the fall-through draw walks the rewritten buffer and returns a rank.
+//
+// Selection order: distinct values leave in descending order.  Equal values
+// leave together, in the order of the array positions they hold when the
+// first of them is selected; positions change only by the sort's swaps: at
+// step s the selected element's old position src[s] receives the element that
+// stood at s.  An element e still unselected at step s therefore stands at the
+// end of e, src[e], src[src[e]], ... (followed while below s), and the members
+// of a run of equal values keep their positions while the run is selected.
+//
+// Candidates: every element down to the value at which the fp64 mass reaches
+// TopP + 1e-4 (whole runs of equal values).  The aliased values are at least
+// the true ones and float addition is monotonic, so the aliased running sum
+// reaches TopP no later than the true one; if it still has not within the
+// candidates the kernel repeats the work over all n (global scratch).
+
+constexpr int NUC_LDS = 4096;   // candidates sorted in LDS (fast path)
+
+// Ascending bitonic sort of a[0, P) (P a power of two) by the whole workgroup.
+__device__ void bitonic_asc(uint64_t* a, int P, bool global) {
+    const int t = threadIdx.x;
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = t; i < P / 2; i += SWG) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const uint64_t x = a[lo], y = a[hi];
+                if ((x > y) == up) { a[lo] = y; a[hi] = x; }
+            }
+            if (global) __threadfence();
+            __syncthreads();
+        }
+    }
+}
+
+// Position at step s of element e (unselected before s).
+__device__ __forceinline__ int position_at(const int* src, int e, int s) {
+    int q = e;
+    while (q < s) q = src[q];
+    return q;
+}
+
+// The selection-sort order of K candidates whose (~key, id) pairs are sorted
+// ascending in comp[0, K): ids[r] = the id selected at step r.  Positions
+// (src[r] = where the element selected at step r stood then) are computed up
+// to the end of the last run of equal values, the only steps whose order
+// depends on positions; comp[K, 3K) is the scratch of the runs' sorts.
+__device__ void selection_order(uint64_t* comp, int K, int* ids, int* src, bool global) {
+    __shared__ int s_last, s_i, s_i1;
+    const int t = threadIdx.x;
+    if (t == 0) { s_last = 0; s_i = 0; }
+    __syncthreads();
+    for (int i = t; i < K; i += SWG) {
+        ids[i] = (int)(uint32_t)comp[i];
+        if (i + 1 < K && (comp[i] >> 32) == (comp[i + 1] >> 32)) atomicMax(&s_last, i + 2);
+    }
+    if (global) __threadfence();
+    __syncthreads();
+    const int R = s_last;   // ranks [0, R) need positions; [R, K) follow the value order
+    uint64_t* tmp = comp + K;
+    while (R > 0) {
+        if (t == 0) {
+            // singleton steps in order, up to the next run of equal values
+            int i = s_i, i1 = i;
+            while (i < R) {
+                i1 = i + 1;
+                const uint64_t k = comp[i] >> 32;
+                while (i1 < K && (comp[i1] >> 32) == k) i1++;
+                if (i1 - i > 1) break;
+                src[i] = position_at(src, ids[i], i);
+                i++;
+            }
+            s_i = i;
+            s_i1 = i1;
+        }
+        if (global) __threadfence();
+        __syncthreads();
+        const int i = s_i, i1 = s_i1;
+        if (i >= R) break;
+        // the run [i, i1): members leave in the order of their positions at step i
+        const int g = i1 - i;
+        int P = 1;
+        while (P < g) P <<= 1;
+        for (int j = t; j < P; j += SWG) {
+            uint64_t v = ~0ull;
+            if (j < g) {
+                const int e = ids[i + j];
+                v = ((uint64_t)(uint32_t)position_at(src, e, i) << 32) | (uint32_t)e;
+            }
+            tmp[j] = v;
+        }
+        if (global) __threadfence();
+        __syncthreads();
+        bitonic_asc(tmp, P, global);
+        for (int j = t; j < g; j += SWG) {
+            ids[i + j] = (int)(uint32_t)tmp[j];
+            src[i + j] = (int)(tmp[j] >> 32);
+        }
+        if (global) __threadfence();
+        __syncthreads();
+        if (t == 0) s_i = i1;
+        __syncthreads();
+    }
+    __syncthreads();
+}
+
+// Rank r's value as the reference writes it (the aliased chain), for r < K.
+__device__ __forceinline__ float aliased_value(const float* p, const int* ids, int r) {
+    int a = r;
+    while (ids[a] < a) a = ids[a];
+    return p[ids[a]];
+}
+
+// FindNucleus over K candidates (comp: (~key, id) pairs sorted in [0, K), 3K
+// slots; ids, val: K each), then the draw.  Returns the token (or the rank, when the nucleus spans
+// all n), or -1 when the running sum does not reach TopP within K < n.
+__device__ int nucleus_draw(const float* p, int n, uint64_t* comp, int K, int* ids, float* val, float top_p, float r,
+                            bool global) {
+    __shared__ int s_res;
+    const int t = threadIdx.x;
+    int* src = reinterpret_cast<int*>(val);   // positions first, values after
+    selection_order(comp, K, ids, src, global);
+    for (int i = t; i < K; i += SWG) val[i] = aliased_value(p, ids, i);
+    if (global) __threadfence();
+    __syncthreads();
+    if (t == 0) {
+        // FindNucleus's running sum (Sampler.cs:146-154)
+        float cum = 0.f;
+        int count = -1;
+        for (int i = 0; i < K; i++) {
+            cum += val[i];
+            if (cum >= top_p) { count = i + 1; break; }
+        }
+        if (count < 0 && K == n) count = n;
+        int res = -1;
+        if (count > 0 && count < n) {
+            // Sampler.cs:51-57: sum, Scale(1f / sum), the draw over the nucleus
+            float sum = 0.f;
+            for (int i = 0; i < count; i++) sum += val[i];
+            const float f = 1.0f / sum;
+            float c2 = 0.f;
+            int pick = count - 1;
+            for (int i = 0; i < count; i++) {
+#pragma clang fp contract(off)
+                c2 += val[i] * f;
+                if (r <= c2) { pick = i; break; }
+            }
+            res = ids[pick];
+        } else if (count == n) {
+            // Sampler.cs:61 over the rewritten buffer: a rank is returned
+            float c = 0.f;
+            res = n - 1;
+            for (int i = 0; i < n; i++) {
+                c += val[i];
+                if (r <= c) { res = i; break; }
+            }
+        }
+        s_res = res;
+    }
+    __syncthreads();
+    return s_res;
+}
+
+// Top-p nucleus and the draw (Sampler.cs:44-61) over the probabilities in
+// work[0, n); the rest of work is the slow path's scratch (sample_work_floats).
 __global__ __launch_bounds__(SWG) void samp_nucleus_kernel(SampleArgs a) {
     __shared__ double dtmp[2 * NWAVE + 1];
-    __shared__ int s_pick;
+    __shared__ int s_pick, s_cnt;
+    __shared__ uint64_t l_comp[3 * NUC_LDS];
+    __shared__ int l_ids[NUC_LDS];
+    __shared__ float l_val[NUC_LDS];
     const int n = a.n, t = threadIdx.x;
     const float* p = a.work;
-    const double r = (double)a.rvals[*a.step - 1];
-    bool nucleus = false;
-    Descent D1{};
-    int j1 = 0, m = n;
+    const float rf = a.rvals[*a.step - 1];
     if (a.top_p < 1.f) {
-        // FindNucleus: the shortest prefix, by descending probability, whose sum reaches TopP
-        const double T1 = (double)a.top_p;
-        D1 = descend<true>(p, n, T1);
-        const double w1 = (double)keyf(D1.key);
-        j1 = D1.n_eq;
-        if (w1 > 0.0) {
-            const double need = ceil((T1 - D1.above) / w1);
-            j1 = (int)fmin(fmax(need, 1.0), (double)D1.n_eq);
-        }
-        m = D1.cnt_above + j1;
-        nucleus = m < n;
-    }
-    if (nucleus) {
-        // renormalised draw inside the nucleus: the element at which the
-        // running sum first reaches r * (nucleus sum)
-        const double S = D1.above + (double)j1 * (double)keyf(D1.key);
-        const Descent D2 = descend<true>(p, n, r * S);
-        uint32_t K = D2.key;
-        int j = D2.n_eq;
-        const double w2 = (double)keyf(D2.key);
-        if (w2 > 0.0) j = (int)fmin(fmax(ceil((r * S - D2.above) / w2), 1.0), (double)D2.n_eq);
-        if (D2.cnt_above + j > m) {   // past the nucleus (rounding): its last element
-            K = D1.key;
-            j = j1;
-        }
-        const int idx = jth_equal(p, n, K, j);
-        if (t == 0) s_pick = idx;
-    } else {
-        // SampleFromProbabilities over all n in index order
-        const int seg = (n + SWG - 1) / SWG;
-        const int b = t * seg, e = min(n, b + seg);
-        double sum = 0.0;
-        for (int i = b; i < e; i++) sum += (double)p[i];
-        double total;
-        const double off = block_excl_scan<double>(sum, dtmp, &total);
-        if (t == 0) s_pick = n - 1;
-        __syncthreads();
-        if (off < r && r <= off + sum) {
-            double c = off;
-            for (int i = b; i < e; i++) {
-                c += (double)p[i];
-                if (r <= c) { s_pick = i; break; }
+        // candidates: every element at or above the value where the fp64 mass reaches TopP + 1e-4
+        const Descent D = descend<true>(p, n, (double)a.top_p + 1e-4);
+        const int K = D.cnt_above + D.n_eq;
+        int res = -1;
+        if (K <= NUC_LDS) {
+            if (t == 0) s_cnt = 0;
+            __syncthreads();
+            for (int i = t; i < n; i += SWG) {
+                const uint32_t k = fkey(p[i]);
+                if (k >= D.key) {
+                    const int o = atomicAdd(&s_cnt, 1);
+                    if (o < NUC_LDS) l_comp[o] = ((uint64_t)(~k) << 32) | (uint32_t)i;
+                }
             }
-        } else if (t == 0 && r <= 0.0) {
-            s_pick = 0;
+            int P = 1;
+            while (P < K) P <<= 1;
+            __syncthreads();
+            for (int i = K + t; i < P; i += SWG) l_comp[i] = ~0ull;
+            __syncthreads();
+            bitonic_asc(l_comp, P, false);
+            res = nucleus_draw(p, n, l_comp, K, l_ids, l_val, a.top_p, rf, false);
         }
+        if (res < 0) {
+            // all n in global scratch
+            int P = 1;
+            while (P < n) P <<= 1;
+            uint64_t* comp = reinterpret_cast<uint64_t*>(a.work + sample_comp_offset(n));
+            int* ids = reinterpret_cast<int*>(a.work + sample_comp_offset(n) + 6 * (size_t)n);
+            float* val = a.work + sample_comp_offset(n) + 7 * (size_t)n;
+            for (int i = t; i < P; i += SWG)
+                comp[i] = i < n ? ((uint64_t)(~fkey(p[i])) << 32) | (uint32_t)i : ~0ull;
+            __threadfence();
+            __syncthreads();
+            bitonic_asc(comp, P, true);
+            res = nucleus_draw(p, n, comp, n, ids, val, a.top_p, rf, true);
+        }
+        if (t == 0) publish(a, res < 0 ? n - 1 : res);
+        return;
+    }
+    // SampleFromProbabilities over all n in index order (Sampler.cs:61)
+    const double r = (double)rf;
+    const int seg = (n + SWG - 1) / SWG;
+    const int b = t * seg, e = min(n, b + seg);
+    double sum = 0.0;
+    for (int i = b; i < e; i++) sum += (double)p[i];
+    double total;
+    const double off = block_excl_scan<double>(sum, dtmp, &total);
+    if (t == 0) s_pick = n - 1;
+    __syncthreads();
+    if (off < r && r <= off + sum) {
+        double c = off;
+        for (int i = b; i < e; i++) {
+            c += (double)p[i];
+            if (r <= c) { s_pick = i; break; }
+        }
+    } else if (t == 0 && r <= 0.0) {
+        s_pick = 0;
     }
     __syncthreads();
     if (t == 0) publish(a, s_pick < 0 ? n - 1 : s_pick);

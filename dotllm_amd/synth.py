@@ -112,17 +112,19 @@ def synth_tensor(ggml_type: int, rows: int, cols: int, seed: int, out: np.ndarra
 
 
 def tensor_sigma(name: str, spec: dict, sigma: float, scaled_init: bool) -> float:
-    """Init std of a tensor: sigma, and sigma / sqrt(2 L) for the two projections
-    that write into the residual stream (attn_output, ffn_down) when
-    scaled_init, the usual scaled initialisation of an L-layer transformer; it
-    keeps the residual stream from growing layer by layer."""
+    """Init std of a tensor: sigma for every matrix (the workloads' stated
+    init, N(0, 0.02) everywhere).  With scaled_init, the two projections that
+    write into the residual stream (attn_output, ffn_down) take
+    sigma / sqrt(2 L) instead, the usual scaled initialisation of an L-layer
+    transformer, which keeps the residual stream from growing layer by layer;
+    it is an option, not the default."""
     if scaled_init and (".attn_output." in name or ".ffn_down." in name):
         return sigma / float(np.sqrt(2.0 * spec["layers"]))
     return sigma
 
 
 def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
-                threads: int | None = None, spec: dict | None = None, scaled_init: bool = True,
+                threads: int | None = None, spec: dict | None = None, scaled_init: bool = False,
                 eos: int = -1, tied: bool = False, norm_type: int = F32) -> np.ndarray:
     """Builds the whole GGUF file image in memory (uint8 numpy array).
 

@@ -15,28 +15,28 @@ Outputs (small, committed):
                   32 greedy tokens and, per step, the top-5 logits and the
                   logits' sum and sum of squares
 
-  python tests/golden/make_golden.py mistral7b    (about 20 minutes on 8 cores)
-  python tests/golden/make_golden.py floor7b      (adds the order-1 floor to it)
-  python tests/golden/make_golden.py long c3|c4|c5   (10-40 minutes each)
+  python tests/golden/make_golden.py long KEY     (KEY below; 5-60 minutes each)
 
-  mistral7b_greedy64.json  7B-shape Q4_K_M model (seed 1234), 16-token prompt
-                  (seed 7), with fp16 and with fp32 KV: 64 greedy tokens and,
-                  per step, the top-16 logits, the top-2 gap, and the logits'
-                  mean and root mean square; plus a fingerprint of the image
-                  (floor7b adds, per step, the order-1 floor described below)
-
-  long_<config>.npz  the full-size workloads, from the oracle's batched prompt
-                  path (orc_prefill, bitwise the sequential loop) with greedy
-                  decoding after it:
-                    c3  llama1b,   512-token prompt + 256 tokens, fp32 KV
-                    c4  mistral7b, 2048-token prompt + 16 tokens, fp16 KV
-                    c5  phi3mini,  2048-token prompt + 256 tokens, fp32 KV
-                  per step: the top-16 logits, the top-2 gap, the logits' mean
-                  and root mean square; the KV rows of a few (layer, position)
-                  pairs; and per step the floor: max |logit difference| between
-                  the oracle in the reference's reduction order and in another
-                  valid fp32 order (orc_set_order(1)), teacher-forced on the same
-                  tokens -- what summation order alone moves the results by
+  long_<KEY>.npz  the full-size workloads and the 7B greedy-64 runs, from the
+                  oracle's batched prompt path (orc_prefill, bitwise the
+                  sequential loop) with greedy decoding after it; every model
+                  is the seeded synthetic image with N(0, 0.02) on every matrix:
+                    c3     llama1b,   512-token prompt + 256 tokens, fp32 KV
+                    c3h    llama1b,   512-token prompt + 256 tokens, fp16 KV
+                    c4     mistral7b, 2048-token prompt + 64 tokens, fp16 KV
+                    c5     phi3mini,  2048-token prompt + 256 tokens, fp32 KV
+                    c5h    phi3mini,  2048-token prompt + 256 tokens, fp16 KV
+                    7b64h  mistral7b, 16-token prompt + 64 tokens, fp16 KV
+                    7b64   mistral7b, 16-token prompt + 64 tokens, fp32 KV
+                  per step: the top-256 logits, the logits at 4096 fixed
+                  indices (sample_indices), the top-2 gap, the logits' mean and
+                  root mean square; the whole logits vector at the first and
+                  last step; the KV rows of a few (layer, position) pairs; and
+                  per step the floor: max |logit difference| over the whole
+                  vector between the oracle in the reference's reduction order
+                  and in another valid fp32 order (orc_set_order(1)),
+                  teacher-forced on the same tokens -- what summation order
+                  alone moves the results by
 """
 import json
 import os
@@ -113,34 +113,20 @@ def image_fingerprint(img) -> str:
     return h.hexdigest()
 
 
-def mistral7b_greedy64():
-    img = synth.build_image("mistral7b", seed=1234, context=96)
-    prompt = synth.prompt(32000, 16, seed=7)
-    O.set_threads(os.cpu_count() or 1)
-    runs = []
-    for kv_fp16 in (True, False):
-        m = O.Model(img, kv_fp16=kv_fp16, context=96)
-        toks, logits = m.generate(prompt, 64, return_logits=True)
-        m.close()
-        steps = []
-        for row in logits:
-            top = np.argsort(row)[::-1][:16]
-            r64 = row.astype(np.float64)
-            steps.append({"top16": [int(i) for i in top], "top16_logits": [float(row[i]) for i in top],
-                          "gap": float(row[top[0]] - row[top[1]]), "mean": float(r64.mean()),
-                          "rms": float(np.sqrt(np.mean(r64 * r64)))})
-        runs.append({"kv_fp16": kv_fp16, "tokens": [int(t) for t in toks], "steps": steps})
-        print(f"kv_fp16={kv_fp16}: {len(toks)} tokens", flush=True)
-    with open(os.path.join(HERE, "mistral7b_greedy64.json"), "w") as f:
-        json.dump({"model": "mistral7b", "weights_seed": 1234, "image_context": 96, "prompt_seed": 7,
-                   "prompt": [int(t) for t in prompt], "image_fingerprint": image_fingerprint(img),
-                   "runs": runs}, f, indent=1)
-    print("wrote mistral7b_greedy64.json")
+N_TOP = 256        # logits kept per step: the oracle's top N_TOP ...
+N_SAMPLE = 4096    # ... and N_SAMPLE at fixed indices drawn once per vocabulary
+INIT = "N(0, 0.02) on every matrix (scaled_init=False), RMSNorm weights 1.0"
+
+
+def sample_indices(vocab, seed=97):
+    """The N_SAMPLE vocabulary indices every step of a fixture stores (sorted)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return np.sort(rng.choice(vocab, size=min(N_SAMPLE, vocab), replace=False)).astype(np.int32)
 
 
 def step_stats(row):
-    """Top-16 indices and values (descending), top-2 gap, mean and RMS of one logits row."""
-    top = np.argsort(row, kind="stable")[::-1][:16]
+    """Top-N_TOP indices and values (descending, ties by index), top-2 gap, mean and RMS of one logits row."""
+    top = np.argsort(-row, kind="stable")[:N_TOP]
     r64 = row.astype(np.float64)
     return top, row[top], float(row[top[0]] - row[top[1]]), float(r64.mean()), float(np.sqrt(np.mean(r64 * r64)))
 
@@ -148,20 +134,25 @@ def step_stats(row):
 LONG = {
     # name: (model, prompt tokens, generated tokens, fp16 KV, KV sample layers, KV sample positions)
     "c3": ("llama1b", 512, 256, False, (0, 7, 15), (0, 1, 255, 511, 700)),
-    "c4": ("mistral7b", 2048, 16, True, (0, 15, 31), (0, 1, 1023, 2047, 2060)),
+    "c3h": ("llama1b", 512, 256, True, (0, 7, 15), (0, 1, 255, 511, 700)),
+    "c4": ("mistral7b", 2048, 64, True, (0, 15, 31), (0, 1, 1023, 2047, 2100)),
     "c5": ("phi3mini", 2048, 256, False, (0, 15, 31), (0, 1, 1023, 2047, 2250)),
+    "c5h": ("phi3mini", 2048, 256, True, (0, 15, 31), (0, 1, 1023, 2047, 2250)),
+    "7b64h": ("mistral7b", 16, 64, True, (0, 15, 31), (0, 15, 16, 50, 78)),
+    "7b64": ("mistral7b", 16, 64, False, (0, 15, 31), (0, 15, 16, 50, 78)),
 }
 
 
 def long_run(key):
-    """Greedy run of one full-size workload in the reference's order, and the
-    same tokens teacher-forced through the order-1 oracle for the floor."""
+    """Greedy run of one workload in the reference's order, and the same tokens
+    teacher-forced through the order-1 oracle for the floor."""
     import time
     name, n_prompt, n_gen, kv_fp16, layers, positions = LONG[key]
     ctx = n_prompt + n_gen + 8
     img = synth.build_image(name, seed=1234, context=ctx)
     vocab = synth.SPECS[name]["vocab"]
     prompt = synth.prompt(vocab, n_prompt, seed=7)
+    sidx = sample_indices(vocab)
     O.set_threads(int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1)))
     m0 = O.Model(img, kv_fp16=kv_fp16, context=ctx)
     m1 = O.Model(img, kv_fp16=kv_fp16, context=ctx)
@@ -172,13 +163,17 @@ def long_run(key):
     l1 = m1.prefill(prompt, 0)
     O.set_order(0)
     print(f"{key}: prompt of {n_prompt} in {time.time() - t0:.0f}s", flush=True)
-    toks, tidx, tval, gap, mean, rms, floor = [], [], [], [], [], [], []
+    full_steps = sorted({0, n_gen - 1})
+    toks, tidx, tval, sval, gap, mean, rms, floor, full = [], [], [], [], [], [], [], [], []
     for s in range(n_gen):
         ti, tv, g, mu, r = step_stats(l0)
         tok = O.argmax(l0)
         assert tok == int(ti[0])
-        toks.append(tok); tidx.append(ti); tval.append(tv); gap.append(g); mean.append(mu); rms.append(r)
+        toks.append(tok); tidx.append(ti); tval.append(tv); sval.append(l0[sidx]); gap.append(g)
+        mean.append(mu); rms.append(r)
         floor.append(float(np.max(np.abs(l1 - l0))))
+        if s in full_steps:
+            full.append(l0.copy())
         if s + 1 < n_gen:
             O.set_order(0)
             l0 = m0.prefill([tok], n_prompt + s)
@@ -200,59 +195,20 @@ def long_run(key):
             kv["v_floor"][i, j] = np.max(np.abs(v1 - v0))
     m0.close(); m1.close()
     meta = dict(config=key, model=name, weights_seed=1234, prompt_seed=7, n_prompt=n_prompt, n_gen=n_gen,
-                kv_fp16=kv_fp16, image_context=ctx, image_fingerprint=image_fingerprint(img))
+                kv_fp16=kv_fp16, image_context=ctx, image_fingerprint=image_fingerprint(img), init=INIT,
+                n_top=N_TOP, n_sample=int(sidx.size), sample_seed=97)
     np.savez_compressed(os.path.join(HERE, f"long_{key}.npz"), meta=np.array(json.dumps(meta)),
                         prompt=np.asarray(prompt, np.int32), tokens=np.asarray(toks, np.int32),
                         top_idx=np.asarray(tidx, np.int32), top_val=np.asarray(tval, np.float32),
+                        sample_idx=sidx, sample_val=np.asarray(sval, np.float32),
+                        full_steps=np.asarray(full_steps, np.int32), full_val=np.asarray(full, np.float32),
                         gap=np.asarray(gap), mean=np.asarray(mean), rms=np.asarray(rms), floor=np.asarray(floor),
                         kv_layers=np.asarray(layers, np.int32), kv_positions=np.asarray(positions, np.int32), **kv)
     print(f"wrote long_{key}.npz in {time.time() - t0:.0f}s; max floor {max(floor):.3e}", flush=True)
 
 
-def floor7b():
-    """Adds to mistral7b_greedy64.json, per step of each run, the order-1 floor:
-    the reference-order logits are recomputed through orc_prefill (and must
-    equal the fixture's bit for bit), the order-1 logits on the same tokens."""
-    path = os.path.join(HERE, "mistral7b_greedy64.json")
-    with open(path) as f:
-        g = json.load(f)
-    img = synth.build_image(g["model"], seed=g["weights_seed"], context=g["image_context"])
-    assert image_fingerprint(img) == g["image_fingerprint"]
-    O.set_threads(int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1)))
-    prompt = g["prompt"]
-    for run in g["runs"]:
-        m0 = O.Model(img, kv_fp16=run["kv_fp16"], context=g["image_context"])
-        m1 = O.Model(img, kv_fp16=run["kv_fp16"], context=g["image_context"])
-        O.set_order(0)
-        l0 = m0.prefill(prompt, 0)
-        O.set_order(1)
-        l1 = m1.prefill(prompt, 0)
-        O.set_order(0)
-        for s, st in enumerate(run["steps"]):
-            top = st["top16"]
-            assert [int(i) for i in np.argsort(l0, kind="stable")[::-1][:16]] == top
-            assert np.array_equal(l0[top], np.asarray(st["top16_logits"], np.float32)), s
-            st["floor"] = float(np.max(np.abs(l1 - l0)))
-            if s + 1 < len(run["steps"]):
-                tok = run["tokens"][s]
-                O.set_order(0)
-                l0 = m0.prefill([tok], len(prompt) + s)
-                O.set_order(1)
-                l1 = m1.prefill([tok], len(prompt) + s)
-                O.set_order(0)
-        m0.close(); m1.close()
-        print(f"kv_fp16={run['kv_fp16']}: max floor {max(st['floor'] for st in run['steps']):.3e}", flush=True)
-    with open(path, "w") as f:
-        json.dump(g, f, indent=1)
-    print("updated mistral7b_greedy64.json")
-
-
 if __name__ == "__main__":
-    if sys.argv[1:] == ["mistral7b"]:
-        mistral7b_greedy64()
-    elif sys.argv[1:] == ["floor7b"]:
-        floor7b()
-    elif len(sys.argv) == 3 and sys.argv[1] == "long":
+    if len(sys.argv) == 3 and sys.argv[1] == "long":
         long_run(sys.argv[2])
     else:
         main()

@@ -9,13 +9,16 @@ bitwise the sequential ProcessToken loop in the reference order
 (tests/test_oracle_prefill.py) and applies order 1 to every reduction.
 
 Bounds built from it (logit_bounds): a step's logits within
-max(2e-2, 2 x the running maximum of the floor up to that step); greedy tokens
-compared up to the first top-2 gap below max(1e-2, twice that bound's floor
-part).  The factor 2: one reordering is one sample of the order noise, not an
-upper bound for another implementation, and the device departs from the
-reference's order in every reduction at once (and uses 24-bit activations in
-the GEMVs, two fp16 activation planes in the prompt GEMMs); measured device
-errors ran at 0.45 to 1.35 times the floor of the same steps.
+max(2e-2, FLOOR_MARGIN x the running maximum of the floor up to that step);
+greedy tokens compared up to the first top-2 gap below max(1e-2, twice that
+bound's floor part).  The margin: one reordering is one sample of the order
+noise, not an upper bound for another implementation, and the device departs
+from the reference's order in every reduction at once (and uses 24-bit
+activations in the GEMVs, two fp16 activation planes in the prompt GEMMs).  It
+is set just above the largest ratio of device error to the same step's
+running floor measured over every model test and fixture with N(0, 0.02)
+weights on every matrix (1.64: the Phi-3-mini shape with fp16 KV, step 4 of
+its 8-step run).
 """
 import numpy as np
 
@@ -23,13 +26,19 @@ from oracle import oracle as O
 
 LOGIT_TOL = 2e-2
 NEAR_TIE = 1e-2
-FLOOR_MARGIN = 2.0
+FLOOR_MARGIN = 1.75
 
 
 def logit_bounds(floors):
-    """Per step: (max(2e-2, 2 x running max of floors), max(1e-2, 4 x running max))."""
+    """Per step: (max(2e-2, FLOOR_MARGIN x running max of floors), max(1e-2, 2 FLOOR_MARGIN x running max))."""
     run = np.maximum.accumulate(np.asarray(floors, dtype=np.float64))
     return np.maximum(LOGIT_TOL, FLOOR_MARGIN * run), np.maximum(NEAR_TIE, 2 * FLOOR_MARGIN * run)
+
+
+def floor_ratio(errors, floors):
+    """max over steps of errors[s] / (running max of floors up to s)."""
+    run = np.maximum.accumulate(np.asarray(floors, dtype=np.float64))[:len(errors)]
+    return float(np.max(np.asarray(errors, dtype=np.float64) / np.maximum(run, 1e-30)))
 
 
 class OraclePair:
@@ -73,6 +82,11 @@ class OraclePair:
     def bounds(self):
         """logit_bounds of the calls so far: (logit bound, near-tie threshold) per call."""
         return logit_bounds(self.floors)
+
+    def floor_ratio(self, errors):
+        """Largest error / running floor over the calls so far (how close the device
+        runs to the order noise; the bound allows FLOOR_MARGIN)."""
+        return floor_ratio(errors, self.floors)
 
     def close(self):
         self.m0.close()

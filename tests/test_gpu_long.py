@@ -1,21 +1,32 @@
-"""The full-size workloads against the oracle's frozen runs (tests/golden/long_*.npz,
-written by tests/golden/make_golden.py from the oracle's batched prompt path,
-which is bitwise the sequential loop of InferenceEngine.cs:84-88):
+"""The full-size workloads and the 7B greedy-64 runs against the oracle's frozen
+runs (tests/golden/long_*.npz, written by tests/golden/make_golden.py from the
+oracle's batched prompt path, which is bitwise the sequential loop of
+InferenceEngine.cs:84-88).  Every model carries the stated init, N(0, 0.02) on
+every matrix:
 
-  c3  1B shape, Q4_K_M mix:      512-token prompt, 256 greedy tokens, fp32 KV
-  c4  7B shape, Q4_K_M mix:      2048-token prompt, 16 greedy tokens, fp16 KV
-  c5  Phi-3-mini shape, Q6_K/Q8_0: 2048-token prompt, 256 greedy tokens, fp32 KV
+  c3     1B shape, Q4_K_M mix:        512-token prompt, 256 greedy tokens, fp32 KV
+  c3h    the same with fp16 KV (the format the decode bench times)
+  c4     7B shape, Q4_K_M mix:        2048-token prompt, 64 greedy tokens, fp16 KV
+  c5     Phi-3-mini shape, Q6_K/Q8_0: 2048-token prompt, 256 greedy tokens, fp32 KV
+  c5h    the same with fp16 KV
+  7b64h  7B shape:                    16-token prompt, 64 greedy tokens, fp16 KV
+  7b64   the same with fp32 KV
 
 The device processes each prompt as batched MFMA GEMMs (the prefill path), then
 decodes with the captured step.  Bars, per step s:
-  * logits (the oracle's top 16, and the mean and RMS of the whole vector, both
-    1-Lipschitz in the max norm) within bound(s) = max(2e-2, 2 floor(s)), where
-    floor(s) is the running maximum, over steps <= s, of how far the oracle's
-    own logits move when only its summation order changes (orc_set_order(1),
-    teacher-forced on the same tokens, stored in the fixture; the factor 2 is
-    explained in tests/oracle_pair.py);
+  * the logits' max absolute error within bound(s) = max(2e-2, 1.75 floor(s)),
+    where floor(s) is the running maximum, over steps <= s, of how far the
+    oracle's own logits move (max over the whole vocabulary) when only its
+    summation order changes (orc_set_order(1), teacher-forced on the same
+    tokens, stored in the fixture; the factor is explained in
+    tests/oracle_pair.py).  The error is taken over every logit the fixture
+    holds: the oracle's top 256 and 4096 fixed indices at every step, the whole
+    vocabulary at the first and last step, and the mean and RMS of the whole
+    vector (both 1-Lipschitz in the max norm);
   * greedy tokens identical up to the oracle's first step whose top-2 gap is
-    below max(1e-2, 4 floor(s)) (a near-tie at that error);
+    below max(1e-2, 3.5 floor(s)) (a near-tie at that error), and at least as far
+    as the device was measured to agree (MIN_SAME: the device is
+    deterministic, so a shorter run is a regression);
   * the same argmax, teacher-forced, wherever the gap is at least that;
   * the fresh engine's first prefill (inside generate_all: workspace allocated
     and zeroed just before) and the re-run after reset give bit-identical
@@ -34,14 +45,16 @@ import pytest
 
 from dotllm_amd import synth
 from dotllm_amd.engine import InferenceEngine, LoadedModel, greedy
-from oracle_pair import logit_bounds
+from oracle_pair import floor_ratio, logit_bounds
 
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-LOGIT_TOL = 2e-2
-NEAR_TIE = 1e-2
 KV_TOL = 1e-3
+
+# free-running greedy tokens the device was measured to share with the oracle
+# (identical prefix length); a run shorter than this is a regression
+MIN_SAME = {"c3": 0, "c3h": 0, "c4": 0, "c5": 0, "c5h": 0, "7b64h": 0, "7b64": 0}
 
 
 def _fixture(key):
@@ -52,12 +65,18 @@ def _fixture(key):
     return {k: z[k] for k in z.files}, json.loads(str(z["meta"]))
 
 
-def _err(row, z, s):
-    """Max of |logit - oracle| at the oracle's top 16, |mean - mean|, |rms - rms|."""
-    idx = z["top_idx"][s]
+def step_error(row, z, s):
+    """Max absolute logit error of one step over what the fixture holds: the
+    oracle's top 256, the fixed sample, the whole vector where kept, and the
+    mean and RMS of the whole vector."""
     r64 = row.astype(np.float64)
-    return max(float(np.max(np.abs(row[idx] - z["top_val"][s]))), abs(float(r64.mean()) - z["mean"][s]),
-               abs(float(np.sqrt(np.mean(r64 * r64))) - z["rms"][s]))
+    e = max(float(np.max(np.abs(row[z["top_idx"][s]] - z["top_val"][s]))),
+            float(np.max(np.abs(row[z["sample_idx"]] - z["sample_val"][s]))),
+            abs(float(r64.mean()) - z["mean"][s]), abs(float(np.sqrt(np.mean(r64 * r64))) - z["rms"][s]))
+    hit = np.where(z["full_steps"] == s)[0]
+    if hit.size:
+        e = max(e, float(np.max(np.abs(row - z["full_val"][hit[0]]))))
+    return e
 
 
 def _run(hip, key):
@@ -75,7 +94,7 @@ def _run(hip, key):
     try:
         toks, logits = eng.generate_all(prompt, greedy(n_gen), return_logits=True)
         same = next((i for i, (a, b) in enumerate(zip(toks, ref)) if a != b), n_gen)
-        free = [_err(logits[s], z, s) for s in range(min(well_posed + 1, n_gen))]
+        free = [step_error(logits[s], z, s) for s in range(min(same + 1, n_gen))]
         first_free = np.array(logits[0], copy=True)   # the fresh engine's first prefill
         del logits
         eng.reset()
@@ -87,7 +106,7 @@ def _run(hip, key):
         for s in range(n_gen):
             if s > 0:
                 row = eng.process_token(ref[s - 1], n_prompt + s - 1)
-            forced.append(_err(row, z, s))
+            forced.append(step_error(row, z, s))
             if int(np.argmax(row)) != ref[s] and not tie[s]:
                 flips.append(s)
         kv_err, kv_bound, kv_mag = [], [], []
@@ -103,13 +122,17 @@ def _run(hip, key):
         eng.dispose()
     forced, free = np.asarray(forced), np.asarray(free)
     ratio = forced / bound
+    w = int(ratio.argmax())
     print(f"{key} ({meta['model']}, {n_prompt}-token prompt, {n_gen} tokens, kv_fp16={meta['kv_fp16']}): "
-          f"free-running tokens identical for {same} steps (required {well_posed}); logit error free-running max "
-          f"{free.max():.3e}, teacher-forced max {forced.max():.3e} at step {int(forced.argmax())} "
-          f"(bound there {bound[int(forced.argmax())]:.3e}, largest error/bound {ratio.max():.2f}, "
-          f"floor max {z['floor'].max():.3e}); KV error max {max(kv_err):.3e} (bound {max(kv_bound):.3e})")
+          f"free-running tokens identical for {same} steps (required {max(well_posed, MIN_SAME[key])}, "
+          f"first near-tie at {well_posed}); logit error free-running max {free.max():.3e}, teacher-forced max "
+          f"{forced.max():.3e} at step {int(forced.argmax())}, first step {forced[0]:.3e}, last {forced[-1]:.3e}; "
+          f"largest error/bound {ratio[w]:.2f} at step {w} (bound {bound[w]:.3e}); largest error/floor "
+          f"{floor_ratio(forced, z['floor']):.2f}; floor max {z['floor'].max():.3e}; "
+          f"KV error max {max(kv_err):.3e} (bound {max(kv_bound):.3e})")
     assert cold_warm_same, "the first prefill of a fresh engine differs from the warm re-run"
     assert same >= well_posed
+    assert same >= MIN_SAME[key], f"greedy tokens identical for {same} steps, {MIN_SAME[key]} before"
     assert np.all(free <= bound[:len(free)])
     assert np.all(forced <= bound), [(s, forced[s], bound[s]) for s in np.where(forced > bound)[0][:5]]
     assert not flips, flips
@@ -121,7 +144,11 @@ def test_c3_llama1b_512_prompt_256_tokens(hip):
     _run(hip, "c3")
 
 
-def test_c4_mistral7b_2048_prompt(hip):
+def test_c3_llama1b_512_prompt_256_tokens_fp16_kv(hip):
+    _run(hip, "c3h")
+
+
+def test_c4_mistral7b_2048_prompt_64_tokens(hip):
     _run(hip, "c4")
 
 
@@ -129,11 +156,22 @@ def test_c5_phi3mini_2048_prompt_256_tokens(hip):
     _run(hip, "c5")
 
 
+def test_c5_phi3mini_2048_prompt_256_tokens_fp16_kv(hip):
+    _run(hip, "c5h")
+
+
+@pytest.mark.parametrize("key", ["7b64h", "7b64"])
+def test_mistral7b_greedy64(hip, key):
+    """The headline model, 64 greedy tokens after a 16-token prompt, fp16 KV
+    (the decode bench's format) and fp32 KV (the reference's)."""
+    _run(hip, key)
+
+
 def test_c4_batched_prompt_matches_device_decode_loop(hip):
     """The 7B 2048-token prompt through the batched MFMA path and through 2048
     captured decode steps of the same device (LLMDOT_HIP_SEQ_PREFILL=1): last
     logits within the fixture's first-step bound, KV rows at the sampled
-    positions within max(1e-3, their floor)."""
+    positions within max(1e-3, 2 x their floor)."""
     z, meta = _fixture("c4")
     img = synth.build_image(meta["model"], seed=meta["weights_seed"], context=meta["image_context"])
     prompt = z["prompt"].tolist()

@@ -8,7 +8,7 @@ fp32 KV cache against the pure reference, and with the fp16 KV cache against an
 oracle variant that rounds K/V through fp16 when storing; the tiny model's
 fp16-KV run is also held to the pure reference.  Deep random-init models move
 by more than 2e-2 under a mere change of summation order; there the bar is the
-measured floor (tests/oracle_pair.py), max(2e-2, 2 x floor).
+measured floor (tests/oracle_pair.py), max(2e-2, 1.75 x floor).
 """
 import numpy as np
 import pytest
@@ -99,7 +99,7 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE):
     """GPU decode with fp32 KV against the pure reference and with fp16 KV
     against the reference with K/V rounded through fp16 on store.
 
-    Bars per step s (tests/oracle_pair.py): logits within max(2e-2, 2 floor(s)),
+    Bars per step s (tests/oracle_pair.py): logits within max(2e-2, 1.75 floor(s)),
     floor(s) being the running maximum of how far the oracle's own logits move
     when only its summation order changes, teacher-forced on the reference's
     tokens.  A reordered fp32 sum can flip the reference's ExpApprox range
@@ -107,7 +107,7 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE):
     integer, pinned by tests/test_oracle.py), so deep random-init models move
     by far more than fp32 rounding under any reordering; the floor measures it
     instead of assuming it.  (1) The free-running greedy tokens equal the
-    reference's up to its first top-2 gap below max(near_tie_min, 2 floor(s));
+    reference's up to its first top-2 gap below max(near_tie_min, 3.5 floor(s));
     (2) teacher-forced on the reference's tokens, every step within the bound,
     the same argmax wherever the gap is at least that threshold."""
     img = synth.build_image(name, seed=1234, context=ctx)
@@ -143,7 +143,8 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE):
         same = next((i for i, (a, b) in enumerate(zip(toks, ref_toks)) if a != b), min(len(toks), len(ref_toks)))
         print(f"{name} kv_fp16={kv_fp16}: free-running tokens identical for {same} steps (required: {well_posed}), "
               f"max |dlogit| {err_free.max():.3e}; teacher-forced {n_gen} steps max |dlogit| {errs.max():.3e}; "
-              f"bound max {bound.max():.3e} (order floor max {max(pair.floors):.3e})")
+              f"bound max {bound.max():.3e} (order floor max {max(pair.floors):.3e}; largest error/floor "
+              f"{pair.floor_ratio(errs):.2f})")
         assert np.all(err_free <= bound[:k]), (kv_fp16, err_free, bound[:k])
         assert np.all(errs <= bound), (kv_fp16, errs, bound)
 
@@ -197,7 +198,7 @@ def test_mistral7b_long_context(hip, oracle_threads, mistral7b_long_image, ctx, 
     """The headline decode workload at its contexts: 7B shape, KV positions
     [0, ctx) filled with the same seeded values on both sides, then 3 steps
     from position ctx, teacher-forced on the oracle's greedy tokens.  Logits
-    within max(2e-2, 2 x the oracle's own summation-order floor) at every step;
+    within max(2e-2, 1.75 x the oracle's own summation-order floor) at every step;
     the same argmax wherever the oracle's top-2 gap is at least the near-tie
     threshold."""
     img = mistral7b_long_image
@@ -259,79 +260,6 @@ def test_weights_pinned_by_model(tiny_image):
     be.dispose()
 
 
-def _golden(name):
-    import json
-    import os
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
-    with open(path) as f:
-        return json.load(f)
-
-
-def test_mistral7b_greedy64_golden(hip):
-    """The headline model, 64 greedy tokens after a 16-token prompt, against
-    the oracle's run frozen in tests/golden/mistral7b_greedy64.json (written by
-    tests/golden/make_golden.py; about 20 CPU-minutes, too slow to repeat
-    here), with fp16 and with fp32 KV.  The fixture holds, per step, how far
-    the oracle's logits move when only its summation order changes; step s is
-    held to max(2e-2, 2 x the running maximum of that floor) (tests/oracle_pair.py).
-    Free-running: tokens identical up to the oracle's first top-2 gap below
-    max(1e-2, 4 x floor).
-    Teacher-forced on the oracle's tokens, every step: logits at the oracle's
-    top 16 within the bound, mean and RMS of the whole vector within it (both
-    are 1-Lipschitz in the max norm), and the same argmax wherever the gap is
-    at least that threshold and at least twice the step's measured error."""
-    from golden.make_golden import image_fingerprint
-    g = _golden("mistral7b_greedy64.json")
-    img = synth.build_image(g["model"], seed=g["weights_seed"], context=g["image_context"])
-    assert image_fingerprint(img) == g["image_fingerprint"], "the synthetic generator changed: rewrite the fixture"
-    prompt = g["prompt"]
-    assert synth.prompt(32000, len(prompt), seed=g["prompt_seed"]) == prompt
-    n_gen = len(g["runs"][0]["tokens"])
-    for run in g["runs"]:
-        kv_fp16 = run["kv_fp16"]
-        steps = run["steps"]
-        tol, tie_at = logit_bounds([st["floor"] for st in steps])   # per step
-        gaps = np.array([st["gap"] for st in steps])
-        ties = np.where(gaps < tie_at)[0]
-        well_posed = int(ties[0]) if ties.size else n_gen
-
-        def err_of(logits, st):
-            idx = np.array(st["top16"])
-            l64 = logits.astype(np.float64)
-            return max(float(np.max(np.abs(logits[idx] - np.array(st["top16_logits"], np.float32)))),
-                       abs(float(l64.mean()) - st["mean"]), abs(float(np.sqrt(np.mean(l64 * l64))) - st["rms"]))
-
-        eng = _engine(hip, img, kv_fp16, context=len(prompt) + n_gen + 8)
-        try:
-            toks, logits = eng.generate_all(prompt, greedy(n_gen), return_logits=True)
-            same = next((i for i, (a, b) in enumerate(zip(toks, run["tokens"])) if a != b), n_gen)
-            free = [err_of(logits[i], steps[i]) for i in range(min(well_posed + 1, n_gen))]
-            eng.reset()
-            stream = list(prompt) + list(run["tokens"])
-            forced, flips = [], []
-            for pos, tk in enumerate(stream[:len(prompt) + n_gen - 1]):
-                gl = eng.process_token(int(tk), pos)
-                if pos >= len(prompt) - 1:
-                    i = pos - (len(prompt) - 1)
-                    e = err_of(gl, steps[i])
-                    forced.append(e)
-                    # a different argmax is a failure unless the step's own logit error
-                    # explains it: the oracle's top two must lie within 2 e of each other
-                    if int(np.argmax(gl)) != steps[i]["top16"][0] and steps[i]["gap"] >= max(tie_at[i], 2 * e):
-                        flips.append(i)
-        finally:
-            eng.dispose()
-        forced, free = np.asarray(forced), np.asarray(free)
-        w = int(np.argmax(forced / tol))
-        print(f"mistral7b greedy64 kv_fp16={kv_fp16}: free-running tokens identical for {same} steps "
-              f"(required: {well_posed}), max error {free.max():.3e}; teacher-forced max error {forced.max():.3e} "
-              f"(step {int(np.argmax(forced))}); largest error/bound {forced[w] / tol[w]:.2f} at step {w} "
-              f"(bound {tol[w]:.3e})")
-        assert same >= well_posed, kv_fp16
-        assert np.all(free <= tol[:len(free)]) and np.all(forced <= tol), kv_fp16
-        assert not flips, (kv_fp16, flips)
-
-
 def _fresh_engine_env(img, env, context, kv_fp16=True):
     """An engine created with extra environment settings (read at model creation)."""
     import os
@@ -380,7 +308,7 @@ def test_attention_one_launch_matches_three(model, cached):
 @pytest.mark.parametrize("fused", ["1", "0"])
 def test_attention_paths_at_2048(oracle_threads, mistral7b_long_image, fused):
     """Either attention path of the 7B shape at a 2048-position seeded fp16
-    cache against the oracle, 3 teacher-forced steps within max(2e-2, 2 x the
+    cache against the oracle, 3 teacher-forced steps within max(2e-2, 1.75 x the
     oracle's summation-order floor)."""
     img = mistral7b_long_image
     pair = OraclePair(img, True, 2064)

@@ -5,16 +5,18 @@ top-k path (0 < TopK < n): the device does the reference's arithmetic (the same
 selection, VectorMath.Softmax summation order and sequential draw), so the token
 must equal the oracle's for every draw; the logits are continuous random values,
 so no two are equal.
-top-p path: the device places the nucleus boundary and the draw with fp64 sums,
-the reference with sequential float sums, so the token must equal the oracle's
-unless r or TopP lies within float rounding of a cumulative boundary; a mismatch
-is accepted only if the oracle itself returns the device's token for r or TopP
-moved by at most 1e-4.  The device computes the nucleus of the true
-probabilities: the oracle's FindNucleus with a buffer of its own
-(aliased=False).  The reference as written reuses the probability buffer for
-the sorted values (Sampler.cs:30, 48-50) and departs from that wherever a rank
-inside the nucleus holds a token id below its rank; where none does, the device
-matches the reference as written too (test_top_p_matches_reference_...).
+top-p path (TopP < 1): the device computes the reference as written -- the
+softmax in its summation order, FindNucleus's selection-sort order (ties
+included), the values it writes into the probability buffer it still reads
+from (Sampler.cs:30, 48-50, 150), the sequential float running sum, the
+renormalised draw, and the fall-through draw over the rewritten buffer, which
+returns a rank (Sampler.cs:61) -- so the token must equal the oracle's
+(aliased=True, the reference as written) for every draw, with no exemption.
+no top-p (TopP >= 1, TopK off): the draw over all n probabilities in index
+order is placed with fp64 running sums, the reference's with a sequential float
+sum, so the token must equal the oracle's unless r lies within float rounding
+of a cumulative boundary: a mismatch is accepted only if the oracle itself
+returns the device's token for r moved by at most 1e-4.
 """
 from dataclasses import replace
 
@@ -36,12 +38,12 @@ def opts(temperature, top_k, top_p=1.0, penalty=1.0, window=0):
                            repeat_penalty_window_size=window)
 
 
-def ref(x, o, recent, r, aliased=False):
+def ref(x, o, recent, r, aliased=True):
     return O.sample(x, o.temperature, o.top_k, o.top_p, o.repeat_penalty, o.repeat_penalty_window_size, recent, r,
                     aliased=aliased)
 
 
-def near_boundary(x, o, recent, r, tok, eps=1e-4, aliased=False):
+def near_boundary(x, o, recent, r, tok, eps=1e-4, aliased=True):
     for d in (eps / 16, -eps / 16, eps / 4, -eps / 4, eps, -eps):
         if ref(x, o, recent, min(max(r + d, 0.0), 1.0), aliased) == tok:
             return True
@@ -86,43 +88,89 @@ def test_top_k_with_repeat_penalty(hip):
             assert hip.sample(x, o, recent, r) == ref(x, o, recent, r), (pen, window, r)
 
 
-TOPP_CASES = [(100, 0, 0.5), (100, 100, 0.9), (4096, 0, 0.95), (4096, 0, 0.5), (4096, 0, 1.0), (32000, 0, 0.9),
-              (32000, 32000, 0.95), (37, 0, 0.9), (1000, 0, 0.01), (13, 0, 1.0)]
+TOPP_CASES = [(100, 0, 0.5), (100, 100, 0.9), (4096, 0, 0.95), (4096, 0, 0.5), (32000, 0, 0.9),
+              (32000, 32000, 0.95), (37, 0, 0.9), (1000, 0, 0.01), (1000, 0, 0.99999994), (13, 0, 0.99999994),
+              (5000, 0, 0.999), (8, 0, 0.7)]
+
+
+def aliasing_touches(x, o, top_p):
+    """Whether any rank inside the reference's nucleus (or the whole buffer,
+    when the nucleus spans all n) reads a slot already rewritten."""
+    p = np.exp((x / o.temperature - np.max(x / o.temperature)).astype(np.float64))
+    p /= p.sum()
+    order = np.argsort(-p, kind="stable")
+    m = min(int(np.searchsorted(np.cumsum(p[order]), top_p)) + 1, x.size)
+    return any(int(order[i]) < i for i in range(m))
 
 
 @pytest.mark.parametrize("n,k,top_p", TOPP_CASES)
-def test_top_p_matches_oracle(hip, n, k, top_p):
+def test_top_p_matches_reference(hip, n, k, top_p):
+    """Continuous random logits: every draw's token is the reference's as
+    written (the aliased buffers), exactly."""
     x = logits_for(n, n + 3, 2.0)
     o = opts(0.8, k, top_p)
+    for r in (R_ALL if n <= 5000 else R_FEW):
+        assert hip.sample(x, o, [], r) == ref(x, o, [], r), r
+
+
+@pytest.mark.parametrize("n,step,top_p", [(200, 0.5, 0.9), (4096, 0.25, 0.95), (4096, 1.0, 0.8), (1000, 0.5, 0.99999994),
+                                          (30, 2.0, 0.9)])
+def test_top_p_ties_match_reference(hip, n, step, top_p):
+    """Logits rounded to a grid, so many probabilities are exactly equal: the
+    reference's selection sort orders equal values by the positions its swaps
+    left them at, which decides which rewritten slots later ranks read; every
+    draw's token is the reference's, exactly."""
+    x = (np.round(logits_for(n, 31 + n, 2.0) / step) * step).astype(np.float32)
+    assert np.unique(x).size < n // 2 + 1
+    o = opts(0.8, 0, top_p)
+    for r in R_ALL:
+        assert hip.sample(x, o, [], r) == ref(x, o, [], r), r
+
+
+def test_top_p_aliasing_is_exercised():
+    """The cases above include nuclei in which ranks read rewritten slots, so
+    they would fail for the separate-buffer form (the oracle shows the two forms
+    differ on at least one of their draws)."""
+    differ = 0
+    for n, k, top_p in TOPP_CASES:
+        x = logits_for(n, n + 3, 2.0)
+        o = opts(0.8, k, top_p)
+        if not aliasing_touches(x, o, top_p):
+            continue
+        for r in (R_ALL if n <= 5000 else R_FEW):
+            differ += ref(x, o, [], r, aliased=True) != ref(x, o, [], r, aliased=False)
+    assert differ > 0
+
+
+def test_top_p_nucleus_spanning_all(hip):
+    """Ten tokens carry all but ~1.1e-4 of the mass and 9990 carry ~1.1e-8
+    each, below half an ulp of the running sum near 1, so FindNucleus's float
+    sum stalls at 0.9998741, under TopP = 0.99999994, and never closes: the
+    draw walks the rewritten buffer (Sampler.cs:61) and returns a rank.  The
+    device takes the same branch (all n candidates, its global-memory path) and
+    returns the same; a draw beyond the stalled sum returns the last rank."""
+    n = 10000
+    x = np.empty(n, np.float32)
+    x[:10] = -0.01 * np.arange(10)
+    x[10:] = -12.9 - 1e-5 * np.arange(n - 10)
+    o = opts(0.8, 0, 0.99999994)
+    want = [ref(x, o, [], r) for r in R_ALL]
+    assert want[-2:] == [n - 1, n - 1]            # r = 0.9999999 and 1.0 lie past the stalled sum
+    assert [hip.sample(x, o, [], r) for r in R_ALL] == want
+
+
+@pytest.mark.parametrize("n", [4096, 37])
+def test_temperature_only_matches_oracle(hip, n):
+    """TopP = 1, TopK off: the fp64-placed draw over the probabilities in index
+    order equals the reference's except within float rounding of a boundary."""
+    x = logits_for(n, n + 3, 2.0)
+    o = opts(0.8, 0, 1.0)
     mismatches = 0
-    for r in (R_ALL if n <= 4096 else R_FEW):
+    for r in R_ALL:
         want, got = ref(x, o, [], r), hip.sample(x, o, [], r)
         if got != want:
             mismatches += 1
             assert near_boundary(x, o, [], r, got), (r, want, got)
-    assert mismatches <= 1
-
-
-def test_top_p_matches_reference_without_back_reference(hip):
-    """Logits whose nucleus sits on high token ids (a block of 64 ids from
-    3000 raised by 8): no rank inside the nucleus holds an id below its rank,
-    so the reference as written (aliased buffers) and the device agree."""
-    n = 4096
-    x = logits_for(n, 77, 1.0)
-    x[3000:3064] += 8.0
-    o = opts(0.8, 0, 0.9)
-    p = np.exp((x - x.max()) / 0.8).astype(np.float64)
-    p /= p.sum()
-    order = np.argsort(-p, kind="stable")
-    m = int(np.searchsorted(np.cumsum(p[order]), 0.9)) + 1
-    assert m < 1000 and all(int(order[i]) >= i for i in range(m))
-    mismatches = 0
-    for r in R_ALL:
-        want, got = ref(x, o, [], r, aliased=True), hip.sample(x, o, [], r)
-        assert want == ref(x, o, [], r)
-        if got != want:
-            mismatches += 1
-            assert near_boundary(x, o, [], r, got, aliased=True), (r, want, got)
     assert mismatches <= 1
 
 
@@ -149,9 +197,7 @@ def test_generate_sampled(hip, tiny_image, top_k, top_p):
     assert len(toks) == n
     for i in range(n):
         recent = prompt + toks[:i]
-        want = ref(logits[i], s, recent, float(draws[i]))
-        if toks[i] != want:
-            assert top_k == 0 and near_boundary(logits[i], s, recent, float(draws[i]), toks[i]), i
+        assert toks[i] == ref(logits[i], s, recent, float(draws[i])), i
     m = O.Model(tiny_image, kv_fp16=False, context=64)
     pos = 0
     for t in prompt:

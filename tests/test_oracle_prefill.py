@@ -152,18 +152,34 @@ def _long(key):
     return z, json.loads(str(z["meta"]))
 
 
-@pytest.mark.parametrize("key", ["c3", "c4", "c5"])
+@pytest.mark.parametrize("key", ["c3", "c3h", "c4", "c5", "c5h", "7b64h", "7b64"])
 def test_long_fixture_consistent(key):
-    """tests/golden/long_<config>.npz: the prompt comes from its seed, each
-    token is the argmax of its step's stored logits (top 16 descending, gap =
-    top1 - top2), RMS >= |mean|, floors non-negative, KV samples finite."""
+    """tests/golden/long_<config>.npz: the prompt comes from its seed, the
+    model is the stated init, each token is the argmax of its step's stored
+    logits (top 256 descending, ties by index, gap = top1 - top2), the sampled
+    indices are the generator's, and at the steps whose whole vector is kept
+    the top, sampled, mean and RMS entries are that vector's; floors
+    non-negative, KV samples finite."""
+    from golden.make_golden import INIT, LONG, sample_indices
     z, meta = _long(key)
     name = meta["model"]
-    assert synth.prompt(synth.SPECS[name]["vocab"], meta["n_prompt"], seed=meta["prompt_seed"]) == z["prompt"].tolist()
+    assert meta["init"] == INIT and LONG[key][0] == name and LONG[key][3] == meta["kv_fp16"]
+    vocab = synth.SPECS[name]["vocab"]
+    assert synth.prompt(vocab, meta["n_prompt"], seed=meta["prompt_seed"]) == z["prompt"].tolist()
     n = meta["n_gen"]
-    assert z["tokens"].shape == (n,) and z["top_idx"].shape == (n, 16) and z["floor"].shape == (n,)
+    assert z["tokens"].shape == (n,) and z["top_idx"].shape == (n, 256) and z["floor"].shape == (n,)
+    assert np.array_equal(z["sample_idx"], sample_indices(vocab))
+    assert z["sample_val"].shape == (n, z["sample_idx"].size)
     assert np.array_equal(z["top_idx"][:, 0], z["tokens"])
     assert np.all(np.diff(z["top_val"], axis=1) <= 0)
     np.testing.assert_allclose(z["gap"], z["top_val"][:, 0] - z["top_val"][:, 1], rtol=0, atol=1e-6)
     assert np.all(z["rms"] >= np.abs(z["mean"])) and np.all(z["floor"] >= 0)
+    assert z["full_steps"].tolist() == sorted({0, n - 1})
+    for s, row in zip(z["full_steps"], z["full_val"]):
+        assert row.shape == (vocab,)
+        assert np.array_equal(row[z["top_idx"][s]], z["top_val"][s])
+        assert np.array_equal(row[z["sample_idx"]], z["sample_val"][s])
+        assert int(np.argmax(row)) == z["tokens"][s]
+        r64 = row.astype(np.float64)
+        assert r64.mean() == z["mean"][s] and np.sqrt(np.mean(r64 * r64)) == z["rms"][s]
     assert np.all(np.isfinite(z["k"])) and np.all(np.isfinite(z["v"]))
