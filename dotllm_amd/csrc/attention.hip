@@ -321,6 +321,31 @@ __device__ __forceinline__ void poll_max(const uint64_t (&v)[HW][4], float (&res
     }
 }
 
+// ---- XCD-local chunk-maximum exchange ----
+// The dispatcher deals a launch's workgroups to the eight XCDs in turn:
+// workgroup w runs on XCD (w + o) mod 8, o fixed for the launch (it varies from
+// launch to launch; checked at context creation).  With the kv heads a
+// multiple of 8, workgroup w serves kv head (w mod 8) + 8 j, so all chunks of a
+// kv head run on one XCD and exchange their maxima through its L2: plain
+// stores, and device-scope loads (cache policy sc1: past the CU's L1, served by
+// the L2), which see a store from the same XCD ~0.2 us after it completes
+// against ~1 us from another XCD (measured).  Each workgroup folds its own o
+// (from its XCC_ID register) into the tag it publishes, so a chunk placed on
+// another XCD never matches: its kv head's wait ends at the spin limit with the
+// device error set, instead of mixing L2s.
+
+constexpr uint32_t RSRC_W3 = 0x00020000u;   // buffer descriptor word 3 for gfx9 raw loads
+
+__device__ __forceinline__ uint32_t xcc_id() {
+    return __builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) & 0xFu;   // HW_REG_XCC_ID[3:0]
+}
+// 8 bytes at byte offset off of a buffer, read past the L1 (cache policy sc1);
+// the load is not volatile, so a poll loop puts a compiler barrier before it
+__device__ __forceinline__ uint64_t l2_load64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 16);
+    return (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+}
+
 // Scores and values in one launch.  Workgroup (chunk c, kv head k) covers 64
 // positions with two pairs of wavefronts: wavefronts 0-1 load the K rows
 // (two threads per row), form the scores (RoPE and the new token's KV write
@@ -330,12 +355,13 @@ __device__ __forceinline__ void poll_max(const uint64_t (&v)[HW][4], float (&res
 // so the exchange waits only for K.  Then all four form the exponentials
 // against the global maxima and the chunk partials for attn_combine_kernel
 // (as attn_pv_kernel).  The wait needs the kv head's workgroups to run
-// together: workgroups are dispatched in index order and a kv head's chunks
-// are consecutive, so once they are all dispatched none of them waits on a
-// workgroup that cannot start; a wait that still runs past spin_max polls
-// gives up and sets *err (the host reports it).
-template <int HD, int G, bool F16>
+// together: workgroups are dispatched in index order and the whole grid (at
+// most 256 chunks per kv head, a few workgroups per CU) is resident at once,
+// so none of them waits on a workgroup that cannot start; a wait that still
+// runs past spin_max polls gives up and sets *err (the host reports it).
+template <int HD, int G, bool F16, bool XL>
 __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
+    // XL: the XCD-local exchange (one-dimensional grid, see above)
     constexpr int HALF_ROW = HD / 2;              // K / V elements per loading thread
     constexpr int DPG = HD / 16;                  // V elements per thread and position (values)
     constexpr int PPT = CH / 16;                  // positions per thread (values)
@@ -349,13 +375,22 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
     __shared__ float gmax[G];
     __shared__ __align__(16) uint8_t pool[VBUF > RED ? VBUF : RED];   // V rows, then the partial sums
     const int T = *a.pos, n = T + 1, n8 = n & ~7;
-    const int c = blockIdx.x, kvh = blockIdx.y;
+    int c, kvh;
+    if (XL) {   // one-dimensional grid: kv head (w mod 8) + 8 j, chunk c; one XCD per kv head
+        const int w = blockIdx.x, per = a.kv_heads >> 3, r = w >> 3;
+        kvh = (w & 7) + 8 * (r % per);
+        c = r / per;
+    } else {
+        c = blockIdx.x;
+        kvh = blockIdx.y;
+    }
     const int p0 = c * CH;
     if (p0 >= n) return;
     const int nch = (n + CH - 1) / CH;            // live chunks of every kv head
     const int cnt = min(CH, n - p0);
     const int mc = XSTRIDE;                       // slots per head: one 4 KiB page each
-    const uint32_t tag = *a.epoch * (uint32_t)a.layers + (uint32_t)a.layer + 1u;
+    uint32_t tag = *a.epoch * (uint32_t)a.layers + (uint32_t)a.layer + 1u;
+    if (XL) tag = (tag << 3) | ((xcc_id() - blockIdx.x) & 7u);   // the launch's XCD offset, as this workgroup sees it
     const int half = a.rope_half;
     const float* cs = a.cos_tab + (int64_t)T * half;
     const float* sn = a.sin_tab + (int64_t)T * half;
@@ -448,13 +483,27 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         // last live one).
         for (int h = wave; h < G; h += 2) {
             const float m = wave_max(sc_s[h][lane]);
-            if (lane == 0) slot_put(a.xmax + ((int64_t)kvh * G + h) * mc + c, tag, m);
+            if (lane == 0) {
+                uint64_t* slot = a.xmax + ((int64_t)kvh * G + h) * mc + c;
+                if (XL) __hip_atomic_store(slot, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(m), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);   // a plain store into this XCD's L2
+                else slot_put(slot, tag, m);
+            }
         }
+        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+            a.xmax, (short)0, (int)((uint32_t)a.heads * XSTRIDE * 8), (int)RSRC_W3);
         for (int h = wave; h < G; h += 2) {
             uint64_t v[1][4];
             float res[1];
             for (int it = 0;; it++) {
-                poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, nch, mc);
+                if (XL) {
+                    asm volatile("" ::: "memory");   // a fresh load every poll
+                    const uint32_t base = (uint32_t)((kvh * G + h) * mc) * 8;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[0][i] = l2_load64(rx, base + 8 * (uint32_t)min(lane + 64 * i, nch - 1));
+                } else {
+                    poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, nch, mc);
+                }
                 if (poll_ready<1>(v, tag)) break;
                 if (it >= a.spin_max) {
                     if (lane == 0) atomicOr(a.err, 1);
@@ -575,8 +624,15 @@ hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
     if (a.fused) {
         if (!a.xmax || !a.epoch || !a.err || !attn_fused_ok(a.heads, a.kv_heads, a.head_dim, a.context))
             return hipErrorInvalidValue;
-        if (a.kv_fp16) attn_fused_kernel<HD, G, true><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
-        else attn_fused_kernel<HD, G, false><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
+        if (a.xcd_exchange) {   // XCD-local exchange: one-dimensional grid
+            if (a.kv_heads % 8) return hipErrorInvalidValue;
+            const dim3 grid(nchunks * a.kv_heads);
+            if (a.kv_fp16) attn_fused_kernel<HD, G, true, true><<<grid, WG, 0, s>>>(a);
+            else attn_fused_kernel<HD, G, false, true><<<grid, WG, 0, s>>>(a);
+        } else {
+            if (a.kv_fp16) attn_fused_kernel<HD, G, true, false><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
+            else attn_fused_kernel<HD, G, false, false><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         attn_combine_kernel<HD><<<a.heads, (1024 / HD) * HD, 0, s>>>(a);
@@ -611,6 +667,62 @@ int attn_max_chunks(int heads, int kv_heads, int context) {
 }
 
 int attn_xmax_slots(int heads) { return heads * XSTRIDE; }
+
+namespace {
+__global__ void xcc_probe_kernel(uint32_t* out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+}  // namespace
+
+namespace {
+template <int HD, int G>
+int xl_per_cu(int kv_fp16) {
+    int n = 0;
+    const hipError_t e = kv_fp16
+        ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_fused_kernel<HD, G, true, true>, WG, 0)
+        : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_fused_kernel<HD, G, false, true>, WG, 0);
+    return e == hipSuccess ? n : 0;
+}
+template <int HD>
+int xl_per_cu_g(int g, int kv_fp16) {
+    switch (g) {
+    case 1: return xl_per_cu<HD, 1>(kv_fp16);
+    case 2: return xl_per_cu<HD, 2>(kv_fp16);
+    case 4: return xl_per_cu<HD, 4>(kv_fp16);
+    case 8: return xl_per_cu<HD, 8>(kv_fp16);
+    default: return 0;
+    }
+}
+}  // namespace
+
+bool attn_xcd_fits(int heads, int kv_heads, int head_dim, int context, int kv_fp16, int cus) {
+    if (!attn_fused_ok(heads, kv_heads, head_dim, context) || kv_heads % 8 || cus < 8) return false;
+    const int g = heads / kv_heads;
+    const int per_cu = head_dim == 64 ? xl_per_cu_g<64>(g, kv_fp16)
+                     : head_dim == 96 ? xl_per_cu_g<96>(g, kv_fp16)
+                     : xl_per_cu_g<128>(g, kv_fp16);
+    const int per_xcd = per_cu * (cus / 8);   // workgroups one XCD holds at once
+    return (kv_heads / 8) * attn_max_chunks(heads, kv_heads, context) * 4 <= per_xcd * 3;
+}
+
+hipError_t attn_xcd_check(hipStream_t s, bool* ok) {
+    constexpr int N = 2048;   // workgroups of the probe launch
+    *ok = false;
+    uint32_t* d = nullptr;
+    hipError_t e = hipMalloc(&d, N * sizeof(uint32_t));
+    if (e != hipSuccess) return e;
+    uint32_t h[N];
+    xcc_probe_kernel<<<N, 64, 0, s>>>(d);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpyAsync(h, d, sizeof h, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(d);
+    if (e != hipSuccess) return e;
+    bool all = true;
+    for (int w = 0; w < N; w++) all = all && ((h[w] - (uint32_t)w) & 7u) == ((h[0] - 0u) & 7u);
+    *ok = all;
+    return hipSuccess;
+}
 
 bool attn_fused_ok(int heads, int kv_heads, int head_dim, int context) {
     return attn_supported(heads, kv_heads, head_dim) && (context + CH - 1) / CH <= 256;

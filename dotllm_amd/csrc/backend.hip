@@ -844,6 +844,7 @@ struct llmdot_hip_model {
     uint64_t* xmax = nullptr;   // tagged chunk maxima of the one-launch attention
     bool attn_fused = false;
     int attn_spin = 1 << 18;
+    bool attn_xcd_exchange = false;    // one-launch attention: chunk maxima through the kv head's XCD L2
     // argmax + device-side loop state: ints[0] token, [1] pos, [2] step,
     // [3] epoch (decode steps run, never reset: tags the attention's slots),
     // [4] error flags set by device waits that gave up
@@ -1014,6 +1015,7 @@ int enqueue_step(llmdot_hip_model* m) {
         aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
         aa.fused = m->attn_fused ? 1 : 0; aa.xmax = m->xmax; aa.epoch = m_epoch(m);
         aa.layer = l; aa.layers = d.layers; aa.spin_max = m->attn_spin; aa.err = m_err(m);
+        aa.xcd_exchange = m->attn_xcd_exchange ? 1 : 0;
         HIPCHK(launch_attention(aa, s));
         {   // O projection + residual (IE:444-449, IE:189), h packed for the FFN RmsNorm
             GemvArgs ga{};
@@ -1370,6 +1372,22 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     if (const char* v = getenv("LLMDOT_HIP_ATTN_FUSED")) m->attn_fused = m->attn_fused && strcmp(v, "0") != 0;
     if (const char* v = getenv("LLMDOT_HIP_ATTN_SPIN")) m->attn_spin = atoi(v) >= 0 ? atoi(v) : m->attn_spin;
     if ((rc = A(sizeof(uint64_t) * (size_t)attn_xmax_slots(d.heads), &p))) return bail(rc); m->xmax = (uint64_t*)p;
+    // The XCD-local chunk-maximum exchange where the shape fits it (attn_xcd_fits)
+    // and the device deals workgroups to XCDs in turn; LLMDOT_HIP_ATTN_XCD=0 keeps
+    // the exchange through the coherence point.
+    {
+        const char* v = getenv("LLMDOT_HIP_ATTN_XCD");
+        int cus = 0;
+        HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device));
+        bool want = m->attn_fused && !(v && strcmp(v, "0") == 0) &&
+                    attn_xcd_fits(d.heads, d.kv_heads, d.head_dim, d.context, d.kv_fp16 ? 1 : 0, cus);
+        if (want) {
+            bool ok = false;
+            HIPCHK(attn_xcd_check(m->ctx->stream, &ok));
+            want = ok;
+        }
+        m->attn_xcd_exchange = want;
+    }
     if ((rc = A(64, &p))) return bail(rc); m->ints = (int32_t*)p;
     if ((rc = A(sizeof(int32_t) * (size_t)(d.context + 1), &p))) return bail(rc); m->token_log = (int32_t*)p;
     {
@@ -1408,8 +1426,9 @@ int check_pos(llmdot_hip_model* m, int32_t pos) {
     if (pos < 0 || pos >= m->d.context) return fail(LLMDOT_E_RANGE, "position outside the KV cache");
     return 0;
 }
-// Device waits that gave up (the attention's chunk-maximum exchange) leave a
-// flag; it is reported once and cleared.
+// Device waits that gave up (the attention's chunk-maximum exchange; in the
+// XCD-local form also a chunk placed on another XCD than its kv head's) leave
+// a flag; it is reported once and cleared.
 int check_device_flags(llmdot_hip_model* m) {
     hipStream_t s = m->ctx->stream;
     int32_t err = 0;
@@ -1419,7 +1438,8 @@ int check_device_flags(llmdot_hip_model* m) {
         HIPCHK(launch_set_scalar(m_err(m), 0, s));
         HIPCHK(hipStreamSynchronize(s));
         return fail(LLMDOT_E_DEVICE, "decode attention: a workgroup gave up waiting for the chunk maxima of its kv "
-                                     "head (spin limit); the step's results are invalid");
+                                     "head (spin limit, or with the XCD-local form a chunk on another XCD: "
+                                     "LLMDOT_HIP_ATTN_XCD=0 avoids it); the step's results are invalid");
     }
     return 0;
 }

@@ -128,7 +128,22 @@ struct AttnArgs {
     const uint32_t* epoch;  // decode steps so far (advanced by the head's argmax pass)
     int layer, layers, spin_max;
     int32_t* err;
+    // One-launch path only: the XCD-local chunk-maximum exchange (kv_heads a
+    // multiple of 8): a one-dimensional grid puts every chunk of a kv head on
+    // one XCD and the maxima go through that XCD's L2.  A chunk placed on
+    // another XCD than the rest of its kv head makes that kv head's wait give
+    // up (*err) rather than mix L2s.
+    int xcd_exchange;
 };
+// Whether the XCD-local exchange suits the shape: kv heads a multiple of 8,
+// and every live chunk of the kv heads one XCD serves (kv_heads / 8 of them,
+// at most attn_max_chunks each) resident at once with a quarter to spare
+// (the chunks of a kv head wait for each other); cus = compute units.
+bool attn_xcd_fits(int heads, int kv_heads, int head_dim, int context, int kv_fp16, int cus);
+// Whether workgroup w of a one-dimensional launch runs on XCD (w + o) mod 8,
+// o fixed within the launch (what the XCD-local attention relies on), from a
+// 2048-workgroup probe launch.
+hipError_t attn_xcd_check(hipStream_t s, bool* ok);
 // Slots of AttnArgs::xmax for `heads` q heads.
 int attn_xmax_slots(int heads);
 int attn_max_chunks(int heads, int kv_heads, int context);

@@ -182,26 +182,6 @@ __device__ Descent descend(const float* x, int n, double T) {
     return Descent{prefix, above, cabove, neq};
 }
 
-// Index of the j-th (1-based) element whose key is K, in index order.
-__device__ int jth_equal(const float* x, int n, uint32_t K, int j) {
-    __shared__ int tmp[2 * NWAVE + 1];
-    __shared__ int s_idx;
-    const int seg = (n + SWG - 1) / SWG;
-    const int b = threadIdx.x * seg, e = min(n, b + seg);
-    int c = 0;
-    for (int i = b; i < e; i++) c += fkey(x[i]) == K;
-    if (threadIdx.x == 0) s_idx = -1;
-    int total;
-    const int off = block_excl_scan<int>(c, tmp, &total);
-    if (off < j && j <= off + c) {
-        int r = off;
-        for (int i = b; i < e; i++)
-            if (fkey(x[i]) == K && ++r == j) { s_idx = i; break; }
-    }
-    __syncthreads();
-    return s_idx;
-}
-
 __global__ void samp_scale_kernel(const float* logits, float inv_temp, float* work, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) work[i] = logits[i] * inv_temp;
 }

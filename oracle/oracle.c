@@ -24,14 +24,22 @@
 #define VEC 8 /* Vector<float>.Count on x86-64 AVX2 */
 
 static int g_threads = 1;
-/* Reduction order: 0 = the reference's; 1 = another valid fp32 order used
- * only to measure how far summation order alone moves the results (see
+/* Reduction order: 0 = the reference's; 1, 2, 3 = other valid fp32 orders
+ * used only to measure how far summation order alone moves the results (see
  * orc_set_order in oracle.h). */
 static int g_order = 0;
+#define N_ORDERS 4
+/* Per order: lanes of the reductions the reference runs over Vector<float>
+ * (its 8; 16 and 32 as 512-bit and wider vectors would give, 4 as 128-bit
+ * ones), the element groups of the scalar K-quant sums (order 0: none, one
+ * running sum), the positions per partial of the attention's value sum. */
+static const int ORD_LANES[N_ORDERS] = {8, 16, 4, 32};
+static const int ORD_GROUP[N_ORDERS] = {0, 32, 64, 16};
+static const int ORD_PVCH[N_ORDERS] = {0, 64, 32, 128};
 
 void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 int orc_get_threads(void) { return g_threads; }
-void orc_set_order(int order) { g_order = order ? 1 : 0; }
+void orc_set_order(int order) { g_order = order > 0 && order < N_ORDERS ? order : 0; }
 int orc_get_order(void) { return g_order; }
 
 static inline float bits_to_float(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
@@ -42,20 +50,24 @@ static inline float hsum8(const float v[VEC]) {
     return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
 }
 
-/* Order 1's lane count for the reductions the reference runs over
- * Vector<float> lanes (what .NET gives with 512-bit vectors). */
-#define VEC_ALT 16
-static inline float hsum16(const float v[VEC_ALT]) { return hsum8(v) + hsum8(v + 8); }
+/* The most lanes any order uses. */
+#define VEC_ALT 32
+/* Horizontal sum of L lanes (L a power of two >= 4) as halves added pairwise;
+ * for L = 8 exactly hsum8. */
+static float hsum_lanes(const float* v, int L) {
+    if (L == 4) return (v[0] + v[1]) + (v[2] + v[3]);
+    return hsum_lanes(v, L / 2) + hsum_lanes(v + L / 2, L / 2);
+}
 
 /* Sum of x[0..n) in the lanes-then-tail order of the reference's vector loops:
- * 8 lanes (order 0) or 16 (order 1), horizontal sum, then the tail in order. */
+ * ORD_LANES lanes (8 for order 0), horizontal sum, then the tail in order. */
 static float lane_sum(const float* x, int n) {
-    const int L = g_order ? VEC_ALT : VEC;
+    const int L = ORD_LANES[g_order];
     float acc[VEC_ALT] = {0};
     int i = 0;
     for (; i <= n - L; i += L)
         for (int l = 0; l < L; l++) acc[l] = acc[l] + x[i + l];
-    float s = L == VEC ? hsum8(acc) : hsum16(acc);
+    float s = hsum_lanes(acc, L);
     for (; i < n; i++) s += x[i];
     return s;
 }
@@ -878,7 +890,7 @@ void orc_softmax(float* in, int n, int has_softcap, float cap) {
         in[j] = expf(in[j] - max);
         sum += in[j];
     }
-    if (g_order) sum = lane_sum(in, n);   /* the same exponentials, summed in order 1 */
+    if (g_order) sum = lane_sum(in, n);   /* the same exponentials, summed in the other order */
     float invSum = 1.0f / sum;
     for (int i = 0; i < n; i++) in[i] = in[i] * invSum;
 }
@@ -1457,10 +1469,11 @@ static void attend_head(const orc_model* m, int layer, int position, int h, cons
     }
     orc_softmax(score, attnLen, 0, 0.0f);
     for (int d = 0; d < hd; d++) rs[d] = 0.0f;
-    if (g_order) {   /* order 1: partial sums over 64-position chunks, chunks in order */
-        for (int s0 = 0; s0 < attnLen; s0 += 64) {
+    if (g_order) {   /* other orders: partial sums over ORD_PVCH-position chunks, chunks in order */
+        const int ch = ORD_PVCH[g_order];
+        for (int s0 = 0; s0 < attnLen; s0 += ch) {
             for (int d = 0; d < hd; d++) prod[d] = 0.0f;
-            for (int s = s0; s < attnLen && s < s0 + 64; s++) {
+            for (int s = s0; s < attnLen && s < s0 + ch; s++) {
                 float sc = score[s];
                 const float* vr = values + (size_t)(attnStart + s) * kvdim + (size_t)kvH * hd;
                 for (int d = 0; d < hd; d++) prod[d] = prod[d] + vr[d] * sc;
@@ -1660,11 +1673,12 @@ static void pf_rows_seq(const float* at, int T, int K, const float* deq, int nr,
         int tb = T - t0 < PF_TB ? T - t0 : PF_TB;
         float acc[PF_RB][PF_TB];
         memset(acc, 0, sizeof acc);
-        if (g_order) {   /* order 1: a partial per 32-element group, groups added in order */
+        if (g_order) {   /* other orders: a partial per ORD_GROUP-element group, groups added in order */
+            const int gs = ORD_GROUP[g_order];
             float gp[PF_RB][PF_TB];
-            for (int g0 = 0; g0 < K; g0 += 32) {
+            for (int g0 = 0; g0 < K; g0 += gs) {
                 memset(gp, 0, sizeof gp);
-                for (int i = g0; i < g0 + 32 && i < K; i++) {
+                for (int i = g0; i < g0 + gs && i < K; i++) {
                     const float* ai = at + (size_t)i * T + t0;
                     for (int j = 0; j < nr; j++) {
                         const float w = deq[(size_t)j * K + i];
@@ -1690,7 +1704,7 @@ static void pf_rows_seq(const float* at, int T, int K, const float* deq, int nr,
 
 __attribute__((target_clones("avx2", "default"), optimize("tree-vectorize")))
 static void pf_rows_lane8(const float* at, int T, int K, const float* deq, int nr, float* out, int ldo, int c0) {
-    const int L = g_order ? VEC_ALT : VEC;   /* lanes: the reference's 8, or order 1's 16 */
+    const int L = ORD_LANES[g_order];   /* lanes: the reference's 8, or another order's */
     const int KL = (K / L) * L;
     for (int t0 = 0; t0 < T; t0 += PF_TB) {
         int tb = T - t0 < PF_TB ? T - t0 : PF_TB;
@@ -1708,7 +1722,7 @@ static void pf_rows_lane8(const float* at, int T, int K, const float* deq, int n
             for (int t = 0; t < tb; t++) {
                 float v[VEC_ALT];
                 for (int l = 0; l < L; l++) v[l] = acc[j][l][t];
-                float dot = L == VEC ? hsum8(v) : hsum16(v);
+                float dot = hsum_lanes(v, L);
                 for (int i = KL; i < K; i++) dot += at[(size_t)i * T + t0 + t] * deq[(size_t)j * K + i];
                 out[(size_t)(t0 + t) * ldo + c0 + j] = dot;
             }

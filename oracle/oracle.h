@@ -91,12 +91,13 @@ void orc_set_threads(int n);   /* row-parallel GEMV/attention; results are bitwi
 int  orc_get_threads(void);
 /* Reduction order of orc_prefill (and of RmsNorm, Softmax and attention,
  * which it shares with orc_process_token): 0 (default) is the reference's;
- * 1 is another valid fp32 order -- 16 lanes instead of Vector<float>'s 8
- * (what .NET gives with 512-bit vectors), a partial per 32-element group in
- * the scalar K-quant GEMV sums, per-64-position partials in the attention's
- * value sum.  Order 1 measures how far summation order alone moves the
- * results (the tolerance floor of tests against other implementations);
- * the fused single-row GEMVs of orc_process_token ignore it. */
+ * 1, 2 and 3 are other valid fp32 orders -- 16, 4 and 32 lanes instead of
+ * Vector<float>'s 8 (what .NET gives with 512-bit, 128-bit and wider vectors),
+ * a partial per 32-, 64- and 16-element group in the scalar K-quant GEMV sums,
+ * per-64-, 32- and 128-position partials in the attention's value sum.  They
+ * measure how far summation order alone moves the results (the tolerance
+ * floor of tests against other implementations); the fused single-row GEMVs
+ * of orc_process_token ignore the order. */
 void orc_set_order(int order);
 int  orc_get_order(void);
 

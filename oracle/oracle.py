@@ -101,7 +101,7 @@ def set_threads(n: int) -> None:
 
 
 def set_order(order: int) -> None:
-    """0: the reference's reduction order; 1: another valid fp32 order (see oracle.h)."""
+    """0: the reference's reduction order; 1, 2, 3: other valid fp32 orders (see oracle.h)."""
     lib().orc_set_order(int(order))
 
 

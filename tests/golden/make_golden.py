@@ -34,9 +34,10 @@ Outputs (small, committed):
                   last step; the KV rows of a few (layer, position) pairs; and
                   per step the floor: max |logit difference| over the whole
                   vector between the oracle in the reference's reduction order
-                  and in another valid fp32 order (orc_set_order(1)),
-                  teacher-forced on the same tokens -- what summation order
-                  alone moves the results by
+                  and in each of three other valid fp32 orders
+                  (orc_set_order(1..3)), teacher-forced on the same tokens, the
+                  largest of the three (each kept in floor_by_order) -- what
+                  summation order alone moves the results by
 """
 import json
 import os
@@ -143,9 +144,12 @@ LONG = {
 }
 
 
+ALT_ORDERS = (1, 2, 3)   # the other valid fp32 orders the floor is taken over (oracle.h)
+
+
 def long_run(key):
     """Greedy run of one workload in the reference's order, and the same tokens
-    teacher-forced through the order-1 oracle for the floor."""
+    teacher-forced through the oracle in each of ALT_ORDERS for the floor."""
     import time
     name, n_prompt, n_gen, kv_fp16, layers, positions = LONG[key]
     ctx = n_prompt + n_gen + 8
@@ -154,55 +158,64 @@ def long_run(key):
     prompt = synth.prompt(vocab, n_prompt, seed=7)
     sidx = sample_indices(vocab)
     O.set_threads(int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1)))
-    m0 = O.Model(img, kv_fp16=kv_fp16, context=ctx)
-    m1 = O.Model(img, kv_fp16=kv_fp16, context=ctx)
+    orders = (0,) + ALT_ORDERS
+    ms = [O.Model(img, kv_fp16=kv_fp16, context=ctx) for _ in orders]
     t0 = time.time()
-    O.set_order(0)
-    l0 = m0.prefill(prompt, 0)
-    O.set_order(1)
-    l1 = m1.prefill(prompt, 0)
-    O.set_order(0)
+
+    def run(tokens, pos0):
+        out = []
+        try:
+            for o, m in zip(orders, ms):
+                O.set_order(o)
+                out.append(m.prefill(tokens, pos0))
+        finally:
+            O.set_order(0)
+        return out
+
+    ls = run(prompt, 0)
     print(f"{key}: prompt of {n_prompt} in {time.time() - t0:.0f}s", flush=True)
     full_steps = sorted({0, n_gen - 1})
-    toks, tidx, tval, sval, gap, mean, rms, floor, full = [], [], [], [], [], [], [], [], []
+    toks, tidx, tval, sval, gap, mean, rms, floor, full, forders = [], [], [], [], [], [], [], [], [], []
     for s in range(n_gen):
+        l0 = ls[0]
         ti, tv, g, mu, r = step_stats(l0)
         tok = O.argmax(l0)
         assert tok == int(ti[0])
         toks.append(tok); tidx.append(ti); tval.append(tv); sval.append(l0[sidx]); gap.append(g)
         mean.append(mu); rms.append(r)
-        floor.append(float(np.max(np.abs(l1 - l0))))
+        fo = [float(np.max(np.abs(lk - l0))) for lk in ls[1:]]
+        forders.append(fo)
+        floor.append(max(fo))
         if s in full_steps:
             full.append(l0.copy())
         if s + 1 < n_gen:
-            O.set_order(0)
-            l0 = m0.prefill([tok], n_prompt + s)
-            O.set_order(1)
-            l1 = m1.prefill([tok], n_prompt + s)
-            O.set_order(0)
+            ls = run([tok], n_prompt + s)
         if s % 16 == 15:
             print(f"{key}: step {s + 1}/{n_gen}, floor so far {max(floor):.3e}, {time.time() - t0:.0f}s", flush=True)
     kv = {}
     for part in ("k", "v"):
-        kv[part] = np.zeros((len(layers), len(positions), m0.config.kv_heads * m0.config.head_dim), np.float32)
+        kv[part] = np.zeros((len(layers), len(positions), ms[0].config.kv_heads * ms[0].config.head_dim), np.float32)
         kv[part + "_floor"] = np.zeros((len(layers), len(positions)), np.float32)
     for i, l in enumerate(layers):
         for j, p in enumerate(positions):
-            k0, v0 = m0.kv_read(l, p)
-            k1, v1 = m1.kv_read(l, p)
+            k0, v0 = ms[0].kv_read(l, p)
             kv["k"][i, j], kv["v"][i, j] = k0, v0
-            kv["k_floor"][i, j] = np.max(np.abs(k1 - k0))
-            kv["v_floor"][i, j] = np.max(np.abs(v1 - v0))
-    m0.close(); m1.close()
+            for m in ms[1:]:
+                k1, v1 = m.kv_read(l, p)
+                kv["k_floor"][i, j] = max(kv["k_floor"][i, j], np.max(np.abs(k1 - k0)))
+                kv["v_floor"][i, j] = max(kv["v_floor"][i, j], np.max(np.abs(v1 - v0)))
+    for m in ms:
+        m.close()
     meta = dict(config=key, model=name, weights_seed=1234, prompt_seed=7, n_prompt=n_prompt, n_gen=n_gen,
                 kv_fp16=kv_fp16, image_context=ctx, image_fingerprint=image_fingerprint(img), init=INIT,
-                n_top=N_TOP, n_sample=int(sidx.size), sample_seed=97)
+                n_top=N_TOP, n_sample=int(sidx.size), sample_seed=97, floor_orders=list(ALT_ORDERS))
     np.savez_compressed(os.path.join(HERE, f"long_{key}.npz"), meta=np.array(json.dumps(meta)),
                         prompt=np.asarray(prompt, np.int32), tokens=np.asarray(toks, np.int32),
                         top_idx=np.asarray(tidx, np.int32), top_val=np.asarray(tval, np.float32),
                         sample_idx=sidx, sample_val=np.asarray(sval, np.float32),
                         full_steps=np.asarray(full_steps, np.int32), full_val=np.asarray(full, np.float32),
                         gap=np.asarray(gap), mean=np.asarray(mean), rms=np.asarray(rms), floor=np.asarray(floor),
+                        floor_by_order=np.asarray(forders),
                         kv_layers=np.asarray(layers, np.int32), kv_positions=np.asarray(positions, np.int32), **kv)
     print(f"wrote long_{key}.npz in {time.time() - t0:.0f}s; max floor {max(floor):.3e}", flush=True)
 

@@ -1,24 +1,33 @@
 """The oracle in the reference's summation order beside the same oracle in
-another valid fp32 order (orc_set_order(1)), fed the same tokens.
+three other valid fp32 orders (orc_set_order(1..3): other vector widths, group
+and chunk sizes), fed the same tokens.
 
-The first gives the expected values; the distance between the two is how far
-summation order alone moves them -- the floor below which no implementation
-with different reductions (the device's tree sums, 24-bit GEMV activations,
-MFMA tiles) can be held.  Both step through the batched prompt path, which is
-bitwise the sequential ProcessToken loop in the reference order
-(tests/test_oracle_prefill.py) and applies order 1 to every reduction.
+The first gives the expected values; the largest distance to the others is how
+far summation order alone moves them -- the floor below which no
+implementation with different reductions (the device's tree sums, 24-bit GEMV
+activations, MFMA tiles) can be held.  All step through the batched prompt
+path, which is bitwise the sequential ProcessToken loop in the reference order
+(tests/test_oracle_prefill.py) and applies the other order to every reduction.
+One alternative order is a single sample of that movement, and with N(0, 0.02)
+weights the movement is heavy-tailed: the reference's ExpApprox jumps by up to
+18% where a score crosses its range-reduction boundary, and fp16 KV rounding
+flips by an ulp, so a step moves a lot only where some reordering happens to
+cross such a boundary; taking the largest of three orders covers more of them.
 
 Bounds built from it (logit_bounds): a step's logits within
 max(2e-2, FLOOR_MARGIN x the running maximum of the floor up to that step);
 greedy tokens compared up to the first top-2 gap below max(1e-2, twice that
-bound's floor part).  The margin: one reordering is one sample of the order
-noise, not an upper bound for another implementation, and the device departs
-from the reference's order in every reduction at once (and uses 24-bit
-activations in the GEMVs, two fp16 activation planes in the prompt GEMMs).  It
-is set just above the largest ratio of device error to the same step's
-running floor measured over every model test and fixture with N(0, 0.02)
-weights on every matrix (1.64: the Phi-3-mini shape with fp16 KV, step 4 of
-its 8-step run).
+bound's floor part).  The margin: the device departs from the reference's order
+in every reduction at once (and uses 24-bit activations in the GEMVs, two fp16
+activation planes in the prompt GEMMs), so it is set just above the largest
+ratio of device error to the same step's running floor measured over every
+model test and fixture (1.70: the 7B shape at a 4096-position fp16 cache).
+For calibration, one of the three orders measured against the running
+maximum of the other two reaches 2.28 (the 7B greedy-64 fixture with fp16 KV,
+step 9), and exceeds 1.5 in 0.5% of its steps: a valid reordering strays that
+far too.  KV rows (single samples, no running maximum) are held to KV_MARGIN
+times their own floor (measured device maximum 2.09: the 7B fp32-KV fixture,
+layer 15, position 50).
 """
 import numpy as np
 
@@ -27,6 +36,8 @@ from oracle import oracle as O
 LOGIT_TOL = 2e-2
 NEAR_TIE = 1e-2
 FLOOR_MARGIN = 1.75
+KV_MARGIN = 2.5
+ALT_ORDERS = (1, 2, 3)
 
 
 def logit_bounds(floors):
@@ -42,21 +53,27 @@ def floor_ratio(errors, floors):
 
 
 class OraclePair:
-    def __init__(self, img, kv_fp16, context=None):
+    """The reference-order oracle (m0) and one per alternative order (alts)."""
+
+    def __init__(self, img, kv_fp16, context=None, orders=ALT_ORDERS):
         self.m0 = O.Model(img, kv_fp16=kv_fp16, context=context)
-        self.m1 = O.Model(img, kv_fp16=kv_fp16, context=context)
+        self.alts = [(o, O.Model(img, kv_fp16=kv_fp16, context=context)) for o in orders]
         self.config = self.m0.config
-        self.floors = []   # max |logit difference| of every call so far
+        self.floors = []          # per call: max over the orders of max |logit difference|
+        self.floors_by_order = []
 
     def _both(self, f):
         try:
             O.set_order(0)
             l0 = f(self.m0)
-            O.set_order(1)
-            l1 = f(self.m1)
+            fo = []
+            for o, m in self.alts:
+                O.set_order(o)
+                fo.append(float(np.max(np.abs(f(m) - l0))))
         finally:
             O.set_order(0)
-        self.floors.append(float(np.max(np.abs(l1 - l0))))
+        self.floors.append(max(fo))
+        self.floors_by_order.append(fo)
         return l0
 
     def prefill(self, tokens, pos0=0):
@@ -68,16 +85,21 @@ class OraclePair:
 
     def kv_fill_random(self, n, seed):
         self.m0.kv_fill_random(n, seed)
-        self.m1.kv_fill_random(n, seed)
+        for _, m in self.alts:
+            m.kv_fill_random(n, seed)
 
     def kv_read(self, layer, pos):
         return self.m0.kv_read(layer, pos)
 
+    def kv_alt_reads(self, layer, pos):
+        """(K, V) rows of every alternative order at (layer, pos)."""
+        return [m.kv_read(layer, pos) for _, m in self.alts]
+
     def kv_floor(self, layer, pos):
-        """max |K/V difference| between the two orders at (layer, pos)."""
+        """max |K/V difference| between the reference order and any other order at (layer, pos)."""
         k0, v0 = self.m0.kv_read(layer, pos)
-        k1, v1 = self.m1.kv_read(layer, pos)
-        return max(float(np.max(np.abs(k1 - k0))), float(np.max(np.abs(v1 - v0))))
+        return max(max(float(np.max(np.abs(k1 - k0))), float(np.max(np.abs(v1 - v0))))
+                   for k1, v1 in self.kv_alt_reads(layer, pos))
 
     def bounds(self):
         """logit_bounds of the calls so far: (logit bound, near-tie threshold) per call."""
@@ -90,12 +112,13 @@ class OraclePair:
 
     def close(self):
         self.m0.close()
-        self.m1.close()
+        for _, m in self.alts:
+            m.close()
 
 
 def greedy_run(img, kv_fp16, context, prompt, n_gen):
     """The reference's greedy Generate (IE:74-132) in the reference order, the
-    order-1 oracle teacher-forced on its tokens beside it.  Returns (tokens,
+    other-order oracles teacher-forced on its tokens beside it.  Returns (tokens,
     logits [n_gen][vocab], pair) -- the logits of step s are those token s was
     taken from; pair.floors[s] is that step's floor."""
     pair = OraclePair(img, kv_fp16, context)

@@ -14,28 +14,28 @@ every matrix:
 
 The device processes each prompt as batched MFMA GEMMs (the prefill path), then
 decodes with the captured step.  Bars, per step s:
-  * the logits' max absolute error within bound(s) = max(2e-2, 1.75 floor(s)),
-    where floor(s) is the running maximum, over steps <= s, of how far the
-    oracle's own logits move (max over the whole vocabulary) when only its
-    summation order changes (orc_set_order(1), teacher-forced on the same
-    tokens, stored in the fixture; the factor is explained in
+  * the logits' max absolute error within
+    bound(s) = max(2e-2, FLOOR_MARGIN floor(s)), where floor(s) is the running
+    maximum, over steps <= s, of how far the oracle's own logits move (max over
+    the whole vocabulary) when only its summation order changes (the largest
+    over three other valid fp32 orders, orc_set_order(1..3), teacher-forced on
+    the same tokens, stored in the fixture; FLOOR_MARGIN is explained in
     tests/oracle_pair.py).  The error is taken over every logit the fixture
-    holds: the oracle's top 256 and 4096 fixed indices at every step, the whole
-    vocabulary at the first and last step, and the mean and RMS of the whole
-    vector (both 1-Lipschitz in the max norm);
+    holds: the oracle's top 256 and 4096 fixed indices at every step, the
+    whole vocabulary at the first and last step, and the mean and RMS of the
+    whole vector (both 1-Lipschitz in the max norm);
   * greedy tokens identical up to the oracle's first step whose top-2 gap is
-    below max(1e-2, 3.5 floor(s)) (a near-tie at that error), and at least as far
-    as the device was measured to agree (MIN_SAME: the device is
-    deterministic, so a shorter run is a regression);
+    below max(1e-2, 2 FLOOR_MARGIN floor(s)) (a near-tie at that error), and
+    at least as far as the device was measured to agree (MIN_SAME: the device
+    is deterministic, so a shorter run is a regression);
   * the same argmax, teacher-forced, wherever the gap is at least that;
   * the fresh engine's first prefill (inside generate_all: workspace allocated
     and zeroed just before) and the re-run after reset give bit-identical
     last-token logits (both runs are deterministic);
   * the KV rows of the sampled (layer, position) pairs within
-    max(1e-3, 2 floor_kv) (floor_kv: how far the same order change moves the
-    oracle's row; a single sample has no running maximum to lean on, and the
-    device changes more than one order -- every reduction, and 24-bit
-    activations in the GEMVs -- so the factor 2 is the margin).
+    max(1e-3, KV_MARGIN floor_kv) (floor_kv: how far the same order changes
+    move the oracle's row; a single row has no running maximum to lean on; the
+    margin is explained in tests/oracle_pair.py).
 """
 import json
 import os
@@ -45,7 +45,7 @@ import pytest
 
 from dotllm_amd import synth
 from dotllm_amd.engine import InferenceEngine, LoadedModel, greedy
-from oracle_pair import floor_ratio, logit_bounds
+from oracle_pair import KV_MARGIN, floor_ratio, logit_bounds
 
 pytestmark = pytest.mark.gpu
 
@@ -54,7 +54,7 @@ KV_TOL = 1e-3
 
 # free-running greedy tokens the device was measured to share with the oracle
 # (identical prefix length); a run shorter than this is a regression
-MIN_SAME = {"c3": 0, "c3h": 0, "c4": 0, "c5": 0, "c5h": 0, "7b64h": 0, "7b64": 0}
+MIN_SAME = {"c3": 0, "c3h": 0, "c4": 0, "c5": 0, "c5h": 0, "7b64h": 10, "7b64": 56}
 
 
 def _fixture(key):
@@ -114,7 +114,7 @@ def _run(hip, key):
             for j, pos in enumerate(z["kv_positions"]):
                 k, v = eng.kv_read(int(layer), int(pos))
                 kv_err.append(max(float(np.max(np.abs(k - z["k"][i, j]))), float(np.max(np.abs(v - z["v"][i, j])))))
-                kv_bound.append(max(KV_TOL, 2 * float(z["k_floor"][i, j]), 2 * float(z["v_floor"][i, j])))
+                kv_bound.append(max(KV_TOL, KV_MARGIN * float(z["k_floor"][i, j]), KV_MARGIN * float(z["v_floor"][i, j])))
                 dk, dv = np.abs(k - z["k"][i, j]), np.abs(v - z["v"][i, j])
                 at = (z["k"][i, j], int(np.argmax(dk))) if dk.max() >= dv.max() else (z["v"][i, j], int(np.argmax(dv)))
                 kv_mag.append((int(layer), int(pos), float(at[0][at[1]])))
@@ -123,12 +123,15 @@ def _run(hip, key):
     forced, free = np.asarray(forced), np.asarray(free)
     ratio = forced / bound
     w = int(ratio.argmax())
+    run_floor = np.maximum(np.maximum.accumulate(z["floor"]), 1e-30)
+    rel = forced / run_floor   # device error in units of the order floor, per step
     print(f"{key} ({meta['model']}, {n_prompt}-token prompt, {n_gen} tokens, kv_fp16={meta['kv_fp16']}): "
           f"free-running tokens identical for {same} steps (required {max(well_posed, MIN_SAME[key])}, "
           f"first near-tie at {well_posed}); logit error free-running max {free.max():.3e}, teacher-forced max "
           f"{forced.max():.3e} at step {int(forced.argmax())}, first step {forced[0]:.3e}, last {forced[-1]:.3e}; "
-          f"largest error/bound {ratio[w]:.2f} at step {w} (bound {bound[w]:.3e}); largest error/floor "
-          f"{floor_ratio(forced, z['floor']):.2f}; floor max {z['floor'].max():.3e}; "
+          f"largest error/bound {ratio[w]:.2f} at step {w} (bound {bound[w]:.3e}); error/floor max "
+          f"{floor_ratio(forced, z['floor']):.2f}, p90 {np.percentile(rel, 90):.2f}, median {np.median(rel):.2f}; "
+          f"floor max {z['floor'].max():.3e}; "
           f"KV error max {max(kv_err):.3e} (bound {max(kv_bound):.3e})")
     assert cold_warm_same, "the first prefill of a fresh engine differs from the warm re-run"
     assert same >= well_posed
@@ -171,7 +174,7 @@ def test_c4_batched_prompt_matches_device_decode_loop(hip):
     """The 7B 2048-token prompt through the batched MFMA path and through 2048
     captured decode steps of the same device (LLMDOT_HIP_SEQ_PREFILL=1): last
     logits within the fixture's first-step bound, KV rows at the sampled
-    positions within max(1e-3, 2 x their floor)."""
+    positions within max(1e-3, KV_MARGIN x their floor)."""
     z, meta = _fixture("c4")
     img = synth.build_image(meta["model"], seed=meta["weights_seed"], context=meta["image_context"])
     prompt = z["prompt"].tolist()
@@ -192,7 +195,7 @@ def test_c4_batched_prompt_matches_device_decode_loop(hip):
             i, j = z["kv_layers"].tolist().index(l), z["kv_positions"].tolist().index(p)
             e = max(float(np.max(np.abs(k - ks))), float(np.max(np.abs(v - vs))))
             worst = max(worst, e)
-            assert e <= max(KV_TOL, 2 * float(z["k_floor"][i, j]), 2 * float(z["v_floor"][i, j])), (l, p, e)
+            assert e <= max(KV_TOL, KV_MARGIN * float(z["k_floor"][i, j]), KV_MARGIN * float(z["v_floor"][i, j])), (l, p, e)
     finally:
         eng.dispose()
     d = float(np.max(np.abs(batched - seq)))

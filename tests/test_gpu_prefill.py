@@ -13,7 +13,7 @@ import pytest
 from dotllm_amd import Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, byte_count, synth
 from dotllm_amd.engine import InferenceEngine, LoadedModel
 from oracle import oracle as O
-from oracle_pair import OraclePair
+from oracle_pair import KV_MARGIN, OraclePair
 
 pytestmark = pytest.mark.gpu
 
@@ -101,23 +101,23 @@ def oracle_threads():
 
 def _kv_err(eng, pair, layer, n):
     """max over positions of |K - K_ref|, |V - V_ref| relative to max |K_ref|, |V_ref|
-    of the layer, and the same for the oracle's order-1 run (the floor)."""
+    of the layer, and the same for the oracle's other-order runs (the floor)."""
     ek = ev = mk = mv = fk = fv = 0.0
     for pos in range(n):
         k, v = eng.kv_read(layer, pos)
         rk, rv = pair.m0.kv_read(layer, pos)
-        ok, ov = pair.m1.kv_read(layer, pos)
         ek, ev = max(ek, float(np.max(np.abs(k - rk)))), max(ev, float(np.max(np.abs(v - rv))))
-        fk, fv = max(fk, float(np.max(np.abs(ok - rk)))), max(fv, float(np.max(np.abs(ov - rv))))
+        for ok, ov in pair.kv_alt_reads(layer, pos):
+            fk, fv = max(fk, float(np.max(np.abs(ok - rk)))), max(fv, float(np.max(np.abs(ov - rv))))
         mk, mv = max(mk, float(np.max(np.abs(rk)))), max(mv, float(np.max(np.abs(rv))))
     return max(ek / mk, ev / mv), max(fk / mk, fv / mv)
 
 
 def _prompt_check(hip, img, prompt, ctx, kv_fp16, layers, split=None):
     """The batched prompt against the oracle's sequential loop (tests/oracle_pair.py;
-    its batched path is bitwise that loop): last logits within max(2e-2, 1.75 x the
+    its batched path is bitwise that loop): last logits within max(2e-2, FLOOR_MARGIN x the
     oracle's summation-order floor), KV of every position of the sampled layers
-    within max(2e-3, 2 x the order-1 run's relative difference), and the next
+    within max(2e-3, KV_MARGIN x the other orders' largest relative difference), and the next
     decode step from the batched cache within the same logit bound."""
     pair = OraclePair(img, kv_fp16, ctx)
     rl = pair.prefill(prompt, 0)
@@ -141,7 +141,7 @@ def _prompt_check(hip, img, prompt, ctx, kv_fp16, layers, split=None):
     if top2[1] - top2[0] >= tie_at[0]:
         assert am == nxt
     for e, f in kv:
-        assert e <= max(KV_MIN, 2 * f), (e, f)
+        assert e <= max(KV_MIN, KV_MARGIN * f), (e, f)
     assert float(np.max(np.abs(dl - rdl))) <= bound[1]
     pair.close()
     eng.dispose()

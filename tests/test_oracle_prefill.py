@@ -123,23 +123,36 @@ def test_prefill_across_the_chunk_boundary(tiny_image):
             assert np.array_equal(np.concatenate(seq.kv_read(layer, pos)), np.concatenate(bat.kv_read(layer, pos)))
 
 
-def test_order1_is_a_reordering(tiny_image):
-    """Order 1 moves the logits (so it measures something), by fp32 rounding
-    size on the 4-layer model; dequantisation (no reductions) is unchanged; the
-    reference order afterwards reproduces the earlier results bit for bit."""
+@pytest.mark.parametrize("order", [1, 2, 3])
+def test_other_orders_are_reorderings(tiny_image, order):
+    """Each other order moves the logits (so it measures something), by fp32
+    rounding size on the 4-layer model, and differently from the others;
+    dequantisation (no reductions) is unchanged; the reference order afterwards
+    reproduces the earlier results bit for bit; an order outside 1..3 is the
+    reference's."""
     toks = synth.prompt(32000, 24, seed=4)
     m0 = O.Model(tiny_image, kv_fp16=False)
     l0 = m0.prefill(toks, 0)
-    O.set_order(1)
-    m1 = O.Model(tiny_image, kv_fp16=False)
-    l1 = m1.prefill(toks, 0)
-    w = blocks(Q4_K, 4, 512, np.random.default_rng(0))
-    d1 = O.dequantize(w, Q4_K, 4, 512)
-    O.set_order(0)
+    outs = {}
+    try:
+        for o in (1, 2, 3):
+            O.set_order(o)
+            outs[o] = O.Model(tiny_image, kv_fp16=False).prefill(toks, 0)
+        w = blocks(Q4_K, 4, 512, np.random.default_rng(0))
+        O.set_order(order)
+        d1 = O.dequantize(w, Q4_K, 4, 512)
+        O.set_order(7)
+        l7 = O.Model(tiny_image, kv_fp16=False).prefill(toks, 0)
+    finally:
+        O.set_order(0)
     d0 = O.dequantize(w, Q4_K, 4, 512)
     assert np.array_equal(d0.view(np.uint32), d1.view(np.uint32))
-    diff = float(np.max(np.abs(l1 - l0)))
+    diff = float(np.max(np.abs(outs[order] - l0)))
     assert 0 < diff < 1e-4, diff
+    for o in (1, 2, 3):
+        if o != order:
+            assert not np.array_equal(outs[o].view(np.uint32), outs[order].view(np.uint32))
+    assert np.array_equal(l7.view(np.uint32), l0.view(np.uint32))
     again = O.Model(tiny_image, kv_fp16=False).prefill(toks, 0)
     assert np.array_equal(again.view(np.uint32), l0.view(np.uint32))
 
@@ -174,6 +187,8 @@ def test_long_fixture_consistent(key):
     assert np.all(np.diff(z["top_val"], axis=1) <= 0)
     np.testing.assert_allclose(z["gap"], z["top_val"][:, 0] - z["top_val"][:, 1], rtol=0, atol=1e-6)
     assert np.all(z["rms"] >= np.abs(z["mean"])) and np.all(z["floor"] >= 0)
+    assert meta["floor_orders"] == [1, 2, 3] and z["floor_by_order"].shape == (n, 3)
+    assert np.array_equal(z["floor"], z["floor_by_order"].max(axis=1))
     assert z["full_steps"].tolist() == sorted({0, n - 1})
     for s, row in zip(z["full_steps"], z["full_val"]):
         assert row.shape == (vocab,)
