@@ -135,8 +135,9 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--config", default="mistral7b")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--cpu-steps", type=int, default=1,
-                    help="timed oracle steps of the single-thread baseline (about 23 s each at the 7B shape)")
+    ap.add_argument("--cpu-steps", type=int, default=2,
+                    help="timed oracle steps of the single-thread baseline, after one warm-up step (about 22 s "
+                         "each at the 7B shape)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads of the second, parallel oracle figure (0: up to 16)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -279,7 +280,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         # the faithful figure: one thread, as the reference runs
         t0 = time.perf_counter()
-        out["cpu_baseline"] = cpu_baseline(img, args.ctx, args.cpu_steps, 1, warmup=False)
+        out["cpu_baseline"] = cpu_baseline(img, args.ctx, args.cpu_steps, 1, warmup=True)
         log(f"cpu baseline (1 thread): {out['cpu_baseline']['value']:.4f} tok/s ({time.perf_counter() - t0:.1f}s)")
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         if threads > 1:

@@ -37,6 +37,7 @@ constexpr int WG = 256;
 constexpr int CH = 64;    // positions per score chunk (scores kernel; one per lane of a wavefront)
 constexpr int CHP = 64;   // positions per pv chunk (pv kernel; its partials feed the combine)
 constexpr int XSTRIDE = 512;   // tagged chunk-maximum slots per q head (4 KiB apart)
+constexpr int READY0 = 256;    // XCD-local form: the kv head's "partials written" slots, after the maxima
 
 // N consecutive cache elements starting at element idx (16-byte aligned) as floats.
 template <int N>
@@ -329,10 +330,13 @@ __device__ __forceinline__ void poll_max(const uint64_t (&v)[HW][4], float (&res
 // kv head run on one XCD and exchange their maxima through its L2: plain
 // stores, and device-scope loads (cache policy sc1: past the CU's L1, served by
 // the L2), which see a store from the same XCD ~0.2 us after it completes
-// against ~1 us from another XCD (measured).  Each workgroup folds its own o
-// (from its XCC_ID register) into the tag it publishes, so a chunk placed on
-// another XCD never matches: its kv head's wait ends at the spin limit with the
-// device error set, instead of mixing L2s.
+// against ~1 us from another XCD (measured).  The chunks then meet a second
+// time, once their partials are written, and each sums every chunk's partials
+// for its own share of the kv head's outputs, so no combine launch follows.
+// Each workgroup folds its own o (from its XCC_ID register) into the tag it
+// publishes, so a chunk placed on another XCD never matches: its kv head's
+// wait ends at the spin limit with the device error set, instead of mixing
+// L2s.
 
 constexpr uint32_t RSRC_W3 = 0x00020000u;   // buffer descriptor word 3 for gfx9 raw loads
 
@@ -584,6 +588,69 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         for (int q = 0; q < NGR; q += 4) r += (red[q][idx] + red[q + 1][idx]) + (red[q + 2][idx] + red[q + 3][idx]);
         a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = r;
     }
+    if (XL) {
+        // The combine without a launch: every chunk of the kv head publishes
+        // "partials written" (after its stores reached the L2) and waits for the
+        // others, as for the maxima; then each workgroup sums all chunks for
+        // its own share of the kv head's G*HD outputs.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const uint32_t rbase = (uint32_t)((kvh * G) * mc + READY0) * 8;   // the kv head's ready slots
+        if (t == 0)
+            __hip_atomic_store(a.xmax + rbase / 8 + c, (uint64_t)tag << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+            a.xmax, (short)0, (int)((uint32_t)a.heads * XSTRIDE * 8), (int)RSRC_W3);
+        if (wave == 0) {
+            uint64_t v[1][4];
+            for (int it = 0;; it++) {
+                asm volatile("" ::: "memory");   // a fresh load every poll
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[0][i] = l2_load64(rx, rbase + 8 * (uint32_t)min(lane + 64 * i, nch - 1));
+                if (poll_ready<1>(v, tag)) break;
+                if (it >= a.spin_max) {
+                    if (lane == 0) atomicOr(a.err, 1);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+        constexpr int NCOL = G * HD;                  // outputs of the kv head
+        const int per = (NCOL + nch - 1) / nch;       // outputs per chunk workgroup
+        const int j0 = c * per, nc = min(NCOL, j0 + per) - j0;
+        if (nc <= 0) return;
+        const int ngrp = max(1, min(WG / nc, nch));   // thread groups over the chunks
+        float* cred = reinterpret_cast<float*>(pool);  // [ngrp][nc]
+        __shared__ float zs[G];
+        const uint32_t chunk_bytes = (uint32_t)a.heads * HD * 4;
+        const __amdgpu_buffer_rsrc_t ro =
+            __builtin_amdgcn_make_buffer_rsrc(a.part_out, (short)0, (int)((uint32_t)nch * chunk_bytes), (int)RSRC_W3);
+        const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+            a.part_sum, (short)0, (int)((uint32_t)nch * a.heads * 4), (int)RSRC_W3);
+        for (int idx = t; idx < nc * ngrp; idx += WG) {
+            const int col = idx % nc, g = idx / nc;
+            const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 4;
+            float acc = 0.f;
+            for (int cc = g; cc < nch; cc += ngrp)
+                acc += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (int)(off + cc * chunk_bytes), 0, 16));
+            cred[g * nc + col] = acc;
+        }
+        for (int h = wave; h < G; h += 4) {   // the sums of exponentials, lanes over the chunks
+            float z = 0.f;
+            for (int cc = lane; cc < nch; cc += 64)
+                z += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   rz, (int)(((uint32_t)cc * a.heads + kvh * G + h) * 4), 0, 16));
+            z = wave_sum(z);
+            if (lane == 0) zs[h] = z;
+        }
+        __syncthreads();
+        for (int col = t; col < nc; col += WG) {
+            float acc = cred[col];
+            for (int g = 1; g < ngrp; g++) acc += cred[g * nc + col];
+            const int j = j0 + col;
+            a.out[(int64_t)kvh * NCOL + j] = acc * (1.0f / zs[j / HD]);
+        }
+    }
 }
 
 // out = sum_c part_out[c] / sum_c part_sum[c] for one q head per workgroup
@@ -634,7 +701,7 @@ hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
             else attn_fused_kernel<HD, G, false, false><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
         }
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if (e != hipSuccess || a.xcd_exchange) return e;   // the XCD-local form combines in the launch
         attn_combine_kernel<HD><<<a.heads, (1024 / HD) * HD, 0, s>>>(a);
         return hipGetLastError();
     }
