@@ -627,19 +627,30 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
             __builtin_amdgcn_make_buffer_rsrc(a.part_out, (short)0, (int)((uint32_t)nch * chunk_bytes), (int)RSRC_W3);
         const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
             a.part_sum, (short)0, (int)((uint32_t)nch * a.heads * 4), (int)RSRC_W3);
+        // loads issued four at a time before any is added (a chunk past nch
+        // reads past the buffer's end: the descriptor returns 0 there)
         for (int idx = t; idx < nc * ngrp; idx += WG) {
             const int col = idx % nc, g = idx / nc;
             const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 4;
             float acc = 0.f;
-            for (int cc = g; cc < nch; cc += ngrp)
-                acc += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (int)(off + cc * chunk_bytes), 0, 16));
+            for (int cc = g; cc < nch; cc += 4 * ngrp) {
+                float v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                         ro, (int)(off + (uint32_t)(cc + u * ngrp) * chunk_bytes), 0, 16));
+#pragma unroll
+                for (int u = 0; u < 4; u++) acc += v[u];
+            }
             cred[g * nc + col] = acc;
         }
-        for (int h = wave; h < G; h += 4) {   // the sums of exponentials, lanes over the chunks
-            float z = 0.f;
-            for (int cc = lane; cc < nch; cc += 64)
-                z += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                   rz, (int)(((uint32_t)cc * a.heads + kvh * G + h) * 4), 0, 16));
+        for (int h = wave; h < G; h += 4) {   // the sums of exponentials, lanes over the chunks (nch <= 256)
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                     rz, (int)(((uint32_t)(lane + 64 * u) * a.heads + kvh * G + h) * 4), 0, 16));
+            float z = (v[0] + v[1]) + (v[2] + v[3]);
             z = wave_sum(z);
             if (lane == 0) zs[h] = z;
         }
