@@ -1744,26 +1744,45 @@ extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t fir
     if (int rc = set_int(m, m_token(m), first_token)) return rc;
     if (int rc = set_int(m, m_pos(m), position)) return rc;
     if (int rc = set_int(m, m_step(m), 0)) return rc;
+    // the dominant kernel alone: every layer's gate/up launch back to back
+    // (distinct weights per layer, past any cache), captured once and replayed
+    // so that host enqueue gaps stay out of the timed region
+    hipGraphExec_t kg = nullptr;
+    if (per_kernel) {
+        hipGraph_t g = nullptr;
+        HIPCHK(hipStreamSynchronize(s));
+        HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        hipError_t le = hipSuccess;
+        for (int l = 0; l < m->d.layers && le == hipSuccess; l++) le = launch_gate_up(m, l);
+        const hipError_t ce = hipStreamEndCapture(s, &g);
+        if (le != hipSuccess || ce != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return fail(LLMDOT_E_DEVICE, std::string("gate/up capture: ") + hipGetErrorString(le != hipSuccess ? le : ce));
+        }
+        const hipError_t ie = hipGraphInstantiate(&kg, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ie != hipSuccess) return fail(LLMDOT_E_DEVICE, std::string("gate/up graph: ") + hipGetErrorString(ie));
+    }
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0));
     HIPCHK(hipEventCreate(&e1));
     HIPCHK(hipStreamSynchronize(s));
     HIPCHK(hipEventRecord(e0, s));
     int launches = 0;
-    for (int i = 0; i < steps; i++) {
+    hipError_t re = hipSuccess;
+    for (int i = 0; i < steps && re == hipSuccess; i++) {
         if (per_kernel) {
-            // the dominant kernel alone: every layer's gate/up launch back to
-            // back (2 GB of distinct weights per pass, past any cache)
-            for (int l = 0; l < m->d.layers; l++) {
-                HIPCHK(launch_gate_up(m, l));
-                launches++;
-            }
+            re = hipGraphLaunch(kg, s);
+            launches += m->d.layers;
         } else if (int rc = run_step(m)) {
+            if (kg) (void)hipGraphExecDestroy(kg);
             return rc;
         }
     }
     HIPCHK(hipEventRecord(e1, s));
     HIPCHK(hipEventSynchronize(e1));
+    if (kg) (void)hipGraphExecDestroy(kg);
+    HIPCHK(re);
     float total = 0;
     HIPCHK(hipEventElapsedTime(&total, e0, e1));
     (void)hipEventDestroy(e0);

@@ -271,10 +271,11 @@ int32_t llmdot_hip_kv_read(llmdot_hip_model* model, int32_t layer, int32_t posit
  * per_kernel == 0: runs `steps` greedy decode steps from the current state
  * (token feedback on the device) and returns the elapsed milliseconds measured
  * with HIP events on the model's stream.
- * per_kernel != 0: times the step's dominant kernel alone -- `steps` passes of
- * every layer's FFN gate/up GEMV launched back to back between two HIP events
- * (distinct weights per layer, so nothing is served from cache) -- and reports
- * the launch count and their algorithmic bytes. */
+ * per_kernel != 0: times the step's dominant kernel alone -- `steps` replays of
+ * a graph of every layer's FFN gate/up GEMV, back to back between two HIP
+ * events (distinct weights per layer, so nothing is served from cache; the
+ * graph keeps host enqueue gaps out) -- and reports the launch count and their
+ * algorithmic bytes. */
 typedef struct llmdot_hip_step_timing {
     float total_ms;
     float gemv_ms;           /* per_kernel: elapsed time of the gate/up launches */
