@@ -155,8 +155,9 @@ int32_t llmdot_hip_sample(llmdot_hip_ctx* ctx, const float* logits, int32_t n, c
  * recent_dev [n_recent] (may be NULL when n_recent is 0) and token_dev [1] all
  * in HBM -- enqueued on the context's stream (call llmdot_hip_synchronize
  * before reading token_dev).  The same kernels and results as
- * llmdot_hip_sample; their scratch (1 MiB + 768 B) is a static array of the
- * library, one per device, so this call allocates nothing.  n is at most
+ * llmdot_hip_sample; their scratch (9 MiB + 768 B: the scaled logits and the
+ * top-p selection buffers) is a static array of the library, one per device,
+ * so this call allocates nothing.  n is at most
  * 262144 (LLMDOT_E_UNSUPPORTED beyond).  Every call on a device shares that
  * device's scratch: calls that overlap on one device (several contexts or
  * threads) race; calls on one context's stream do not. */
