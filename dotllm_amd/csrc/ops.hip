@@ -211,18 +211,33 @@ __global__ __launch_bounds__(WG) void argmax_kernel(const float* x, int n, Argma
 // Second pass over the ncand candidates (a separate launch, so the
 // candidates are visible without fences): the token, and the device-side
 // decode-loop bookkeeping (token log, step, position).
-__global__ __launch_bounds__(WG) void argmax_finish_kernel(ArgmaxState st, int ncand) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+// One workgroup of 1024 threads; each thread's candidates (4 per pass) are
+// loaded before any is compared, so a pass costs one load latency.  Indices
+// past the end re-read the last candidate, which changes nothing.
+__global__ __launch_bounds__(WG_BIG) void argmax_finish_kernel(ArgmaxState st, int ncand) {
+    constexpr int NWF = WG_BIG / 64;
+    __shared__ float sv[NWF];
+    __shared__ int si[NWF];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int c = threadIdx.x; c < ncand; c += WG) am_pick(v, idx, st.cand_val[c], st.cand_idx[c]);
+    for (int c0 = 0; c0 < ncand; c0 += 4 * WG_BIG) {
+        float cv[4];
+        int ci[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int c = min(c0 + u * WG_BIG + (int)threadIdx.x, ncand - 1);
+            cv[u] = st.cand_val[c];
+            ci[u] = st.cand_idx[c];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) am_pick(v, idx, cv[u], ci[u]);
+    }
     wave_argmax(v, idx);
     if (lane == 0) { sv[wave] = v; si[wave] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) am_pick(v, idx, sv[w], si[w]);
+        for (int w = 1; w < NWF; w++) am_pick(v, idx, sv[w], si[w]);
         if (idx == 0x7FFFFFFF) idx = 0;   // all NaN: ArgMax returns 0
         if (st.first && __builtin_isnan(*st.first)) idx = 0;   // NaN at [0] is never replaced (VM:414-419)
         *st.token_out = idx;
@@ -353,7 +368,7 @@ hipError_t launch_argmax(const float* x, int n, const ArgmaxState& st, hipStream
 }
 hipError_t launch_argmax_finish(const ArgmaxState& st, int ncand, hipStream_t s) {
     if (ncand <= 0 || ncand > st.cap) return hipErrorInvalidValue;
-    argmax_finish_kernel<<<1, WG, 0, s>>>(st, ncand);
+    argmax_finish_kernel<<<1, WG_BIG, 0, s>>>(st, ncand);
     return hipGetLastError();
 }
 hipError_t launch_stream_probe(void* buf, size_t nbytes, int mode, uint32_t* sink, hipStream_t s) {
