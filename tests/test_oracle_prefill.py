@@ -8,10 +8,11 @@ reference's MatMul has (scalar sequential K-quant sums, 8-lane sums with a
 horizontal sum, Q3_K's own association), GQA and MHA, fp16 and fp32 KV, a
 prompt split over two calls and one that crosses the 512-token chunk.
 
-orc_set_order(1) is the same computation in another valid fp32 summation
-order; the long fixtures use it to measure how far summation order alone moves
-the logits.  It must change results (or it measures nothing), stay at fp32
-rounding size on a shallow model, and leave the reference order untouched.
+orc_set_order(1..3) is the same computation in three other valid fp32
+summation orders; the long fixtures use them to measure how far summation
+order alone moves the logits.  Each must change results (or it measures
+nothing), stay at fp32 rounding size on a shallow model, and leave the
+reference order untouched.
 """
 import json
 import os
