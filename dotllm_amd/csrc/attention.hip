@@ -13,9 +13,13 @@
 // exponent.  The sequence is split into 64-position chunks per kv head (grid
 // = chunks x kv heads; chunks past T exit).  Up to 16384 positions the
 // scores and the values run in one launch (attn_fused_kernel: the workgroups
-// of a kv head exchange their chunk maxima through tagged slots), then the
-// combine; beyond that, or with LLMDOT_HIP_ATTN_FUSED=0, three launches (each
-// reads what the previous wrote, so no fences or atomics are needed):
+// of a kv head exchange their chunk maxima through tagged slots).  Where the
+// kv heads are a multiple of 8 and a kv head's chunks fit one XCD, they all
+// run on one XCD, exchange through its L2 and also sum their partials inside
+// the launch; otherwise the exchange goes through the coherence point and the
+// combine launch follows.  Beyond 16384 positions, or with
+// LLMDOT_HIP_ATTN_FUSED=0, three launches (each reads what the previous
+// wrote, so no fences or atomics are needed):
 //   scores:  64-position chunks: RoPE + KV write + scores + chunk max (per q head).
 //            4 threads per position, each loading a quarter of the K row with
 //            16-byte loads; every K row is read once for all G q heads.
