@@ -623,47 +623,87 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         const int per = (NCOL + nch - 1) / nch;       // outputs per chunk workgroup
         const int j0 = c * per, nc = min(NCOL, j0 + per) - j0;
         if (nc <= 0) return;
-        const int ngrp = max(1, min(WG / nc, nch));   // thread groups over the chunks
-        float* cred = reinterpret_cast<float*>(pool);  // [ngrp][nc]
-        __shared__ float zs[G];
+        // Two lane layouts.  Many chunks (fewer than 64 columns each): columns
+        // run fastest over the lanes (padded to a power of two, ncp), so a load
+        // instruction reads whole runs of a chunk's columns, and a column's
+        // chunk groups meet in an xor tree inside the wavefront, then through
+        // at most four LDS partials.  Few chunks (64 or more columns): the
+        // chunk groups (at most four) run fastest and their xor tree ends the
+        // sum.  Either way ngrp groups (a power of two) each take every
+        // ngrp-th chunk, and each column also sums its head's exponent sums
+        // over the same chunks (one round of loads for both).
+        int ncp = 1;
+        while (ncp < nc) ncp *= 2;
+        const bool wide = ncp >= 64;
+        int ngrp = 1;
+        while (2 * ngrp * (wide ? nc : ncp) <= WG && 2 * ngrp <= nch && 2 * ngrp <= 64) ngrp *= 2;
+        const int np = wide ? 1 : (ngrp * ncp + 63) / 64;   // partials per column
+        float* cred = reinterpret_cast<float*>(pool);  // [np][ncp] sums of e.V, then [np][ncp] sums of e
+        float* zred = cred + np * ncp;
         const uint32_t chunk_bytes = (uint32_t)a.heads * HD * 4;
         const __amdgpu_buffer_rsrc_t ro =
             __builtin_amdgcn_make_buffer_rsrc(a.part_out, (short)0, (int)((uint32_t)nch * chunk_bytes), (int)RSRC_W3);
         const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
             a.part_sum, (short)0, (int)((uint32_t)nch * a.heads * 4), (int)RSRC_W3);
-        // loads issued four at a time before any is added (a chunk past nch
-        // reads past the buffer's end: the descriptor returns 0 there)
-        for (int idx = t; idx < nc * ngrp; idx += WG) {
-            const int col = idx % nc, g = idx / nc;
-            const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 4;
+        // column col over chunks g, g + ngrp, ... (loads past a buffer's end,
+        // chunks >= nch, return 0)
+        auto column_sum = [&](int col, int g, float& zacc) {
             float acc = 0.f;
+            zacc = 0.f;
+            const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 4;
+            const uint32_t zoff = ((uint32_t)kvh * G + (uint32_t)(j0 + col) / HD) * 4;
             for (int cc = g; cc < nch; cc += 4 * ngrp) {
-                float v[4];
+                float v[4], w[4];
 #pragma unroll
-                for (int u = 0; u < 4; u++)
-                    v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                         ro, (int)(off + (uint32_t)(cc + u * ngrp) * chunk_bytes), 0, 16));
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t ch = (uint32_t)(cc + u * ngrp);
+                    v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (int)(off + ch * chunk_bytes), 0, 16));
+                    w[u] = __builtin_bit_cast(float,
+                                              __builtin_amdgcn_raw_buffer_load_b32(rz, (int)(zoff + ch * (uint32_t)a.heads * 4), 0, 16));
+                }
 #pragma unroll
-                for (int u = 0; u < 4; u++) acc += v[u];
+                for (int u = 0; u < 4; u++) {
+                    acc += v[u];
+                    zacc += w[u];
+                }
             }
-            cred[g * nc + col] = acc;
-        }
-        for (int h = wave; h < G; h += 4) {   // the sums of exponentials, lanes over the chunks (nch <= 256)
-            float v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                     rz, (int)(((uint32_t)(lane + 64 * u) * a.heads + kvh * G + h) * 4), 0, 16));
-            float z = (v[0] + v[1]) + (v[2] + v[3]);
-            z = wave_sum(z);
-            if (lane == 0) zs[h] = z;
+            return acc;
+        };
+        if (wide) {
+            const int g = t & (ngrp - 1), slots = WG / ngrp;
+            for (int col = t / ngrp; col < nc; col += slots) {   // the ngrp lanes of a column share the loop
+                float z;
+                float acc = column_sum(col, g, z);
+                for (int o = ngrp >> 1; o > 0; o >>= 1) {
+                    acc += __shfl_xor(acc, o, 64);
+                    z += __shfl_xor(z, o, 64);
+                }
+                if (g == 0) {
+                    cred[col] = acc;
+                    zred[col] = z;
+                }
+            }
+        } else {
+            const int col = t & (ncp - 1), g = t / ncp;
+            float z = 0.f;
+            float acc = g < ngrp && col < nc ? column_sum(col, g, z) : 0.f;
+            for (int o = ncp; o < 64; o <<= 1) {   // the wavefront's groups of this column
+                acc += __shfl_xor(acc, o, 64);
+                z += __shfl_xor(z, o, 64);
+            }
+            if (lane < ncp && wave < np) {
+                cred[wave * ncp + col] = acc;
+                zred[wave * ncp + col] = z;
+            }
         }
         __syncthreads();
-        for (int col = t; col < nc; col += WG) {
-            float acc = cred[col];
-            for (int g = 1; g < ngrp; g++) acc += cred[g * nc + col];
-            const int j = j0 + col;
-            a.out[(int64_t)kvh * NCOL + j] = acc * (1.0f / zs[j / HD]);
+        for (int cl = t; cl < nc; cl += WG) {
+            float r = cred[cl], z = zred[cl];
+            for (int q = 1; q < np; q++) {
+                r += cred[q * ncp + cl];
+                z += zred[q * ncp + cl];
+            }
+            a.out[(int64_t)kvh * NCOL + j0 + cl] = r * (1.0f / z);
         }
     }
 }
