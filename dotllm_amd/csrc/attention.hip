@@ -41,7 +41,6 @@ constexpr int WG = 256;
 constexpr int CH = 64;    // positions per score chunk (scores kernel; one per lane of a wavefront)
 constexpr int CHP = 64;   // positions per pv chunk (pv kernel; its partials feed the combine)
 constexpr int XSTRIDE = 512;   // tagged chunk-maximum slots per q head (4 KiB apart)
-constexpr int READY0 = 256;    // XCD-local form: the kv head's "partials written" slots, after the maxima
 
 // N consecutive cache elements starting at element idx (16-byte aligned) as floats.
 template <int N>
@@ -334,9 +333,10 @@ __device__ __forceinline__ void poll_max(const uint64_t (&v)[HW][4], float (&res
 // kv head run on one XCD and exchange their maxima through its L2: plain
 // stores, and device-scope loads (cache policy sc1: past the CU's L1, served by
 // the L2), which see a store from the same XCD ~0.2 us after it completes
-// against ~1 us from another XCD (measured).  The chunks then meet a second
-// time, once their partials are written, and each sums every chunk's partials
-// for its own share of the kv head's outputs, so no combine launch follows.
+// against ~1 us from another XCD (measured).  The partials go out the same
+// way, as tagged words, and each chunk sums every chunk's partials for its
+// own share of the kv head's outputs (reloading words whose tag is not yet
+// this step's), so no combine launch follows.
 // Each workgroup folds its own o (from its XCC_ID register) into the tag it
 // publishes, so a chunk placed on another XCD never matches: its kv head's
 // wait ends at the spin limit with the device error set, instead of mixing
@@ -558,9 +558,16 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         sc_s[h][pp] = pp < cnt ? e : 0.f;
     }
     __syncthreads();   // exponentials visible; the V rows are in registers (pool reused below)
+    // XL: the partials go out as tagged 64-bit words, (tag << 32) | float bits,
+    // which the kv head's other chunks poll for (no separate "written" flag)
+    uint64_t* const xz = XL ? a.xpart + (int64_t)((a.context + CH - 1) / CH) * a.heads * HD : nullptr;   // [chunks][heads]
     for (int h = wave; h < G; h += 4) {   // this chunk's sum of exponentials
         const float z = wave_sum(sc_s[h][lane]);
-        if (lane == 0) a.part_sum[(int64_t)c * a.heads + kvh * G + h] = z;
+        if (lane == 0) {
+            if (XL) __hip_atomic_store(xz + (int64_t)c * a.heads + kvh * G + h, ((uint64_t)tag << 32) | __float_as_uint(z),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            else a.part_sum[(int64_t)c * a.heads + kvh * G + h] = z;
+        }
     }
     float (*red)[G * HD + 4] = reinterpret_cast<float (*)[G * HD + 4]>(pool);
 #pragma unroll
@@ -590,34 +597,16 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         float r = 0.f;
 #pragma unroll
         for (int q = 0; q < NGR; q += 4) r += (red[q][idx] + red[q + 1][idx]) + (red[q + 2][idx] + red[q + 3][idx]);
-        a.part_out[((int64_t)c * a.heads + kvh * G + h) * HD + d] = r;
+        const int64_t o = ((int64_t)c * a.heads + kvh * G + h) * HD + d;
+        if (XL) __hip_atomic_store(a.xpart + o, ((uint64_t)tag << 32) | __float_as_uint(r), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        else a.part_out[o] = r;
     }
     if (XL) {
-        // The combine without a launch: every chunk of the kv head publishes
-        // "partials written" (after its stores reached the L2) and waits for the
-        // others, as for the maxima; then each workgroup sums all chunks for
-        // its own share of the kv head's G*HD outputs.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const uint32_t rbase = (uint32_t)((kvh * G) * mc + READY0) * 8;   // the kv head's ready slots
-        if (t == 0)
-            __hip_atomic_store(a.xmax + rbase / 8 + c, (uint64_t)tag << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-            a.xmax, (short)0, (int)((uint32_t)a.heads * XSTRIDE * 8), (int)RSRC_W3);
-        if (wave == 0) {
-            uint64_t v[1][4];
-            for (int it = 0;; it++) {
-                asm volatile("" ::: "memory");   // a fresh load every poll
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[0][i] = l2_load64(rx, rbase + 8 * (uint32_t)min(lane + 64 * i, nch - 1));
-                if (poll_ready<1>(v, tag)) break;
-                if (it >= a.spin_max) {
-                    if (lane == 0) atomicOr(a.err, 1);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
+        // The combine without a launch: each workgroup sums every chunk's
+        // partials for its own share of the kv head's G*HD outputs, polling the
+        // tagged words until each carries this step's tag (the barrier only
+        // frees the LDS pool for reuse).
         __syncthreads();
         constexpr int NCOL = G * HD;                  // outputs of the kv head
         const int per = (NCOL + nch - 1) / nch;       // outputs per chunk workgroup
@@ -640,31 +629,44 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         const int np = wide ? 1 : (ngrp * ncp + 63) / 64;   // partials per column
         float* cred = reinterpret_cast<float*>(pool);  // [np][ncp] sums of e.V, then [np][ncp] sums of e
         float* zred = cred + np * ncp;
-        const uint32_t chunk_bytes = (uint32_t)a.heads * HD * 4;
+        const uint32_t chunk_bytes = (uint32_t)a.heads * HD * 8;
         const __amdgpu_buffer_rsrc_t ro =
-            __builtin_amdgcn_make_buffer_rsrc(a.part_out, (short)0, (int)((uint32_t)nch * chunk_bytes), (int)RSRC_W3);
-        const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
-            a.part_sum, (short)0, (int)((uint32_t)nch * a.heads * 4), (int)RSRC_W3);
-        // column col over chunks g, g + ngrp, ... (loads past a buffer's end,
-        // chunks >= nch, return 0)
+            __builtin_amdgcn_make_buffer_rsrc(a.xpart, (short)0, (int)((uint32_t)nch * chunk_bytes), (int)RSRC_W3);
+        const __amdgpu_buffer_rsrc_t rz =
+            __builtin_amdgcn_make_buffer_rsrc(xz, (short)0, (int)((uint32_t)nch * a.heads * 8), (int)RSRC_W3);
+        // column col over chunks g, g + ngrp, ...: the four chunks' words are
+        // loaded again until every live one carries the tag (chunks >= nch
+        // read past the buffer's end and count as 0)
         auto column_sum = [&](int col, int g, float& zacc) {
             float acc = 0.f;
             zacc = 0.f;
-            const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 4;
-            const uint32_t zoff = ((uint32_t)kvh * G + (uint32_t)(j0 + col) / HD) * 4;
+            const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 8;
+            const uint32_t zoff = ((uint32_t)kvh * G + (uint32_t)(j0 + col) / HD) * 8;
             for (int cc = g; cc < nch; cc += 4 * ngrp) {
-                float v[4], w[4];
+                uint64_t v[4], w[4];
+                for (int it = 0;; it++) {
+                    asm volatile("" ::: "memory");   // a fresh load every poll
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const uint32_t ch = (uint32_t)(cc + u * ngrp);
-                    v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (int)(off + ch * chunk_bytes), 0, 16));
-                    w[u] = __builtin_bit_cast(float,
-                                              __builtin_amdgcn_raw_buffer_load_b32(rz, (int)(zoff + ch * (uint32_t)a.heads * 4), 0, 16));
+                    for (int u = 0; u < 4; u++) {
+                        const uint32_t ch = (uint32_t)(cc + u * ngrp);
+                        v[u] = l2_load64(ro, off + ch * chunk_bytes);
+                        w[u] = l2_load64(rz, zoff + ch * (uint32_t)a.heads * 8);
+                    }
+                    bool ok = true;
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        ok = ok && (cc + u * ngrp >= nch || ((uint32_t)(v[u] >> 32) == tag && (uint32_t)(w[u] >> 32) == tag));
+                    if (ok) break;
+                    if (it >= a.spin_max) {
+                        atomicOr(a.err, 1);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    acc += v[u];
-                    zacc += w[u];
+                    acc += __uint_as_float((uint32_t)v[u]);
+                    zacc += __uint_as_float((uint32_t)w[u]);
                 }
             }
             return acc;
@@ -747,7 +749,7 @@ hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
         if (!a.xmax || !a.epoch || !a.err || !attn_fused_ok(a.heads, a.kv_heads, a.head_dim, a.context))
             return hipErrorInvalidValue;
         if (a.xcd_exchange) {   // XCD-local exchange: one-dimensional grid
-            if (a.kv_heads % 8) return hipErrorInvalidValue;
+            if (a.kv_heads % 8 || !a.xpart) return hipErrorInvalidValue;
             const dim3 grid(nchunks * a.kv_heads);
             if (a.kv_fp16) attn_fused_kernel<HD, G, true, true><<<grid, WG, 0, s>>>(a);
             else attn_fused_kernel<HD, G, false, true><<<grid, WG, 0, s>>>(a);

@@ -842,6 +842,7 @@ struct llmdot_hip_model {
     // attention scratch
     float *scores = nullptr, *chunk_max = nullptr, *part_out = nullptr, *part_sum = nullptr;
     uint64_t* xmax = nullptr;   // tagged chunk maxima of the one-launch attention
+    uint64_t* xpart = nullptr;  // tagged chunk partials of its XCD-local form
     bool attn_fused = false;
     int attn_spin = 1 << 18;
     bool attn_xcd_exchange = false;    // one-launch attention: chunk maxima through the kv head's XCD L2
@@ -1015,7 +1016,7 @@ int enqueue_step(llmdot_hip_model* m) {
         aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
         aa.fused = m->attn_fused ? 1 : 0; aa.xmax = m->xmax; aa.epoch = m_epoch(m);
         aa.layer = l; aa.layers = d.layers; aa.spin_max = m->attn_spin; aa.err = m_err(m);
-        aa.xcd_exchange = m->attn_xcd_exchange ? 1 : 0;
+        aa.xcd_exchange = m->attn_xcd_exchange ? 1 : 0; aa.xpart = m->xpart;
         HIPCHK(launch_attention(aa, s));
         {   // O projection + residual (IE:444-449, IE:189), h packed for the FFN RmsNorm
             GemvArgs ga{};
@@ -1387,6 +1388,8 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
             want = ok;
         }
         m->attn_xcd_exchange = want;
+        if (want && (rc = A(sizeof(uint64_t) * (size_t)nch * d.heads * (d.head_dim + 1), &p))) return bail(rc);
+        if (want) m->xpart = (uint64_t*)p;
     }
     if ((rc = A(64, &p))) return bail(rc); m->ints = (int32_t*)p;
     if ((rc = A(sizeof(int32_t) * (size_t)(d.context + 1), &p))) return bail(rc); m->token_log = (int32_t*)p;

@@ -134,6 +134,10 @@ struct AttnArgs {
     // another XCD than the rest of its kv head makes that kv head's wait give
     // up (*err) rather than mix L2s.
     int xcd_exchange;
+    // XCD-local form: the chunk partials as tagged words, (tag << 32) | float
+    // bits: [max_chunks][heads][head_dim] sums of e.V, then [max_chunks][heads]
+    // sums of e (max_chunks = attn_max_chunks)
+    uint64_t* xpart;
 };
 // Whether the XCD-local exchange suits the shape: kv heads a multiple of 8,
 // and every live chunk of the kv heads one XCD serves (kv_heads / 8 of them,
