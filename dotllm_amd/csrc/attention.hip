@@ -500,27 +500,48 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         }
         const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
             a.xmax, (short)0, (int)((uint32_t)a.heads * XSTRIDE * 8), (int)RSRC_W3);
-        for (int h = wave; h < G; h += 2) {
-            uint64_t v[1][4];
-            float res[1];
-            for (int it = 0;; it++) {
-                if (XL) {
+        if (XL) {   // all of the wavefront's heads in one poll loop
+            constexpr int HW = (G + 1) / 2;
+            const int nh = (G - wave + 1) / 2;   // heads of this wavefront (none: wavefront 1 when G = 1)
+            if (nh > 0) {
+                uint64_t v[HW][4];
+                float res[HW];
+                for (int it = 0;; it++) {
                     asm volatile("" ::: "memory");   // a fresh load every poll
-                    const uint32_t base = (uint32_t)((kvh * G + h) * mc) * 8;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) v[0][i] = l2_load64(rx, base + 8 * (uint32_t)min(lane + 64 * i, nch - 1));
-                } else {
-                    poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, nch, mc);
+                    for (int j = 0; j < HW; j++) {
+                        const uint32_t base = (uint32_t)((kvh * G + wave + 2 * min(j, nh - 1)) * mc) * 8;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) v[j][i] = l2_load64(rx, base + 8 * (uint32_t)min(lane + 64 * i, nch - 1));
+                    }
+                    if (poll_ready<HW>(v, tag)) break;
+                    if (it >= a.spin_max) {
+                        if (lane == 0) atomicOr(a.err, 1);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
                 }
-                if (poll_ready<1>(v, tag)) break;
-                if (it >= a.spin_max) {
-                    if (lane == 0) atomicOr(a.err, 1);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
+                poll_max<HW>(v, res);
+#pragma unroll
+                for (int j = 0; j < HW; j++)
+                    if (lane == 0 && j < nh) gmax[wave + 2 * j] = res[j];
             }
-            poll_max<1>(v, res);
-            if (lane == 0) gmax[h] = res[0];
+        } else {
+            for (int h = wave; h < G; h += 2) {
+                uint64_t v[1][4];
+                float res[1];
+                for (int it = 0;; it++) {
+                    poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, nch, mc);
+                    if (poll_ready<1>(v, tag)) break;
+                    if (it >= a.spin_max) {
+                        if (lane == 0) atomicOr(a.err, 1);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                poll_max<1>(v, res);
+                if (lane == 0) gmax[h] = res[0];
+            }
         }
     }
     __syncthreads();
