@@ -732,13 +732,28 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x >> 6) / HV;   // waves per half
     const int half = wave / nw, hw = wave - half * nw;
-    // segment and first row of this workgroup
-    int blk = blockIdx.x, si = 0;
-    for (; si < a.nseg - 1; si++) {
-        if (blk < a.seg[si].wgs) break;
-        blk -= a.seg[si].wgs;
-    }
-    const GemvSeg seg = a.seg[si];
+    // Segment and first row of this workgroup.  Every argument is read at once
+    // and the segment picked by selects: a search loop made each argument load
+    // wait for the one before it (~0.8 us of dependent round trips before the
+    // first activation load, measured).
+    const GemvSeg s0 = a.seg[0], s1 = a.seg[1], s2 = a.seg[2];
+    int blk = blockIdx.x;
+    const bool in1 = a.nseg > 1 && blk >= s0.wgs;
+    const bool in2 = in1 && a.nseg > 2 && blk >= s0.wgs + s1.wgs;
+    blk -= in2 ? s0.wgs + s1.wgs : (in1 ? s0.wgs : 0);
+    GemvSeg seg;
+    seg.w = in2 ? s2.w : (in1 ? s1.w : s0.w);
+    seg.w2 = in2 ? s2.w2 : (in1 ? s1.w2 : s0.w2);
+    seg.out = in2 ? s2.out : (in1 ? s1.out : s0.out);
+    seg.rows = in2 ? s2.rows : (in1 ? s1.rows : s0.rows);
+    seg.wgs = in2 ? s2.wgs : (in1 ? s1.wgs : s0.wgs);
+    seg.type = in2 ? s2.type : (in1 ? s1.type : s0.type);
+    // the remaining arguments the first loads and the epilogue need, in SGPRs
+    // in the same round
+    asm volatile("" ::"s"(a.x), "s"(a.ssq), "s"(seg.w), "s"(seg.w2), "s"(seg.out), "s"(a.pack_w), "s"(a.cols));
+    if (EPI == EPI_ADD) asm volatile("" ::"s"(a.pack_out), "s"(a.pack_ssq));
+    if (NORM) asm volatile("" ::"s"(a.eps));
+    if (EPI == EPI_ARGMAX) asm volatile("" ::"s"(a.am.cand_val), "s"(a.am.cand_idx));
     // Output rows in slabs of SLAB: slab j of this workgroup is rows
     // (j * wgs + blk) * SLAB ..., so at any moment the workgroups of a
     // segment stream through one contiguous stretch of each matrix.  The ADD
@@ -778,14 +793,15 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         for (int k = 0; k < 4; k++) sq[k] = a.ssq[min((int)threadIdx.x + k * (int)blockDim.x, nq - 1)];
     }
     // ADD: the residual and norm weight of this lane's output row, loaded
-    // before the rows so the epilogue does not wait on them
+    // before the rows so the epilogue does not wait on them; unconditional
+    // (clamped row, and the output itself standing in for an absent norm
+    // weight), so no branch waits on an argument: the epilogue uses them only
+    // for valid rows
     float res = 0.f, pw = 0.f;
-    if (EPI == EPI_ADD && (int)threadIdx.x < rows_wg) {
-        const int r = out_row(threadIdx.x);
-        if (r < seg.rows) {
-            res = seg.out[r];
-            if (a.pack_out) pw = a.pack_w[r];
-        }
+    if (EPI == EPI_ADD) {
+        const int r = min(out_row(min((int)threadIdx.x, rows_wg - 1)), seg.rows - 1);
+        res = seg.out[r];
+        pw = (a.pack_out ? a.pack_w : seg.out)[r];
     }
     if (T2 != T && second) gemv_rows<TT2, NB2>(a, uu, has, row_ptr, red[wave]);
     else gemv_rows<TT, NB, HV>(a, uu, has, row_ptr, red[wave], half == 0, xq_s, K / 32);
