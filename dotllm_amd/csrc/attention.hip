@@ -382,7 +382,13 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
     __shared__ float sc_s[G][CH];                 // scores (-inf past T), then exponentials
     __shared__ float gmax[G];
     __shared__ __align__(16) uint8_t pool[VBUF > RED ? VBUF : RED];   // V rows, then the partial sums
-    const int T = *a.pos, n = T + 1, n8 = n & ~7;
+    // Every kernel argument in one round (a load of an argument that waits on
+    // another's use adds a scalar round trip to every launch).
+    asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kcache), "s"(a.vcache), "s"(a.cos_tab), "s"(a.sin_tab),
+                 "s"(a.pos), "s"(a.epoch), "s"(a.heads), "s"(a.kv_heads), "s"(a.rope_half), "s"(a.context));
+    asm volatile("" ::"s"(a.xmax), "s"(a.layer), "s"(a.layers), "s"(a.spin_max), "s"(a.err), "s"(a.out));
+    if (XL) asm volatile("" ::"s"(a.xpart));
+    __builtin_amdgcn_sched_barrier(0);   // the argument loads go out together, before any use
     int c, kvh;
     if (XL) {   // one-dimensional grid: kv head (w mod 8) + 8 j, chunk c; one XCD per kv head
         const int w = blockIdx.x, per = a.kv_heads >> 3, r = w >> 3;
@@ -392,51 +398,62 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         c = blockIdx.x;
         kvh = blockIdx.y;
     }
-    const int p0 = c * CH;
-    if (p0 >= n) return;
-    const int nch = (n + CH - 1) / CH;            // live chunks of every kv head
-    const int cnt = min(CH, n - p0);
-    const int mc = XSTRIDE;                       // slots per head: one 4 KiB page each
-    uint32_t tag = *a.epoch * (uint32_t)a.layers + (uint32_t)a.layer + 1u;
-    if (XL) tag = (tag << 3) | ((xcc_id() - blockIdx.x) & 7u);   // the launch's XCD offset, as this workgroup sees it
     const int half = a.rope_half;
-    const float* cs = a.cos_tab + (int64_t)T * half;
-    const float* sn = a.sin_tab + (int64_t)T * half;
-    const int64_t cache_base = (int64_t)kvh * a.context * HD;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const bool kwave = wave < 2;
-
-    // Loads in the order they are consumed (each wavefront's wait counter
-    // retires them in issue order): q, the RoPE table and the new token's k
-    // and v first, then the thread's half row of K (wavefronts 0-1) or of V
-    // (2-3).  Rows past T read row p0 (written) and are masked; row T is
-    // written below by this workgroup and taken from LDS instead.
+    // Loads: the position and the epoch first (each wavefront's wait counter
+    // retires loads in issue order, so waiting for them waits for nothing
+    // else), then q and the new token's k and v, which do not need the
+    // position; after it, the RoPE table rows of the position and the
+    // thread's half row of K (wavefronts 0-1) or of V (2-3).  Rows past T read
+    // row p0 (written) and are masked; row T is written below by this
+    // workgroup and taken from LDS instead.
+    const int T = *a.pos;
+    const uint32_t epoch = *a.epoch;
     constexpr int QI = (G * HD + WG - 1) / WG;    // q elements per thread
-    const bool owner = T >= p0 && T < p0 + CH;
     float qa[QI], qb[QI], qc[QI], qs[QI];
 #pragma unroll
     for (int j = 0; j < QI; j++) {
         const int idx = min(t + j * WG, G * HD - 1);
         const int h = idx / HD, d = idx - h * HD;
         const float* x = a.q + (int64_t)(kvh * G + h) * HD;
-        const int i = d < half ? d : (d < 2 * half ? d - half : 0);
         qa[j] = x[d];
         qb[j] = x[d < half ? d + half : (d < 2 * half ? d - half : d)];
-        qc[j] = cs[i];
-        qs[j] = sn[i];
     }
     // the new token's k pair and v element (read by every workgroup, used by
     // the owner: a load under a branch would be waited on inside it)
     float ka, kb, kc, ks, vn;
+    const int dk = t < HD ? t : 0, ik = dk < half ? dk : (dk < 2 * half ? dk - half : 0);
     {
         const float* x = a.k + (int64_t)kvh * HD;
-        const int d = t < HD ? t : 0, i = d < half ? d : (d < 2 * half ? d - half : 0);
-        ka = x[d];
-        kb = x[d < half ? d + half : (d < 2 * half ? d - half : d)];
-        kc = cs[i];
-        ks = sn[i];
-        vn = a.v[(int64_t)kvh * HD + d];
+        ka = x[dk];
+        kb = x[dk < half ? dk + half : (dk < 2 * half ? dk - half : dk)];
+        vn = a.v[(int64_t)kvh * HD + dk];
     }
+    // nothing above moves below the exit (a load used only past it would be
+    // sunk there, behind the wait for the position)
+    asm volatile("" ::: "memory");
+    const int p0 = c * CH;
+    const int n = T + 1, n8 = n & ~7;
+    if (p0 >= n) return;
+    const int nch = (n + CH - 1) / CH;            // live chunks of every kv head
+    const int cnt = min(CH, n - p0);
+    const int mc = XSTRIDE;                       // slots per head: one 4 KiB page each
+    uint32_t tag = epoch * (uint32_t)a.layers + (uint32_t)a.layer + 1u;
+    if (XL) tag = (tag << 3) | ((xcc_id() - blockIdx.x) & 7u);   // the launch's XCD offset, as this workgroup sees it
+    const float* cs = a.cos_tab + (int64_t)T * half;
+    const float* sn = a.sin_tab + (int64_t)T * half;
+    const int64_t cache_base = (int64_t)kvh * a.context * HD;
+    const bool owner = T >= p0 && T < p0 + CH;
+#pragma unroll
+    for (int j = 0; j < QI; j++) {
+        const int idx = min(t + j * WG, G * HD - 1);
+        const int d = idx % HD, i = d < half ? d : (d < 2 * half ? d - half : 0);
+        qc[j] = cs[i];
+        qs[j] = sn[i];
+    }
+    kc = cs[ik];
+    ks = sn[ik];
     __builtin_amdgcn_sched_barrier(0);   // the small loads stay ahead of the rows
     const int lt = t & 127, rp = lt >> 1, rh = lt & 1;   // row (position) and half of it
     const int rpos = p0 + rp;
