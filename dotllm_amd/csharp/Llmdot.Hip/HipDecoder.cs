@@ -34,7 +34,7 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
 {
     private static int s_next;
     private static readonly string[] LayerTensors =
-        ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"];
+        ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_qkv", "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"];
 
     private readonly LoadedModel _model;
     private readonly HipBackend _backend;
@@ -49,7 +49,7 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
 
     /// <summary>
     /// Whether the device step covers this model: the LLaMA-like template with
-    /// RMSNorm, separate Q/K/V, SwiGLU, no sliding window, softcaps, post-norms,
+    /// RMSNorm, separate or fused Q/K/V, SwiGLU, no sliding window, softcaps, post-norms,
     /// Q/K norms, experts or convolution layers, one KV head count for every
     /// layer, and an embedding scale of 1 (the paths of IE:134-196 and
     /// IE:304-476 that the LLaMA, Mistral, Phi-3 and Qwen2 GGUFs take).
@@ -60,7 +60,6 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
         reason = c.Template != ExecutionTemplate.LlamaLike ? $"template {c.Template}"
             : c.NormType != NormType.RmsNorm ? $"norm {c.NormType}"
             : c.FfnType != FfnType.SwiGLU ? $"FFN {c.FfnType}"
-            : c.QkvLayout == QkvLayout.Fused ? "fused QKV"
             : c.SlidingWindow > 0 ? "sliding-window attention"
             : c.ExpertCount > 0 ? "mixture of experts"
             : c.HasConvLayers ? "convolution layers"
@@ -101,9 +100,16 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
     {
         var names = new List<string> { "token_embd.weight", "output_norm.weight" };
         if (_model.TryGetTensor("output.weight", out _)) names.Add("output.weight");   // else tied (IE:586-589)
+        // fused Q/K/V (IE:321-332): the library takes blk.N.attn_qkv.weight in
+        // place of the three projections and reads Q, K, V as its row ranges
+        var fused = _cfg.QkvLayout == QkvLayout.Fused;
         for (var l = 0; l < _cfg.LayerCount; l++)
             foreach (var t in LayerTensors)
+            {
+                if (fused ? t is "attn_q" or "attn_k" or "attn_v" : t == "attn_qkv") continue;
+                if (t == "ffn_norm" && !_model.TryGetTensor($"blk.{l}.ffn_norm.weight", out _)) continue;
                 names.Add($"blk.{l}.{t}.weight");
+            }
         foreach (var name in names)
         {
             var t = _model.GetTensor(name);

@@ -23,6 +23,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <deque>
 #include <set>
 #include <string>
 #include <unordered_map>
@@ -830,6 +831,7 @@ struct llmdot_hip_model {
     const Weight *embd = nullptr, *out = nullptr, *out_norm = nullptr;
     float* out_norm_f = nullptr;
     std::vector<void*> owned;          // device allocations owned by the model
+    std::deque<Weight> views;          // Q, K and V row ranges of fused attn_qkv tensors
     // activations
     float *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
     // h packed for its next RmsNorm consumer: xn = w * h, xssq[i] = sum of h^2 over h[8i .. 8i+7]
@@ -1302,15 +1304,45 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
         return bail(fail(LLMDOT_E_UNSUPPORTED, "token_embd type not supported"));
     if ((rc = norm_f32(m, onorm, d.hidden, &m->out_norm_f))) return bail(rc);
     m->L.resize((size_t)d.layers);
+    // Fused Q/K/V (QkvLayout.Fused, ArchitectureResolver.cs:145-146: some
+    // tensor is an attn_qkv): every layer then has blk.N.attn_qkv.weight
+    // (TensorNameResolver.cs:123-126) of qdim + 2 kvdim rows, Q, K, V in that
+    // order, and the reference's one product over it split into q, k, v
+    // (IE:321-332) equals the three products over its row ranges, each output
+    // row being its own dot product: Q, K and V are views of the one tensor.
+    bool fused = false;
+    for (int l = 0; l < d.layers && !fused; l++)
+        fused = m->ctx->weights.count(m->prefix + "blk." + std::to_string(l) + ".attn_qkv.weight") > 0;
     for (int l = 0; l < d.layers; l++) {
         LayerW& w = m->L[l];
         const std::string p = "blk." + std::to_string(l) + ".";
         if ((rc = need_w(m, p + "attn_norm.weight", -1, -1, &w.attn_norm))) return bail(rc);
         w.ffn_norm = find_w(m, p + "ffn_norm.weight");
         if (!w.ffn_norm) w.ffn_norm = w.attn_norm;   // IE:547
-        if ((rc = need_w(m, p + "attn_q.weight", qdim, d.hidden, &w.q))) return bail(rc);
-        if ((rc = need_w(m, p + "attn_k.weight", kvdim, d.hidden, &w.k))) return bail(rc);
-        if ((rc = need_w(m, p + "attn_v.weight", kvdim, d.hidden, &w.v))) return bail(rc);
+        if (fused) {
+            const Weight* f = find_w(m, p + "attn_qkv.weight");
+            if (!f)
+                return bail(fail(LLMDOT_E_NOT_FOUND, "Expected fused QKV tensor '" + m->prefix + p +
+                                                         "attn_qkv.weight' for QkvLayout.Fused."));
+            if ((rc = need_w(m, p + "attn_qkv.weight", qdim + 2 * kvdim, d.hidden, &f))) return bail(rc);
+            const int64_t rb = byte_count(f->type, d.hidden);
+            auto view = [&](int64_t r0, int64_t nr) {
+                Weight& v = m->views.emplace_back();
+                v.type = f->type;
+                v.rows = nr;
+                v.cols = d.hidden;
+                v.nbytes = (size_t)(nr * rb);
+                v.dev = f->dev + r0 * rb;
+                return (const Weight*)&v;
+            };
+            w.q = view(0, qdim);
+            w.k = view(qdim, kvdim);
+            w.v = view(qdim + kvdim, kvdim);
+        } else {
+            if ((rc = need_w(m, p + "attn_q.weight", qdim, d.hidden, &w.q))) return bail(rc);
+            if ((rc = need_w(m, p + "attn_k.weight", kvdim, d.hidden, &w.k))) return bail(rc);
+            if ((rc = need_w(m, p + "attn_v.weight", kvdim, d.hidden, &w.v))) return bail(rc);
+        }
         if ((rc = need_w(m, p + "attn_output.weight", d.hidden, qdim, &w.o))) return bail(rc);
         if ((rc = need_w(m, p + "ffn_gate.weight", d.ffn, d.hidden, &w.gate))) return bail(rc);
         if ((rc = need_w(m, p + "ffn_up.weight", d.ffn, d.hidden, &w.up))) return bail(rc);

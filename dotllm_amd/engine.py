@@ -47,7 +47,8 @@ def greedy(max_tokens: int) -> GenerationOptions:
 
 
 # Tensor names of the LLaMA-like template (src/Llmdot.Core/Loading/TensorNameResolver.cs:22-107).
-LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")
+LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_qkv", "attn_output", "ffn_norm", "ffn_gate", "ffn_up",
+                 "ffn_down")
 
 
 class LoadedModel:
@@ -96,8 +97,8 @@ class InferenceEngine:
     def __init__(self, model: LoadedModel, backend: HipBackend | None = None, *, kv_fp16: bool = True,
                  context: int | None = None):
         cfg = model.config
-        if cfg.qkv_fused or cfg.ffn_type != "swiglu":
-            raise NotImplementedError("only separate Q/K/V and SwiGLU FFN tensors are supported")
+        if cfg.ffn_type != "swiglu":
+            raise NotImplementedError("only SwiGLU FFN tensors are supported")
         if cfg.sliding_window:
             raise NotImplementedError("sliding-window attention is not supported")
         if cfg.qk_norm:

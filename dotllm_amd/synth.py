@@ -61,18 +61,23 @@ def tensor_type(mix: str, name: str) -> int:
     raise ValueError(f"unknown mix {mix}")
 
 
-def tensor_list(spec: dict) -> list:
-    """(name, rows, cols, ggml_type) in file order."""
+def tensor_list(spec: dict, fused_qkv: bool = False) -> list:
+    """(name, rows, cols, ggml_type) in file order.  fused_qkv: one
+    blk.N.attn_qkv.weight of q + 2 kv rows (Q, then K, then V, in attn_q's
+    type) in place of the three attention projections, the layout of Phi-3
+    GGUFs (QkvLayout.Fused)."""
     d, f, v = spec["hidden"], spec["ffn"], spec["vocab"]
     q, kv = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
     out = [("token_embd.weight", v, d)]
     for l in range(spec["layers"]):
         p = f"blk.{l}."
-        out += [(p + "attn_norm.weight", 1, d), (p + "attn_q.weight", q, d), (p + "attn_k.weight", kv, d),
-                (p + "attn_v.weight", kv, d), (p + "attn_output.weight", d, q), (p + "ffn_norm.weight", 1, d),
-                (p + "ffn_gate.weight", f, d), (p + "ffn_up.weight", f, d), (p + "ffn_down.weight", d, f)]
+        qkv = ([(p + "attn_qkv.weight", q + 2 * kv, d)] if fused_qkv else
+               [(p + "attn_q.weight", q, d), (p + "attn_k.weight", kv, d), (p + "attn_v.weight", kv, d)])
+        out += [(p + "attn_norm.weight", 1, d)] + qkv + [
+            (p + "attn_output.weight", d, q), (p + "ffn_norm.weight", 1, d),
+            (p + "ffn_gate.weight", f, d), (p + "ffn_up.weight", f, d), (p + "ffn_down.weight", d, f)]
     out += [("output_norm.weight", 1, d), ("output.weight", v, d)]
-    return [(n, r, c, tensor_type(spec["mix"], n)) for n, r, c in out]
+    return [(n, r, c, tensor_type(spec["mix"], n.replace("attn_qkv", "attn_q"))) for n, r, c in out]
 
 
 def tensor_seed(seed: int, name: str) -> int:
@@ -125,15 +130,19 @@ def tensor_sigma(name: str, spec: dict, sigma: float, scaled_init: bool) -> floa
 
 def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
                 threads: int | None = None, spec: dict | None = None, scaled_init: bool = False,
-                eos: int = -1, tied: bool = False, norm_type: int = F32) -> np.ndarray:
+                eos: int = -1, tied: bool = False, norm_type: int = F32, fused_qkv: bool = False) -> np.ndarray:
     """Builds the whole GGUF file image in memory (uint8 numpy array).
 
     eos: tokenizer.ggml.eos_token_id (-1: never stops); tied: no output.weight,
     so the LM head reads token_embd.weight (InferenceEngine.cs:585-589);
-    norm_type: F32 or F16 RMSNorm weights (ones either way)."""
+    norm_type: F32 or F16 RMSNorm weights (ones either way); fused_qkv: Q, K
+    and V rows in one attn_qkv tensor, each range filled exactly as the
+    separate tensor of the same type would be (same seed), so a fused image
+    holds the same weights as the separate one wherever the types agree."""
     spec = spec or SPECS[name]
-    tl = [(n, r, c, (norm_type if n.endswith("_norm.weight") else t)) for n, r, c, t in tensor_list(spec)
+    tl = [(n, r, c, (norm_type if n.endswith("_norm.weight") else t)) for n, r, c, t in tensor_list(spec, fused_qkv)
           if not (tied and n == "output.weight")]
+    qd, kvd = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
     infos = [(n, (c,) if r == 1 else (c, r), t, byte_count(t, r * c)) for n, r, c, t in tl]
     hdr, offsets, total = gguf.header_bytes(metadata(spec, context, eos), infos)
     img = np.empty(total, dtype=np.uint8)
@@ -149,6 +158,14 @@ def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int |
                 view.view(np.float16)[:] = 1.0
             else:
                 raise ValueError("norm weights are F32 or F16")
+        elif n.endswith("attn_qkv.weight"):
+            rb = byte_count(t, c)
+            o = 0
+            for part, pr in (("attn_q", qd), ("attn_k", kvd), ("attn_v", kvd)):
+                pn = n.replace("attn_qkv", part)
+                synth_tensor(t, pr, c, tensor_seed(seed, pn), view[o:o + pr * rb],
+                             tensor_sigma(pn, spec, sigma, scaled_init), threads)
+                o += pr * rb
         else:
             synth_tensor(t, r, c, tensor_seed(seed, n), view, tensor_sigma(n, spec, sigma, scaled_init), threads)
         nxt = base + off + nb
@@ -176,9 +193,10 @@ def quantize(ggml_type: int, x: np.ndarray) -> np.ndarray:
 QUANT_NAMES = {"f32": F32, "q8_0": Q8_0, "q4_0": _lib.Q4_0, "q4_k": Q4_K, "q5_k": _lib.Q5_K, "q6_k": Q6_K}
 
 
-def write_model(name: str, path: str, seed: int = 1234, context: int | None = None, sigma: float = 0.02) -> int:
+def write_model(name: str, path: str, seed: int = 1234, context: int | None = None, sigma: float = 0.02,
+                fused_qkv: bool = False) -> int:
     """Writes the seeded synthetic model `name` (SPECS) as a GGUF file; returns its size."""
-    img = build_image(name, seed=seed, sigma=sigma, context=context)
+    img = build_image(name, seed=seed, sigma=sigma, context=context, fused_qkv=fused_qkv)
     with open(path, "wb") as f:
         f.write(img.tobytes())
     return int(img.size)
@@ -215,7 +233,7 @@ def quantize_tensors(tensors: dict, ggml_type: int, path: str, metadata_items: l
 
 
 def main(argv=None) -> int:
-    """python -m dotllm_amd.synth model NAME OUT.gguf [--seed S] [--context N] [--sigma X]
+    """python -m dotllm_amd.synth model NAME OUT.gguf [--seed S] [--context N] [--sigma X] [--fused-qkv]
     python -m dotllm_amd.synth quantize IN.npz OUT.gguf --type q4_k|q5_k|q6_k|q8_0|q4_0|f32"""
     import argparse
     ap = argparse.ArgumentParser(prog="python -m dotllm_amd.synth",
@@ -227,13 +245,14 @@ def main(argv=None) -> int:
     m.add_argument("--seed", type=int, default=1234)
     m.add_argument("--context", type=int, default=None)
     m.add_argument("--sigma", type=float, default=0.02)
+    m.add_argument("--fused-qkv", action="store_true", help="one attn_qkv tensor per layer (the Phi-3 GGUF layout)")
     q = sub.add_parser("quantize", help="quantize the fp32 arrays of an .npz file into a GGUF file")
     q.add_argument("inp")
     q.add_argument("out")
     q.add_argument("--type", required=True, choices=sorted(QUANT_NAMES))
     args = ap.parse_args(argv)
     if args.cmd == "model":
-        n = write_model(args.name, args.out, args.seed, args.context, args.sigma)
+        n = write_model(args.name, args.out, args.seed, args.context, args.sigma, args.fused_qkv)
     else:
         with np.load(args.inp, allow_pickle=False) as z:
             tensors = {k: z[k] for k in z.files}

@@ -207,7 +207,11 @@ typedef struct llmdot_hip_model_desc {
     /* Weight keys follow GGUF tensor names (src/Llmdot.Core/Loading/TensorNameResolver.cs:22-107):
      * token_embd.weight, output_norm.weight, output.weight (optional: tied to
      * token_embd), blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,
-     * ffn_gate,ffn_up,ffn_down}.weight, each optionally prefixed by key_prefix. */
+     * ffn_gate,ffn_up,ffn_down}.weight, each optionally prefixed by key_prefix.
+     * Fused Q/K/V (QkvLayout.Fused, ArchitectureResolver.cs:145-146): when any
+     * layer has blk.N.attn_qkv.weight (heads*head_dim + 2*kv_heads*head_dim
+     * rows, Q then K then V), every layer must, and it replaces attn_q/k/v
+     * (IE:321-332). */
     const char* key_prefix;  /* may be NULL */
 } llmdot_hip_model_desc;
 

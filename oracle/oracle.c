@@ -1112,6 +1112,8 @@ struct orc_model {
     int kv_fp16;
     /* per layer */
     const gg_tensor **attn_norm, **ffn_norm, **wq, **wk, **wv, **wo, **wg, **wu, **wd;
+    const gg_tensor** wqkv;     /* fused Q/K/V (QkvLayout.Fused), else NULL */
+    int ffn_buf_len;            /* InferenceBuffers' FfnBuf length */
     float **attn_norm_f, **ffn_norm_f;
     const gg_tensor *embd, *out, *out_norm;
     float* out_norm_f;
@@ -1192,7 +1194,7 @@ void orc_model_close(orc_model* m) {
     if (!m) return;
     if (m->mapped) munmap((void*)m->buf, m->len);
     free(m->kv); free(m->t);
-    free(m->attn_norm); free(m->ffn_norm); free(m->wq); free(m->wk); free(m->wv); free(m->wo);
+    free(m->attn_norm); free(m->ffn_norm); free(m->wq); free(m->wk); free(m->wv); free(m->wo); free(m->wqkv);
     free(m->wg); free(m->wu); free(m->wd);
     if (m->attn_norm_f) for (int l = 0; l < m->cfg.layers; l++) free(m->attn_norm_f[l]);
     if (m->ffn_norm_f) for (int l = 0; l < m->cfg.layers; l++) free(m->ffn_norm_f[l]);
@@ -1355,11 +1357,23 @@ orc_model* orc_model_open_buffer(const uint8_t* buf, size_t len, int kv_fp16, ch
         if (!dst) { char e[200]; snprintf(e, sizeof e, "Tensor '%s' not found.", name); \
                     seterr(err, errlen, e); orc_model_close(m); return NULL; }   \
     } while (0)
+    /* QkvLayout: Fused when any tensor name contains "attn_qkv"
+       (ArchitectureResolver.cs:145-146); then every layer needs its
+       blk.N.attn_qkv.weight (TensorNameResolver.cs:123-126). */
+    int fused = 0;
+    for (uint64_t i = 0; i < m->nt && !fused; i++)
+        for (uint64_t j = 0; j + 8 <= m->t[i].namelen && !fused; j++)
+            if (memcmp(m->t[i].name + j, "attn_qkv", 8) == 0) fused = 1;
+    if (fused) m->wqkv = calloc((size_t)L, sizeof(void*));
     for (int l = 0; l < L; l++) {
         NEED(m->attn_norm[l], "blk.%d.attn_norm.weight");
-        NEED(m->wq[l], "blk.%d.attn_q.weight");
-        NEED(m->wk[l], "blk.%d.attn_k.weight");
-        NEED(m->wv[l], "blk.%d.attn_v.weight");
+        if (fused) {
+            NEED(m->wqkv[l], "blk.%d.attn_qkv.weight");
+        } else {
+            NEED(m->wq[l], "blk.%d.attn_q.weight");
+            NEED(m->wk[l], "blk.%d.attn_k.weight");
+            NEED(m->wv[l], "blk.%d.attn_v.weight");
+        }
         NEED(m->wo[l], "blk.%d.attn_output.weight");
         NEED(m->wg[l], "blk.%d.ffn_gate.weight");
         NEED(m->wu[l], "blk.%d.ffn_up.weight");
@@ -1398,6 +1412,7 @@ orc_model* orc_model_open_buffer(const uint8_t* buf, size_t len, int kv_fp16, ch
     m->attn_out = calloc((size_t)cf->hidden, 4);
     int maxInter = 2 * cf->ffn > 3 * cf->hidden ? 2 * cf->ffn : 3 * cf->hidden;
     m->ffn_buf = calloc((size_t)maxInter, 4);
+    m->ffn_buf_len = maxInter;
     m->ffn_result = calloc((size_t)cf->hidden, 4);
     m->logits = calloc((size_t)(cf->vocab > 0 ? cf->vocab : 1), 4);
     if (!alloc_buffers(m)) { seterr(err, errlen, "out of memory for KV cache"); orc_model_close(m); return NULL; }
@@ -1490,16 +1505,29 @@ static void attend_head(const orc_model* m, int layer, int position, int h, cons
     free(score);
 }
 
-/* AttentionForward, IE:304-450 (separate Q/K/V, no q/k norm, no softcap). */
+/* AttentionForward, IE:304-450 (separate or fused Q/K/V, no q/k norm, no softcap). */
 static int attention(orc_model* m, int layer, int position) {
     orc_config* c = &m->cfg;
     int hd = c->head_dim, H = c->heads, Hkv = c->kv_heads;
     int qdim = H * hd, kvdim = Hkv * hd, hidden = c->hidden;
     const float* input = m->norm;
     int rc = 0;
-    rc |= matmul_tensor(m, input, m->wq[layer], m->q, (int)(m->wq[layer]->nelem / (uint32_t)hidden));
-    rc |= matmul_tensor(m, input, m->wk[layer], m->k, (int)(m->wk[layer]->nelem / (uint32_t)hidden));
-    rc |= matmul_tensor(m, input, m->wv[layer], m->v, (int)(m->wv[layer]->nelem / (uint32_t)hidden));
+    if (m->wqkv) {
+        /* fused: one MatMul into FfnBuf (or a fresh array when it is too
+           short), then q, k, v copied out of it (IE:321-332) */
+        const int fusedCols = qdim + 2 * kvdim;
+        float* fb = fusedCols <= m->ffn_buf_len ? m->ffn_buf : (float*)malloc(sizeof(float) * (size_t)fusedCols);
+        if (!fb) return -4;
+        rc |= matmul_tensor(m, input, m->wqkv[layer], fb, fusedCols);
+        memcpy(m->q, fb, sizeof(float) * (size_t)qdim);
+        memcpy(m->k, fb + qdim, sizeof(float) * (size_t)kvdim);
+        memcpy(m->v, fb + qdim + kvdim, sizeof(float) * (size_t)kvdim);
+        if (fb != m->ffn_buf) free(fb);
+    } else {
+        rc |= matmul_tensor(m, input, m->wq[layer], m->q, (int)(m->wq[layer]->nelem / (uint32_t)hidden));
+        rc |= matmul_tensor(m, input, m->wk[layer], m->k, (int)(m->wk[layer]->nelem / (uint32_t)hidden));
+        rc |= matmul_tensor(m, input, m->wv[layer], m->v, (int)(m->wv[layer]->nelem / (uint32_t)hidden));
+    }
     if (rc) return rc;
     int half = (c->rope_dim > 0 ? c->rope_dim : hd) / 2;
     for (int h = 0; h < H; h++) {
@@ -1855,9 +1883,22 @@ int orc_prefill(orc_model* m, const int* tokens, int n, int pos0, float* logits)
                            (int)m->embd->dims[0]);
         for (int l = 0; l < c->layers && !rc; l++) {
             for (int t = 0; t < T; t++) orc_rms_norm(X + (size_t)t * d, m->attn_norm_f[l], Nn + (size_t)t * d, d, c->eps);
-            rc |= pf_matmul(Nn, T, m->wq[l], Q, qdim);
-            rc |= pf_matmul(Nn, T, m->wk[l], Kb, kvdim);
-            rc |= pf_matmul(Nn, T, m->wv[l], Vb, kvdim);
+            if (m->wqkv) {   /* fused (IE:321-332): one product, then each token's q, k, v copied out */
+                const int fc = qdim + 2 * kvdim;
+                float* F3 = (float*)malloc(sizeof(float) * (size_t)T * fc);
+                if (!F3) { rc = -4; break; }
+                rc |= pf_matmul(Nn, T, m->wqkv[l], F3, fc);
+                for (int t = 0; t < T && !rc; t++) {
+                    memcpy(Q + (size_t)t * qdim, F3 + (size_t)t * fc, sizeof(float) * (size_t)qdim);
+                    memcpy(Kb + (size_t)t * kvdim, F3 + (size_t)t * fc + qdim, sizeof(float) * (size_t)kvdim);
+                    memcpy(Vb + (size_t)t * kvdim, F3 + (size_t)t * fc + qdim + kvdim, sizeof(float) * (size_t)kvdim);
+                }
+                free(F3);
+            } else {
+                rc |= pf_matmul(Nn, T, m->wq[l], Q, qdim);
+                rc |= pf_matmul(Nn, T, m->wk[l], Kb, kvdim);
+                rc |= pf_matmul(Nn, T, m->wv[l], Vb, kvdim);
+            }
             if (rc) break;
             for (int t = 0; t < T; t++) {   /* RoPE and the KV write of each token (IE:362-381) */
                 const int pos = pos0 + c0 + t;

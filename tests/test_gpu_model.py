@@ -95,7 +95,7 @@ def test_generate_past_context_raises(hip, tiny_image):
 NEAR_TIE = 1e-2   # reference top-2 logit gap below which argmax may legitimately differ
 
 
-def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE):
+def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE, fused_qkv=False):
     """GPU decode with fp32 KV against the pure reference and with fp16 KV
     against the reference with K/V rounded through fp16 on store.
 
@@ -110,7 +110,7 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE):
     reference's up to its first top-2 gap below max(near_tie_min, 2 FLOOR_MARGIN floor(s));
     (2) teacher-forced on the reference's tokens, every step within the bound,
     the same argmax wherever the gap is at least that threshold."""
-    img = synth.build_image(name, seed=1234, context=ctx)
+    img = synth.build_image(name, seed=1234, context=ctx, fused_qkv=fused_qkv)
     spec = synth.SPECS[name]
     prompt = synth.prompt(spec["vocab"], n_prompt, seed=7)
     for kv_fp16 in (False, True):
@@ -170,6 +170,35 @@ def test_mistral7b_steps(hip, oracle_threads):
 def test_phi3mini_steps(hip, oracle_threads):
     """Phi-3-mini shape, MHA head_dim 96, Q6_K/Q8_0 mix: 4-token prompt, 8 tokens."""
     _big_model_check(hip, "phi3mini", 4, 8, 16)
+
+
+def test_phi3mini_fused_qkv_steps(hip, oracle_threads):
+    """The Phi-3 GGUF layout: one blk.N.attn_qkv.weight (Q8_0, Q then K then
+    V rows) per layer in place of attn_q/k/v (QkvLayout.Fused, IE:321-332),
+    against the oracle's fused path; 4-token prompt (batched), 8 tokens."""
+    _big_model_check(hip, "phi3mini", 4, 8, 16, fused_qkv=True)
+
+
+def test_fused_qkv_equals_separate(hip):
+    """Fused Q/K/V is a layout, not arithmetic: a tiny model (every matrix
+    Q8_0) with its Q, K, V rows in one attn_qkv tensor decodes bit-identically
+    to the same weights as three tensors, through the batched prompt path and
+    the decode step; and both stay on the oracle's tokens."""
+    sep = synth.build_image("tiny", seed=21)
+    fus = synth.build_image("tiny", seed=21, fused_qkv=True)
+    assert LoadedModel.load(fus).config.qkv_fused and not LoadedModel.load(sep).config.qkv_fused
+    prompt = synth.prompt(32000, 24, seed=3)
+    out = []
+    for img in (sep, fus):
+        eng = _engine(hip, img, True)
+        toks, logits = eng.generate_all(prompt, greedy(32), return_logits=True)
+        eng.dispose()
+        out.append((toks, logits))
+    assert out[0][0] == out[1][0]
+    assert np.array_equal(out[0][1], out[1][1])
+    ref = O.Model(fus, kv_fp16=True)
+    rt, _ = ref.generate(prompt, 32, return_logits=False)
+    assert out[1][0] == rt
 
 
 @pytest.mark.parametrize("kv_fp16", [False, True])

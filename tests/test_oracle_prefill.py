@@ -199,3 +199,51 @@ def test_long_fixture_consistent(key):
         r64 = row.astype(np.float64)
         assert r64.mean() == z["mean"][s] and np.sqrt(np.mean(r64 * r64)) == z["rms"][s]
     assert np.all(np.isfinite(z["k"])) and np.all(np.isfinite(z["v"]))
+
+
+@pytest.mark.parametrize("order", [0, 2])
+def test_fused_qkv_is_the_separate_product(order):
+    """QkvLayout.Fused (IE:321-332): one MatMul over blk.N.attn_qkv.weight, its
+    output split into q, k, v.  Every output row of MatMul is its own dot
+    product (TO:60-90), so on the same weights the fused model is the separate
+    one bit for bit, in the step, in the batched prompt path and in a
+    reordered summation; tiny's matrices are all Q8_0, so the fused image holds
+    exactly the separate image's Q, K, V bytes."""
+    sep = synth.build_image("tiny", seed=11)
+    fus = synth.build_image("tiny", seed=11, fused_qkv=True)
+    ms, mf = O.Model(sep), O.Model(fus)
+    try:
+        O.set_order(order)
+        p = synth.prompt(ms.config.vocab, 9, seed=4)
+        a, b = ms.prefill(p, 0), mf.prefill(p, 0)
+        assert np.array_equal(a, b)
+        t = int(np.argmax(a))
+        for s in range(5):
+            a, b = ms.process_token(t, len(p) + s), mf.process_token(t, len(p) + s)
+            assert np.array_equal(a, b), s
+            t = int(np.argmax(a))
+        for layer in (0, 3):
+            for pos in (0, len(p) + 2):
+                ka, va = ms.kv_read(layer, pos)
+                kb, vb = mf.kv_read(layer, pos)
+                assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    finally:
+        O.set_order(0)
+        ms.close()
+        mf.close()
+
+
+def test_fused_qkv_rows_are_the_three_tensors():
+    """The synthetic fused tensor is attn_q, attn_k, attn_v's bytes in that
+    order (what the device's row-range views and the equality above assume),
+    and the GGUF config reports the fused layout (ArchitectureResolver.cs:145-146)."""
+    from dotllm_amd.engine import LoadedModel
+    sep = LoadedModel.load(synth.build_image("tiny", seed=11))
+    fus = LoadedModel.load(synth.build_image("tiny", seed=11, fused_qkv=True))
+    assert fus.config.qkv_fused and not sep.config.qkv_fused
+    for layer in (0, 1):
+        f = fus.tensor(f"blk.{layer}.attn_qkv.weight")
+        parts = [sep.tensor(f"blk.{layer}.attn_{x}.weight") for x in "qkv"]
+        assert f.rows == sum(t.rows for t in parts) and f.cols == parts[0].cols
+        assert np.array_equal(np.asarray(f.data).reshape(-1),
+                              np.concatenate([np.asarray(t.data).reshape(-1) for t in parts]))
