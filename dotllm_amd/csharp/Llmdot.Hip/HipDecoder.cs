@@ -34,7 +34,8 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
 {
     private static int s_next;
     private static readonly string[] LayerTensors =
-        ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_qkv", "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"];
+        ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_qkv", "attn_q_norm", "attn_k_norm", "attn_output", "ffn_norm",
+         "ffn_gate", "ffn_up", "ffn_down"];
 
     private readonly LoadedModel _model;
     private readonly HipBackend _backend;
@@ -49,10 +50,11 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
 
     /// <summary>
     /// Whether the device step covers this model: the LLaMA-like template with
-    /// RMSNorm, separate or fused Q/K/V, SwiGLU, no sliding window, softcaps, post-norms,
-    /// Q/K norms, experts or convolution layers, one KV head count for every
-    /// layer, and an embedding scale of 1 (the paths of IE:134-196 and
-    /// IE:304-476 that the LLaMA, Mistral, Phi-3 and Qwen2 GGUFs take).
+    /// RMSNorm, separate or fused Q/K/V, optional per-head Q/K norms, SwiGLU; no
+    /// sliding window, softcaps, post-norms, experts or convolution layers, one
+    /// KV head count for every layer, and an embedding scale of 1 (the paths of
+    /// IE:134-196 and IE:304-476 that the LLaMA, Mistral, Phi-3, Qwen2 and Qwen3
+    /// GGUFs take).
     /// </summary>
     public static bool Supports(LoadedModel model, out string? reason)
     {
@@ -67,7 +69,6 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
             : c.AttnLogitSoftcap.HasValue || c.FinalLogitSoftcap.HasValue ? "logit softcaps"
             : c.EmbeddingScale != 1f ? "embedding scale"
             : c.HeadCountKvPerLayer.Any(h => h != c.HeadCountKv) ? "per-layer KV head counts"
-            : model.TensorNames.TryGet("blk.0.attn_q_norm.weight") is not null ? "Q/K norms"
             : null;
         return reason is null;
     }
@@ -107,7 +108,9 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
             foreach (var t in LayerTensors)
             {
                 if (fused ? t is "attn_q" or "attn_k" or "attn_v" : t == "attn_qkv") continue;
-                if (t == "ffn_norm" && !_model.TryGetTensor($"blk.{l}.ffn_norm.weight", out _)) continue;
+                // optional per layer: ffn_norm (attn_norm stands in, IE:547), the Q/K norms (IE:354-373)
+                if (t is "ffn_norm" or "attn_q_norm" or "attn_k_norm" && !_model.TryGetTensor($"blk.{l}.{t}.weight", out _))
+                    continue;
                 names.Add($"blk.{l}.{t}.weight");
             }
         foreach (var name in names)

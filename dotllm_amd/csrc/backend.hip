@@ -818,6 +818,7 @@ namespace {
 struct LayerW {
     const Weight *attn_norm, *ffn_norm, *q, *k, *v, *o, *gate, *up, *down;
     float *attn_norm_f, *ffn_norm_f;   // fp32 norm weights on the device
+    float *q_norm_f = nullptr, *k_norm_f = nullptr;   // per-head Q/K norms [head_dim] (absent: null)
 };
 
 }  // namespace
@@ -1007,6 +1008,8 @@ int enqueue_step(llmdot_hip_model* m) {
                 }
             HIPCHK(step_gemv(m, lt, EPI_STORE, ga));
         }
+        if (w.q_norm_f || w.k_norm_f)   // per-head Q/K RmsNorm before RoPE (IE:354-359, IE:367-372)
+            HIPCHK(launch_qk_norm(m->q, m->k, w.q_norm_f, w.k_norm_f, d.heads, d.kv_heads, d.head_dim, d.eps, s));
         AttnArgs aa{};
         aa.q = m->q; aa.k = m->k; aa.v = m->v;
         aa.kcache = m->kcache + (size_t)l * m->kv_layer_bytes;
@@ -1076,6 +1079,9 @@ bool prefill_check(const llmdot_hip_model* m) {
     const auto& d = m->d;
     const int qdim = d.heads * d.head_dim;
     for (const auto& w : m->L) {
+        // the batched path has no per-head Q/K norm stage: such a model's
+        // prompt runs through the decode step token by token
+        if (w.q_norm_f || w.k_norm_f) return false;
         const Weight* in_h[5] = {w.q, w.k, w.v, w.gate, w.up};
         for (auto* x : in_h)
             if (!prefill_gemm_supported(x->type, d.hidden)) return false;
@@ -1354,6 +1360,11 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
         if (w.gate->type != w.up->type) return bail(fail(LLMDOT_E_UNSUPPORTED, "ffn_gate and ffn_up must share a type"));
         if ((rc = norm_f32(m, w.attn_norm, d.hidden, &w.attn_norm_f))) return bail(rc);
         if ((rc = norm_f32(m, w.ffn_norm, d.hidden, &w.ffn_norm_f))) return bail(rc);
+        // optional per-head Q/K norms (attn_q_norm / attn_k_norm, head_dim each)
+        if (const Weight* qn = find_w(m, p + "attn_q_norm.weight"))
+            if ((rc = norm_f32(m, qn, d.head_dim, &w.q_norm_f))) return bail(rc);
+        if (const Weight* kn = find_w(m, p + "attn_k_norm.weight"))
+            if ((rc = norm_f32(m, kn, d.head_dim, &w.k_norm_f))) return bail(rc);
     }
     // RoPE tables: PrecomputeRopeFrequencies (IE:57-72) then, per position, the
     // reference's per-call cosf/sinf of position * freq (TO:688-693).

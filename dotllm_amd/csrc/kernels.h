@@ -76,6 +76,10 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s);
 
 // ---- ops.hip (op-level IComputeBackend members) ----
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, int n, float eps, hipStream_t s);
+// Per-head RmsNorm in place: q [heads][hd] with wq, k [kv_heads][hd] with wk
+// (either weight may be null: that side is left as it is).
+hipError_t launch_qk_norm(float* q, float* k, const float* wq, const float* wk, int heads, int kv_heads, int hd,
+                          float eps, hipStream_t s);
 hipError_t launch_rope(float* q, float* k, const float* cosv, const float* sinv, int half, int same,
                        hipStream_t s);
 hipError_t launch_softmax(float* x, int n, int has_softcap, float cap, hipStream_t s);

@@ -52,6 +52,25 @@ __global__ __launch_bounds__(WG_BIG) void rmsnorm_kernel(const float* in, const 
         out[i] = i < n8 ? ((w[i] * in[i]) * inv) : (w[i] * (in[i] * inv));
 }
 
+// Per-head Q/K norms (IE:354-359, IE:367-372): VectorMath.RmsNorm in place
+// over each head_dim slice of q (workgroups 0 .. heads - 1, weight wq) and of
+// k (the rest, weight wk); a null weight skips that side.  One wavefront per
+// head: the sum of squares over the wavefront, then the reference's vector
+// lanes (w x) inv and tail w (x inv).
+__global__ __launch_bounds__(64) void qk_norm_kernel(float* q, float* k, const float* wq, const float* wk, int heads,
+                                                     int hd, float eps) {
+    const bool isq = (int)blockIdx.x < heads;
+    const float* w = isq ? wq : wk;
+    if (!w) return;
+    float* x = isq ? q + (int64_t)blockIdx.x * hd : k + (int64_t)(blockIdx.x - heads) * hd;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < hd; i += 64) ss += x[i] * x[i];
+    ss = wave_sum(ss);
+    const float inv = (1.0f / (sqrtf(((ss / (float)hd) + eps))));
+    const int n8 = hd & ~7;
+    for (int i = threadIdx.x; i < hd; i += 64) x[i] = i < n8 ? ((w[i] * x[i]) * inv) : (w[i] * (x[i] * inv));
+}
+
 // TensorOps.ApplyRoPECore, TO:699-743 (cos/sin supplied by the host).
 __global__ void rope_kernel(float* q, float* k, const float* cosv, const float* sinv, int half, int same) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -301,6 +320,13 @@ int grid_for(int n, int nt) {
 }
 
 }  // namespace
+
+hipError_t launch_qk_norm(float* q, float* k, const float* wq, const float* wk, int heads, int kv_heads, int hd,
+                          float eps, hipStream_t s) {
+    if (heads <= 0 || kv_heads < 0 || hd <= 0) return hipErrorInvalidValue;
+    qk_norm_kernel<<<heads + kv_heads, 64, 0, s>>>(q, k, wq, wk, heads, hd, eps);
+    return hipGetLastError();
+}
 
 hipError_t launch_rmsnorm(const float* in, const float* w, float* out, int n, float eps, hipStream_t s) {
     rmsnorm_kernel<<<1, WG_BIG, 0, s>>>(in, w, out, n, eps);

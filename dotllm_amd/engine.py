@@ -47,8 +47,8 @@ def greedy(max_tokens: int) -> GenerationOptions:
 
 
 # Tensor names of the LLaMA-like template (src/Llmdot.Core/Loading/TensorNameResolver.cs:22-107).
-LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_qkv", "attn_output", "ffn_norm", "ffn_gate", "ffn_up",
-                 "ffn_down")
+LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_qkv", "attn_q_norm", "attn_k_norm", "attn_output",
+                 "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")
 
 
 class LoadedModel:
@@ -101,8 +101,6 @@ class InferenceEngine:
             raise NotImplementedError("only SwiGLU FFN tensors are supported")
         if cfg.sliding_window:
             raise NotImplementedError("sliding-window attention is not supported")
-        if cfg.qk_norm:
-            raise NotImplementedError("Q/K norms are not supported")
         if any(h != cfg.head_count_kv for h in cfg.kv_heads_per_layer):
             raise NotImplementedError("per-layer KV head counts are not supported")
         self.model = model

@@ -61,11 +61,12 @@ def tensor_type(mix: str, name: str) -> int:
     raise ValueError(f"unknown mix {mix}")
 
 
-def tensor_list(spec: dict, fused_qkv: bool = False) -> list:
+def tensor_list(spec: dict, fused_qkv: bool = False, qk_norm: bool = False) -> list:
     """(name, rows, cols, ggml_type) in file order.  fused_qkv: one
     blk.N.attn_qkv.weight of q + 2 kv rows (Q, then K, then V, in attn_q's
     type) in place of the three attention projections, the layout of Phi-3
-    GGUFs (QkvLayout.Fused)."""
+    GGUFs (QkvLayout.Fused).  qk_norm: per-head RmsNorm weights
+    blk.N.attn_q_norm.weight and blk.N.attn_k_norm.weight (head_dim each)."""
     d, f, v = spec["hidden"], spec["ffn"], spec["vocab"]
     q, kv = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
     out = [("token_embd.weight", v, d)]
@@ -73,7 +74,9 @@ def tensor_list(spec: dict, fused_qkv: bool = False) -> list:
         p = f"blk.{l}."
         qkv = ([(p + "attn_qkv.weight", q + 2 * kv, d)] if fused_qkv else
                [(p + "attn_q.weight", q, d), (p + "attn_k.weight", kv, d), (p + "attn_v.weight", kv, d)])
-        out += [(p + "attn_norm.weight", 1, d)] + qkv + [
+        qkn = [(p + "attn_q_norm.weight", 1, spec["head_dim"]), (p + "attn_k_norm.weight", 1, spec["head_dim"])] \
+            if qk_norm else []
+        out += [(p + "attn_norm.weight", 1, d)] + qkv + qkn + [
             (p + "attn_output.weight", d, q), (p + "ffn_norm.weight", 1, d),
             (p + "ffn_gate.weight", f, d), (p + "ffn_up.weight", f, d), (p + "ffn_down.weight", d, f)]
     out += [("output_norm.weight", 1, d), ("output.weight", v, d)]
@@ -130,7 +133,8 @@ def tensor_sigma(name: str, spec: dict, sigma: float, scaled_init: bool) -> floa
 
 def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
                 threads: int | None = None, spec: dict | None = None, scaled_init: bool = False,
-                eos: int = -1, tied: bool = False, norm_type: int = F32, fused_qkv: bool = False) -> np.ndarray:
+                eos: int = -1, tied: bool = False, norm_type: int = F32, fused_qkv: bool = False,
+                qk_norm: bool = False) -> np.ndarray:
     """Builds the whole GGUF file image in memory (uint8 numpy array).
 
     eos: tokenizer.ggml.eos_token_id (-1: never stops); tied: no output.weight,
@@ -138,9 +142,11 @@ def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int |
     norm_type: F32 or F16 RMSNorm weights (ones either way); fused_qkv: Q, K
     and V rows in one attn_qkv tensor, each range filled exactly as the
     separate tensor of the same type would be (same seed), so a fused image
-    holds the same weights as the separate one wherever the types agree."""
+    holds the same weights as the separate one wherever the types agree;
+    qk_norm: per-head Q/K RmsNorm weights (1 + 0.3 N(0, 1), seeded), so that a
+    path that skipped or misplaced them would show."""
     spec = spec or SPECS[name]
-    tl = [(n, r, c, (norm_type if n.endswith("_norm.weight") else t)) for n, r, c, t in tensor_list(spec, fused_qkv)
+    tl = [(n, r, c, (norm_type if n.endswith("_norm.weight") else t)) for n, r, c, t in tensor_list(spec, fused_qkv, qk_norm)
           if not (tied and n == "output.weight")]
     qd, kvd = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
     infos = [(n, (c,) if r == 1 else (c, r), t, byte_count(t, r * c)) for n, r, c, t in tl]
@@ -151,7 +157,15 @@ def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int |
     for (n, r, c, t), off, info in zip(tl, offsets, infos):
         nb = info[3]
         view = img[base + off: base + off + nb]
-        if n.endswith("_norm.weight"):
+        if n.endswith(("attn_q_norm.weight", "attn_k_norm.weight")):
+            w = 1.0 + 0.3 * np.random.default_rng(tensor_seed(seed, n)).standard_normal(c)
+            if t == F32:
+                view.view(np.float32)[:] = w.astype(np.float32)
+            elif t == _lib.F16:
+                view.view(np.float16)[:] = w.astype(np.float16)
+            else:
+                raise ValueError("norm weights are F32 or F16")
+        elif n.endswith("_norm.weight"):
             if t == F32:
                 view.view(np.float32)[:] = 1.0
             elif t == _lib.F16:

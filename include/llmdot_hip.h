@@ -211,7 +211,9 @@ typedef struct llmdot_hip_model_desc {
      * Fused Q/K/V (QkvLayout.Fused, ArchitectureResolver.cs:145-146): when any
      * layer has blk.N.attn_qkv.weight (heads*head_dim + 2*kv_heads*head_dim
      * rows, Q then K then V), every layer must, and it replaces attn_q/k/v
-     * (IE:321-332). */
+     * (IE:321-332).  Optional per layer: blk.N.attn_q_norm.weight and
+     * blk.N.attn_k_norm.weight (head_dim each), per-head RmsNorm of q and k
+     * before RoPE (IE:354-373). */
     const char* key_prefix;  /* may be NULL */
 } llmdot_hip_model_desc;
 

@@ -1113,6 +1113,7 @@ struct orc_model {
     /* per layer */
     const gg_tensor **attn_norm, **ffn_norm, **wq, **wk, **wv, **wo, **wg, **wu, **wd;
     const gg_tensor** wqkv;     /* fused Q/K/V (QkvLayout.Fused), else NULL */
+    float **q_norm_f, **k_norm_f;   /* per-head Q/K RmsNorm weights [head_dim] (NULL entries: none) */
     int ffn_buf_len;            /* InferenceBuffers' FfnBuf length */
     float **attn_norm_f, **ffn_norm_f;
     const gg_tensor *embd, *out, *out_norm;
@@ -1198,6 +1199,9 @@ void orc_model_close(orc_model* m) {
     free(m->wg); free(m->wu); free(m->wd);
     if (m->attn_norm_f) for (int l = 0; l < m->cfg.layers; l++) free(m->attn_norm_f[l]);
     if (m->ffn_norm_f) for (int l = 0; l < m->cfg.layers; l++) free(m->ffn_norm_f[l]);
+    if (m->q_norm_f) for (int l = 0; l < m->cfg.layers; l++) free(m->q_norm_f[l]);
+    if (m->k_norm_f) for (int l = 0; l < m->cfg.layers; l++) free(m->k_norm_f[l]);
+    free(m->q_norm_f); free(m->k_norm_f);
     free(m->attn_norm_f); free(m->ffn_norm_f); free(m->out_norm_f); free(m->rope_freqs);
     free(m->kcache); free(m->vcache);
     free(m->hidden); free(m->norm); free(m->normtmp); free(m->q); free(m->k); free(m->v);
@@ -1383,6 +1387,16 @@ orc_model* orc_model_open_buffer(const uint8_t* buf, size_t len, int kv_fp16, ch
         if (!m->ffn_norm[l]) m->ffn_norm[l] = m->attn_norm[l];   /* IE:547 */
         m->attn_norm_f[l] = dequant_whole(m->attn_norm[l]);
         m->ffn_norm_f[l] = dequant_whole(m->ffn_norm[l]);
+        /* optional per-head Q/K norms (TensorNameResolver: attn_q_norm / attn_k_norm) */
+        const gg_tensor* qn; const gg_tensor* kn;
+        snprintf(name, sizeof name, "blk.%d.attn_q_norm.weight", l); qn = find_tensor(m, name);
+        snprintf(name, sizeof name, "blk.%d.attn_k_norm.weight", l); kn = find_tensor(m, name);
+        if ((qn || kn) && !m->q_norm_f) {
+            m->q_norm_f = calloc((size_t)L, sizeof(float*));
+            m->k_norm_f = calloc((size_t)L, sizeof(float*));
+        }
+        if (qn) m->q_norm_f[l] = dequant_whole(qn);
+        if (kn) m->k_norm_f[l] = dequant_whole(kn);
     }
 #undef NEED
     m->embd = find_tensor(m, "token_embd.weight");
@@ -1505,7 +1519,7 @@ static void attend_head(const orc_model* m, int layer, int position, int h, cons
     free(score);
 }
 
-/* AttentionForward, IE:304-450 (separate or fused Q/K/V, no q/k norm, no softcap). */
+/* AttentionForward, IE:304-450 (separate or fused Q/K/V, optional per-head Q/K norms, no softcap). */
 static int attention(orc_model* m, int layer, int position) {
     orc_config* c = &m->cfg;
     int hd = c->head_dim, H = c->heads, Hkv = c->kv_heads;
@@ -1529,6 +1543,11 @@ static int attention(orc_model* m, int layer, int position) {
         rc |= matmul_tensor(m, input, m->wv[layer], m->v, (int)(m->wv[layer]->nelem / (uint32_t)hidden));
     }
     if (rc) return rc;
+    /* per-head RmsNorm of q and of k before their RoPE (IE:354-359, IE:367-372) */
+    if (m->q_norm_f && m->q_norm_f[layer])
+        for (int h = 0; h < H; h++) orc_rms_norm(m->q + h * hd, m->q_norm_f[layer], m->q + h * hd, hd, c->eps);
+    if (m->k_norm_f && m->k_norm_f[layer])
+        for (int h = 0; h < Hkv; h++) orc_rms_norm(m->k + h * hd, m->k_norm_f[layer], m->k + h * hd, hd, c->eps);
     int half = (c->rope_dim > 0 ? c->rope_dim : hd) / 2;
     for (int h = 0; h < H; h++) {
         float* qh = m->q + h * hd;
@@ -1900,11 +1919,15 @@ int orc_prefill(orc_model* m, const int* tokens, int n, int pos0, float* logits)
                 rc |= pf_matmul(Nn, T, m->wv[l], Vb, kvdim);
             }
             if (rc) break;
-            for (int t = 0; t < T; t++) {   /* RoPE and the KV write of each token (IE:362-381) */
+            for (int t = 0; t < T; t++) {   /* Q/K norms, RoPE and the KV write of each token (IE:354-381) */
                 const int pos = pos0 + c0 + t;
                 float* qt = Q + (size_t)t * qdim;
                 float* kt = Kb + (size_t)t * kvdim;
                 const float* vt = Vb + (size_t)t * kvdim;
+                if (m->q_norm_f && m->q_norm_f[l])
+                    for (int h = 0; h < H; h++) orc_rms_norm(qt + h * hd, m->q_norm_f[l], qt + h * hd, hd, c->eps);
+                if (m->k_norm_f && m->k_norm_f[l])
+                    for (int h = 0; h < Hkv; h++) orc_rms_norm(kt + h * hd, m->k_norm_f[l], kt + h * hd, hd, c->eps);
                 for (int h = 0; h < H; h++) orc_rope_table(qt + h * hd, qt + h * hd, hd, pos, m->rope_freqs, half, 1);
                 size_t slot = ((size_t)l * (size_t)m->cache_ctx + (size_t)pos) * (size_t)kvdim;
                 for (int h = 0; h < Hkv; h++) {

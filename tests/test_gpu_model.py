@@ -95,7 +95,7 @@ def test_generate_past_context_raises(hip, tiny_image):
 NEAR_TIE = 1e-2   # reference top-2 logit gap below which argmax may legitimately differ
 
 
-def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE, fused_qkv=False):
+def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE, **build):
     """GPU decode with fp32 KV against the pure reference and with fp16 KV
     against the reference with K/V rounded through fp16 on store.
 
@@ -110,7 +110,7 @@ def _big_model_check(hip, name, n_prompt, n_gen, ctx, near_tie_min=NEAR_TIE, fus
     reference's up to its first top-2 gap below max(near_tie_min, 2 FLOOR_MARGIN floor(s));
     (2) teacher-forced on the reference's tokens, every step within the bound,
     the same argmax wherever the gap is at least that threshold."""
-    img = synth.build_image(name, seed=1234, context=ctx, fused_qkv=fused_qkv)
+    img = synth.build_image(name, seed=1234, context=ctx, **build)
     spec = synth.SPECS[name]
     prompt = synth.prompt(spec["vocab"], n_prompt, seed=7)
     for kv_fp16 in (False, True):
@@ -177,6 +177,31 @@ def test_phi3mini_fused_qkv_steps(hip, oracle_threads):
     V rows) per layer in place of attn_q/k/v (QkvLayout.Fused, IE:321-332),
     against the oracle's fused path; 4-token prompt (batched), 8 tokens."""
     _big_model_check(hip, "phi3mini", 4, 8, 16, fused_qkv=True)
+
+
+def test_small5_qk_norm_fused_greedy(hip, oracle_threads):
+    """Per-head Q/K RmsNorm (attn_q_norm / attn_k_norm, IE:354-373, the Qwen3
+    layout) with fused Q/K/V, query groups of 2: 8-token prompt (token by
+    token: the batched prompt path has no Q/K norm stage), 32 greedy tokens."""
+    _big_model_check(hip, "small5", 8, 32, 48, near_tie_min=1e-4, fused_qkv=True, qk_norm=True)
+
+
+def test_tiny_qk_norm_teacher_forced(hip):
+    """Q/K norms on the tiny MHA model: every step within 2e-2 of the oracle
+    over a random token stream, and the norms matter (the same weights
+    without them move the logits by far more)."""
+    img = synth.build_image("tiny", seed=8, qk_norm=True)
+    plain = O.Model(synth.build_image("tiny", seed=8), kv_fp16=True)
+    ref = O.Model(img, kv_fp16=True)
+    eng = _engine(hip, img, True)
+    moved = 0.0
+    for pos, t in enumerate(synth.prompt(32000, 24, seed=12)):
+        rl = ref.process_token(t, pos)
+        gl = eng.process_token(t, pos)
+        moved = max(moved, float(np.max(np.abs(plain.process_token(t, pos) - rl))))
+        assert float(np.max(np.abs(gl - rl))) <= LOGIT_TOL, pos
+    eng.dispose()
+    assert moved > 10 * LOGIT_TOL
 
 
 def test_fused_qkv_equals_separate(hip):

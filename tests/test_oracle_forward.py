@@ -102,9 +102,18 @@ class Forward:
         for l in range(self.cfg.layer_count):
             p = f"blk.{l}."
             h = self.norm(x, W[p + "attn_norm.weight"])
-            q = self.rope((W[p + "attn_q.weight"] @ h).reshape(H, hd), pos)
-            k = self.rope((W[p + "attn_k.weight"] @ h).reshape(Hkv, hd), pos)
-            v = (W[p + "attn_v.weight"] @ h).reshape(Hkv, hd)
+            if p + "attn_qkv.weight" in W:   # fused (IE:321-332): one product, split Q | K | V
+                f = W[p + "attn_qkv.weight"] @ h
+                q, k, v = f[:H * hd], f[H * hd:(H + Hkv) * hd], f[(H + Hkv) * hd:]
+            else:
+                q, k, v = W[p + "attn_q.weight"] @ h, W[p + "attn_k.weight"] @ h, W[p + "attn_v.weight"] @ h
+            q, k, v = q.reshape(H, hd), k.reshape(Hkv, hd), v.reshape(Hkv, hd)
+            # per-head RmsNorm of q and k before RoPE (IE:354-373)
+            if p + "attn_q_norm.weight" in W:
+                q = np.stack([self.norm(r, W[p + "attn_q_norm.weight"]) for r in q])
+            if p + "attn_k_norm.weight" in W:
+                k = np.stack([self.norm(r, W[p + "attn_k_norm.weight"]) for r in k])
+            q, k = self.rope(q, pos), self.rope(k, pos)
             self.K[l, pos], self.V[l, pos] = k, v
             out = np.zeros((H, hd))
             for hh in range(H):
@@ -127,16 +136,19 @@ def test_exp_approx_restatement_matches_oracle():
     assert np.array_equal(mine.view(np.uint32), theirs.view(np.uint32))
 
 
-@pytest.mark.parametrize("name,spec", [("tiny", None), ("small5", None),
-                                       ("gqa4", dict(arch="llama", hidden=512, layers=2, heads=8, kv_heads=2,
-                                                     head_dim=64, ffn=1024, vocab=2000, rope_base=500000.0,
-                                                     context=64, mix="q4_k_m"))])
-def test_process_token_composition(name, spec):
+GQA4 = dict(arch="llama", hidden=512, layers=2, heads=8, kv_heads=2, head_dim=64, ffn=1024, vocab=2000,
+            rope_base=500000.0, context=64, mix="q4_k_m")
+
+
+@pytest.mark.parametrize("name,spec,opts", [("tiny", None, {}), ("small5", None, {}), ("gqa4", GQA4, {}),
+                                            ("gqa4", GQA4, dict(qk_norm=True)),
+                                            ("small5", None, dict(fused_qkv=True, qk_norm=True))])
+def test_process_token_composition(name, spec, opts):
     """16 teacher-forced steps of a random token stream: the oracle's logits
     within 1e-4 of the fp64 forward at every step (MHA head_dim 64 Q8_0;
     query groups of 2 with head_dim 128 and Q5_K/Q6_K; groups of 4 with
-    Q4_K/Q6_K and theta 500000)."""
-    img = synth.build_image(name if spec is None else "x", seed=31, spec=spec)
+    Q4_K/Q6_K and theta 500000; per-head Q/K norms, alone and with fused Q/K/V)."""
+    img = synth.build_image(name if spec is None else "x", seed=31, spec=spec, **opts)
     fw = Forward(img, 32)
     m = O.Model(img, kv_fp16=False, context=32)
     toks = synth.prompt(fw.cfg.vocab_size, 16, seed=5)
