@@ -361,8 +361,8 @@ __device__ __forceinline__ uint64_t l2_load64(__amdgpu_buffer_rsrc_t r, uint32_t
 // until every live chunk of the kv head has published; wavefronts 2-3 load
 // the V rows into LDS at the same time.  The wait counter is per wavefront,
 // so the exchange waits only for K.  Then all four form the exponentials
-// against the global maxima and the chunk partials for attn_combine_kernel
-// (as attn_pv_kernel).  The wait needs the kv head's workgroups to run
+// against the global maxima and the chunk partials (as attn_pv_kernel),
+// summed by attn_combine_kernel or, in the XCD-local form, inside this launch.  The wait needs the kv head's workgroups to run
 // together: workgroups are dispatched in index order and the whole grid (at
 // most 256 chunks per kv head, a few workgroups per CU) is resident at once,
 // so none of them waits on a workgroup that cannot start; a wait that still
