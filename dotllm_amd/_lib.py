@@ -53,7 +53,8 @@ class ModelDesc(C.Structure):
                 ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32),
                 ("vocab", C.c_int32), ("context", C.c_int32), ("rope_dim", C.c_int32),
                 ("eps", C.c_float), ("rope_base", C.c_float), ("rope_linear_factor", C.c_float),
-                ("kv_fp16", C.c_int32), ("bos", C.c_int32), ("key_prefix", C.c_char_p)]
+                ("kv_fp16", C.c_int32), ("bos", C.c_int32), ("sliding_window", C.c_int32),
+                ("key_prefix", C.c_char_p)]
 
 
 class DeviceInfo(C.Structure):

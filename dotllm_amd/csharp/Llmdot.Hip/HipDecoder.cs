@@ -50,11 +50,11 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
 
     /// <summary>
     /// Whether the device step covers this model: the LLaMA-like template with
-    /// RMSNorm, separate or fused Q/K/V, optional per-head Q/K norms, SwiGLU; no
-    /// sliding window, softcaps, post-norms, experts or convolution layers, one
-    /// KV head count for every layer, and an embedding scale of 1 (the paths of
-    /// IE:134-196 and IE:304-476 that the LLaMA, Mistral, Phi-3, Qwen2 and Qwen3
-    /// GGUFs take).
+    /// RMSNorm, separate or fused Q/K/V, optional per-head Q/K norms, an optional
+    /// sliding window, SwiGLU; no softcaps, post-norms, experts or convolution
+    /// layers, one KV head count for every layer, and an embedding scale of 1
+    /// (the paths of IE:134-196 and IE:304-476 that the LLaMA, Mistral, Phi-3,
+    /// Qwen2 and Qwen3 GGUFs take).
     /// </summary>
     public static bool Supports(LoadedModel model, out string? reason)
     {
@@ -62,7 +62,6 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
         reason = c.Template != ExecutionTemplate.LlamaLike ? $"template {c.Template}"
             : c.NormType != NormType.RmsNorm ? $"norm {c.NormType}"
             : c.FfnType != FfnType.SwiGLU ? $"FFN {c.FfnType}"
-            : c.SlidingWindow > 0 ? "sliding-window attention"
             : c.ExpertCount > 0 ? "mixture of experts"
             : c.HasConvLayers ? "convolution layers"
             : c.HasPostNorm ? "post-norms"
@@ -138,7 +137,7 @@ public sealed unsafe class HipDecoder : IDeviceDecoder
                 RopeDim = c.RopeDimensionCount, Eps = c.NormEpsilon, RopeBase = c.RopeFreqBase,
                 // PrecomputeRopeFrequencies (IE:57-72): only Linear scaling changes the table
                 RopeLinearFactor = c.RopeScalingType == RopeScalingType.Linear && c.RopeScalingFactor > 1f ? c.RopeScalingFactor : 1f,
-                KvFp16 = kvFp16 ? 1 : 0, Bos = c.BosTokenId, KeyPrefix = pp,
+                KvFp16 = kvFp16 ? 1 : 0, Bos = c.BosTokenId, SlidingWindow = c.SlidingWindow, KeyPrefix = pp,
             };
             nint m;
             HipNative.Check(HipNative.llmdot_hip_model_create(_backend.Handle, &d, &m));

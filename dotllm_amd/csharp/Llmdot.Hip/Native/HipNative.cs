@@ -59,6 +59,7 @@ internal static unsafe partial class HipNative
         public float RopeLinearFactor;
         public int KvFp16;
         public int Bos;
+        public int SlidingWindow; // attend to the last N positions (IE:385-387); 0 = all
         public byte* KeyPrefix;   // NUL-terminated UTF-8, may be null
     }
 

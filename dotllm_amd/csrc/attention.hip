@@ -296,13 +296,13 @@ __device__ __forceinline__ uint64_t slot_get(const uint64_t* p) {
 // One poll of the tagged chunk maxima of the G heads of kv head kvh: four
 // slots per lane and head.
 template <int G>
-__device__ __forceinline__ void poll_issue(uint64_t (&v)[G][4], const uint64_t* xmax, int kvh, int lane, int nch,
-                                           int mc) {
+__device__ __forceinline__ void poll_issue(uint64_t (&v)[G][4], const uint64_t* xmax, int kvh, int lane, int c0,
+                                           int nch, int mc) {
 #pragma unroll
     for (int j = 0; j < G; j++) {
         const uint64_t* slots = xmax + ((int64_t)kvh * G + j) * mc;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[j][i] = slot_get(slots + min(lane + 64 * i, nch - 1));
+        for (int i = 0; i < 4; i++) v[j][i] = slot_get(slots + min(c0 + lane + 64 * i, nch - 1));
     }
 }
 template <int HW>
@@ -434,9 +434,14 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
     // sunk there, behind the wait for the position)
     asm volatile("" ::: "memory");
     const int p0 = c * CH;
-    const int n = T + 1, n8 = n & ~7;
-    if (p0 >= n) return;
-    const int nch = (n + CH - 1) / CH;            // live chunks of every kv head
+    const int n = T + 1;
+    // SlidingWindow (IE:385-387): positions s0 .. T attend, chunks c0 .. nch-1
+    // hold them, and the Softmax's vector lanes are the window's first
+    // 8 floor(len / 8) positions (without a window: s0 = c0 = 0)
+    const int s0 = a.window > 0 ? max(0, n - a.window) : 0, c0 = s0 / CH;
+    const int n8 = s0 + ((n - s0) & ~7);
+    if (p0 >= n || c < c0) return;
+    const int nch = (n + CH - 1) / CH;            // chunks up to the last live one
     const int cnt = min(CH, n - p0);
     const int mc = XSTRIDE;                       // slots per head: one 4 KiB page each
     uint32_t tag = epoch * (uint32_t)a.layers + (uint32_t)a.layer + 1u;
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);   // the small loads stay ahead of the rows
     const int lt = t & 127, rp = lt >> 1, rh = lt & 1;   // row (position) and half of it
     const int rpos = p0 + rp;
-    const bool rlive = rpos < n;
+    const bool rlive = rpos < n && rpos >= s0;
     KvRaw<HALF_ROW, F16> row;
     row.load(kwave ? a.kcache : a.vcache,
              cache_base + (int64_t)(rlive && rpos != T ? rpos : p0) * HD + rh * HALF_ROW);
@@ -529,7 +534,8 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
                     for (int j = 0; j < HW; j++) {
                         const uint32_t base = (uint32_t)((kvh * G + wave + 2 * min(j, nh - 1)) * mc) * 8;
 #pragma unroll
-                        for (int i = 0; i < 4; i++) v[j][i] = l2_load64(rx, base + 8 * (uint32_t)min(lane + 64 * i, nch - 1));
+                        for (int i = 0; i < 4; i++)
+                            v[j][i] = l2_load64(rx, base + 8 * (uint32_t)min(c0 + lane + 64 * i, nch - 1));
                     }
                     if (poll_ready<HW>(v, tag)) break;
                     if (it >= a.spin_max) {
@@ -548,7 +554,7 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
                 uint64_t v[1][4];
                 float res[1];
                 for (int it = 0;; it++) {
-                    poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, nch, mc);
+                    poll_issue<1>(v, a.xmax + ((int64_t)kvh * G + h) * mc, 0, lane, c0, nch, mc);
                     if (poll_ready<1>(v, tag)) break;
                     if (it >= a.spin_max) {
                         if (lane == 0) atomicOr(a.err, 1);
@@ -590,10 +596,10 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         {
 #pragma clang fp contract(off)
             const float x = sc_s[h][pp] - gmax[h];
-            // Softmax: ExpApprox on the vector lanes (first 8*floor(n/8)), expf on the tail
+            // Softmax: ExpApprox on the vector lanes (first 8*floor(len/8) of the window), expf on the tail
             e = sidx < n8 ? exp_approx(x) : expf(x);
         }
-        sc_s[h][pp] = pp < cnt ? e : 0.f;
+        sc_s[h][pp] = pp < cnt && sidx >= s0 ? e : 0.f;
     }
     __syncthreads();   // exponentials visible; the V rows are in registers (pool reused below)
     // XL: the partials go out as tagged 64-bit words, (tag << 32) | float bits,
@@ -647,8 +653,9 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         // frees the LDS pool for reuse).
         __syncthreads();
         constexpr int NCOL = G * HD;                  // outputs of the kv head
-        const int per = (NCOL + nch - 1) / nch;       // outputs per chunk workgroup
-        const int j0 = c * per, nc = min(NCOL, j0 + per) - j0;
+        const int nlive = nch - c0;                   // chunks in the window
+        const int per = (NCOL + nlive - 1) / nlive;   // outputs per chunk workgroup
+        const int j0 = (c - c0) * per, nc = min(NCOL, j0 + per) - j0;
         if (nc <= 0) return;
         // Two lane layouts.  Many chunks (fewer than 64 columns each): columns
         // run fastest over the lanes (padded to a power of two, ncp), so a load
@@ -663,7 +670,7 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
         while (ncp < nc) ncp *= 2;
         const bool wide = ncp >= 64;
         int ngrp = 1;
-        while (2 * ngrp * (wide ? nc : ncp) <= WG && 2 * ngrp <= nch && 2 * ngrp <= 64) ngrp *= 2;
+        while (2 * ngrp * (wide ? nc : ncp) <= WG && 2 * ngrp <= nlive && 2 * ngrp <= 64) ngrp *= 2;
         const int np = wide ? 1 : (ngrp * ncp + 63) / 64;   // partials per column
         float* cred = reinterpret_cast<float*>(pool);  // [np][ncp] sums of e.V, then [np][ncp] sums of e
         float* zred = cred + np * ncp;
@@ -680,7 +687,7 @@ __global__ __launch_bounds__(WG) void attn_fused_kernel(AttnArgs a) {
             zacc = 0.f;
             const uint32_t off = ((uint32_t)kvh * NCOL + j0 + col) * 8;
             const uint32_t zoff = ((uint32_t)kvh * G + (uint32_t)(j0 + col) / HD) * 8;
-            for (int cc = g; cc < nch; cc += 4 * ngrp) {
+            for (int cc = c0 + g; cc < nch; cc += 4 * ngrp) {
                 uint64_t v[4], w[4];
                 for (int it = 0;; it++) {
                     asm volatile("" ::: "memory");   // a fresh load every poll
@@ -759,10 +766,11 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(AttnArgs a) {
     __shared__ float z_s[NG];
     const int n = *a.pos + 1;
     const int nch = (n + CHP - 1) / CHP;
+    const int c0 = a.window > 0 ? max(0, n - a.window) / CHP : 0;   // the window's first chunk
     const int hq = blockIdx.x, g = threadIdx.x / HD, d = threadIdx.x - g * HD;
     float acc = 0.f, z = 0.f;
 #pragma unroll 8
-    for (int i = g; i < nch; i += NG) {
+    for (int i = c0 + g; i < nch; i += NG) {
         acc += a.part_out[((int64_t)i * a.heads + hq) * HD + d];
         z += a.part_sum[(int64_t)i * a.heads + hq];
     }
@@ -800,6 +808,9 @@ hipError_t launch_hg(const AttnArgs& a, hipStream_t s) {
         attn_combine_kernel<HD><<<a.heads, (1024 / HD) * HD, 0, s>>>(a);
         return hipGetLastError();
     }
+    // the three-launch form attends to every position: a model with a window
+    // runs the one-launch form (its creation refuses a window otherwise)
+    if (a.window > 0) return hipErrorInvalidValue;
     attn_scores_kernel<HD, G><<<dim3(nchunks, a.kv_heads), WG, 0, s>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -1022,6 +1022,7 @@ int enqueue_step(llmdot_hip_model* m) {
         aa.fused = m->attn_fused ? 1 : 0; aa.xmax = m->xmax; aa.epoch = m_epoch(m);
         aa.layer = l; aa.layers = d.layers; aa.spin_max = m->attn_spin; aa.err = m_err(m);
         aa.xcd_exchange = m->attn_xcd_exchange ? 1 : 0; aa.xpart = m->xpart;
+        aa.window = d.sliding_window;
         HIPCHK(launch_attention(aa, s));
         {   // O projection + residual (IE:444-449, IE:189), h packed for the FFN RmsNorm
             GemvArgs ga{};
@@ -1079,9 +1080,10 @@ bool prefill_check(const llmdot_hip_model* m) {
     const auto& d = m->d;
     const int qdim = d.heads * d.head_dim;
     for (const auto& w : m->L) {
-        // the batched path has no per-head Q/K norm stage: such a model's
-        // prompt runs through the decode step token by token
-        if (w.q_norm_f || w.k_norm_f) return false;
+        // the batched path has no per-head Q/K norm stage and attends to every
+        // position: such a model's prompt runs through the decode step token
+        // by token
+        if (w.q_norm_f || w.k_norm_f || d.sliding_window > 0) return false;
         const Weight* in_h[5] = {w.q, w.k, w.v, w.gate, w.up};
         for (auto* x : in_h)
             if (!prefill_gemm_supported(x->type, d.hidden)) return false;
@@ -1415,6 +1417,10 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     m->attn_fused = attn_fused_ok(d.heads, d.kv_heads, d.head_dim, d.context);
     if (const char* v = getenv("LLMDOT_HIP_ATTN_FUSED")) m->attn_fused = m->attn_fused && strcmp(v, "0") != 0;
     if (const char* v = getenv("LLMDOT_HIP_ATTN_SPIN")) m->attn_spin = atoi(v) >= 0 ? atoi(v) : m->attn_spin;
+    if (d.sliding_window < 0) return bail(fail(LLMDOT_E_INVALID, "negative sliding window"));
+    if (d.sliding_window > 0 && !m->attn_fused)
+        return bail(fail(LLMDOT_E_UNSUPPORTED, "sliding-window attention needs the one-launch attention "
+                                               "(at most 16384 positions, LLMDOT_HIP_ATTN_FUSED not 0)"));
     if ((rc = A(sizeof(uint64_t) * (size_t)attn_xmax_slots(d.heads), &p))) return bail(rc); m->xmax = (uint64_t*)p;
     // The XCD-local chunk-maximum exchange where the shape fits it (attn_xcd_fits)
     // and the device deals workgroups to XCDs in turn; LLMDOT_HIP_ATTN_XCD=0 keeps

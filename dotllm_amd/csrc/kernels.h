@@ -142,6 +142,9 @@ struct AttnArgs {
     // bits: [max_chunks][heads][head_dim] sums of e.V, then [max_chunks][heads]
     // sums of e (max_chunks = attn_max_chunks)
     uint64_t* xpart;
+    // SlidingWindow (IE:385-387): with window > 0 only the last `window`
+    // positions attend (one-launch form only); 0 attends to all
+    int window;
 };
 // Whether the XCD-local exchange suits the shape: kv heads a multiple of 8,
 // and every live chunk of the kv heads one XCD serves (kv_heads / 8 of them,

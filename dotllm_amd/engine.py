@@ -99,8 +99,6 @@ class InferenceEngine:
         cfg = model.config
         if cfg.ffn_type != "swiglu":
             raise NotImplementedError("only SwiGLU FFN tensors are supported")
-        if cfg.sliding_window:
-            raise NotImplementedError("sliding-window attention is not supported")
         if any(h != cfg.head_count_kv for h in cfg.kv_heads_per_layer):
             raise NotImplementedError("per-layer KV head counts are not supported")
         self.model = model
@@ -124,6 +122,7 @@ class InferenceEngine:
                                 if cfg.rope_scaling_type == "linear" and cfg.rope_scaling_factor > 1 else 1.0)
         d.kv_fp16 = 1 if kv_fp16 else 0
         d.bos = cfg.bos_token_id
+        d.sliding_window = int(cfg.sliding_window)
         d.key_prefix = prefix.encode()
         self._m = C.c_void_p()
         _call(lib().llmdot_hip_model_create(self.backend.handle, C.byref(d), C.byref(self._m)))

@@ -87,11 +87,12 @@ def tensor_seed(seed: int, name: str) -> int:
     return (int(seed) * 0x9E3779B1 + zlib.crc32(name.encode())) & 0xFFFFFFFFFFFFFFFF
 
 
-def metadata(spec: dict, context: int | None = None, eos: int = -1) -> list:
+def metadata(spec: dict, context: int | None = None, eos: int = -1, sliding_window: int = 0) -> list:
     a = spec["arch"]
     ctx = int(context or spec["context"])
     toks = [f"<t{i}>" for i in range(spec["vocab"])]
-    return [
+    swa = [(f"{a}.attention.sliding_window", gguf.U32, int(sliding_window))] if sliding_window else []
+    return swa + [
         ("general.architecture", gguf.STR, a),
         ("general.name", gguf.STR, f"synthetic-{a}"),
         ("general.alignment", gguf.U32, 32),
@@ -134,7 +135,7 @@ def tensor_sigma(name: str, spec: dict, sigma: float, scaled_init: bool) -> floa
 def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int | None = None,
                 threads: int | None = None, spec: dict | None = None, scaled_init: bool = False,
                 eos: int = -1, tied: bool = False, norm_type: int = F32, fused_qkv: bool = False,
-                qk_norm: bool = False) -> np.ndarray:
+                qk_norm: bool = False, sliding_window: int = 0) -> np.ndarray:
     """Builds the whole GGUF file image in memory (uint8 numpy array).
 
     eos: tokenizer.ggml.eos_token_id (-1: never stops); tied: no output.weight,
@@ -144,13 +145,14 @@ def build_image(name: str, seed: int = 1234, sigma: float = 0.02, context: int |
     separate tensor of the same type would be (same seed), so a fused image
     holds the same weights as the separate one wherever the types agree;
     qk_norm: per-head Q/K RmsNorm weights (1 + 0.3 N(0, 1), seeded), so that a
-    path that skipped or misplaced them would show."""
+    path that skipped or misplaced them would show; sliding_window:
+    {arch}.attention.sliding_window (attend to the last N positions)."""
     spec = spec or SPECS[name]
     tl = [(n, r, c, (norm_type if n.endswith("_norm.weight") else t)) for n, r, c, t in tensor_list(spec, fused_qkv, qk_norm)
           if not (tied and n == "output.weight")]
     qd, kvd = spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
     infos = [(n, (c,) if r == 1 else (c, r), t, byte_count(t, r * c)) for n, r, c, t in tl]
-    hdr, offsets, total = gguf.header_bytes(metadata(spec, context, eos), infos)
+    hdr, offsets, total = gguf.header_bytes(metadata(spec, context, eos, sliding_window), infos)
     img = np.empty(total, dtype=np.uint8)
     img[:len(hdr)] = np.frombuffer(hdr, dtype=np.uint8)
     base = len(hdr)

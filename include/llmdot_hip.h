@@ -204,6 +204,7 @@ typedef struct llmdot_hip_model_desc {
     float rope_linear_factor;/* RopeScalingFactor when type is Linear, else 1 */
     int32_t kv_fp16;         /* 1: fp16 KV cache (default), 0: fp32 as the reference */
     int32_t bos;             /* BosTokenId (used when the prompt is empty) */
+    int32_t sliding_window;  /* SlidingWindow: attend to the last N positions (IE:385-387); 0 = all */
     /* Weight keys follow GGUF tensor names (src/Llmdot.Core/Loading/TensorNameResolver.cs:22-107):
      * token_embd.weight, output_norm.weight, output.weight (optional: tied to
      * token_embd), blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,

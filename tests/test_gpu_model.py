@@ -407,3 +407,50 @@ def test_attention_wait_limit_reports_error(tiny_image):
     eng.dispose()
     be.dispose()
     assert errors >= 1
+
+
+@pytest.mark.parametrize("window,path", [(40, "one launch, XCD-local exchange"),
+                                         (40, "one launch, exchange through the coherence point"),
+                                         (100, "one launch, XCD-local exchange")])
+def test_sliding_window_tiny(window, path):
+    """SlidingWindow (IE:385-387): the last `window` positions attend, the
+    Softmax's vector lanes counted from the window's start.  A 20-token
+    prompt (token by token: the batched prompt path has no window) and 180
+    greedy tokens take the window's start across the 64-position chunks
+    (chunks wholly before it leave at once; the first live one masks its
+    early rows), in both exchange forms, against the oracle: every token and
+    every step's logits within 2e-2, fp16 KV."""
+    img = synth.build_image("tiny", seed=17, context=256, sliding_window=window)
+    prompt = synth.prompt(32000, 20, seed=6)
+    be, eng = _fresh_engine_env(img, ATTN_PATHS[path], 256, kv_fp16=True)
+    toks, logits = eng.generate_all(prompt, greedy(180), return_logits=True)
+    eng.dispose()
+    be.dispose()
+    ref = O.Model(img, kv_fp16=True, context=256)
+    rt, rl = ref.generate(prompt, 180, return_logits=True)
+    ref.close()
+    assert toks == rt
+    err = float(np.max(np.abs(np.asarray(logits) - rl)))
+    plain = O.Model(synth.build_image("tiny", seed=17, context=256), kv_fp16=True, context=256)
+    pt, _ = plain.generate(prompt, 180)
+    plain.close()
+    print(f"window {window}, {path}: 180 tokens identical, max |dlogit| {err:.2e}; "
+          f"without the window the oracle's tokens first differ at step "
+          f"{next((i for i, (a, b) in enumerate(zip(pt, rt)) if a != b), len(rt))}")
+    assert err <= LOGIT_TOL
+    assert pt != rt   # the window changes the result
+
+
+def test_sliding_window_small5_greedy(hip, oracle_threads):
+    """A window of 30 positions with query groups of 2 (kv heads not a
+    multiple of 8: the exchange through the coherence point and the combine
+    launch): 8-token prompt, 100 greedy tokens, under the floor-based bounds."""
+    _big_model_check(hip, "small5", 8, 100, 112, near_tie_min=1e-4, sliding_window=30)
+
+
+def test_sliding_window_needs_one_launch_attention():
+    """The three-launch attention has no window: a windowed model asks for
+    the one-launch form and is refused (LLMDOT_E_UNSUPPORTED) without it."""
+    img = synth.build_image("tiny", seed=17, context=256, sliding_window=40)
+    with pytest.raises(Exception, match="sliding-window"):
+        _fresh_engine_env(img, ATTN_PATHS["three launches"], 256, kv_fp16=True)

@@ -115,11 +115,14 @@ class Forward:
                 k = np.stack([self.norm(r, W[p + "attn_k_norm.weight"]) for r in k])
             q, k = self.rope(q, pos), self.rope(k, pos)
             self.K[l, pos], self.V[l, pos] = k, v
+            # SlidingWindow (IE:385-387): the last W positions only
+            w = self.cfg.sliding_window
+            lo = max(0, pos + 1 - w) if w > 0 else 0
             out = np.zeros((H, hd))
             for hh in range(H):
                 kv = hh // group
-                sc = self.K[l, :pos + 1, kv] @ q[hh] * (1.0 / np.sqrt(hd))
-                out[hh] = self.softmax(sc) @ self.V[l, :pos + 1, kv]
+                sc = self.K[l, lo:pos + 1, kv] @ q[hh] * (1.0 / np.sqrt(hd))
+                out[hh] = self.softmax(sc) @ self.V[l, lo:pos + 1, kv]
             x = x + W[p + "attn_output.weight"] @ out.reshape(-1)
             h2 = self.norm(x, W[p + "ffn_norm.weight"])
             a = self.silu(W[p + "ffn_gate.weight"] @ h2) * (W[p + "ffn_up.weight"] @ h2)
@@ -142,12 +145,15 @@ GQA4 = dict(arch="llama", hidden=512, layers=2, heads=8, kv_heads=2, head_dim=64
 
 @pytest.mark.parametrize("name,spec,opts", [("tiny", None, {}), ("small5", None, {}), ("gqa4", GQA4, {}),
                                             ("gqa4", GQA4, dict(qk_norm=True)),
-                                            ("small5", None, dict(fused_qkv=True, qk_norm=True))])
+                                            ("small5", None, dict(fused_qkv=True, qk_norm=True)),
+                                            ("tiny", None, dict(sliding_window=5))])
 def test_process_token_composition(name, spec, opts):
     """16 teacher-forced steps of a random token stream: the oracle's logits
     within 1e-4 of the fp64 forward at every step (MHA head_dim 64 Q8_0;
     query groups of 2 with head_dim 128 and Q5_K/Q6_K; groups of 4 with
-    Q4_K/Q6_K and theta 500000; per-head Q/K norms, alone and with fused Q/K/V)."""
+    Q4_K/Q6_K and theta 500000; per-head Q/K norms, alone and with fused Q/K/V;
+    a sliding window of 5 positions, so 11 of the 16 steps attend to a window
+    whose vector lanes start inside the cache)."""
     img = synth.build_image(name if spec is None else "x", seed=31, spec=spec, **opts)
     fw = Forward(img, 32)
     m = O.Model(img, kv_fp16=False, context=32)
