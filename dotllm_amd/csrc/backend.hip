@@ -1080,10 +1080,9 @@ bool prefill_check(const llmdot_hip_model* m) {
     const auto& d = m->d;
     const int qdim = d.heads * d.head_dim;
     for (const auto& w : m->L) {
-        // the batched path has no per-head Q/K norm stage and attends to every
-        // position: such a model's prompt runs through the decode step token
-        // by token
-        if (w.q_norm_f || w.k_norm_f || d.sliding_window > 0) return false;
+        // the window is on the fp16 (MFMA) attention only: with an fp32 KV
+        // cache a windowed model's prompt runs through the decode step
+        if (d.sliding_window > 0 && !d.kv_fp16) return false;
         const Weight* in_h[5] = {w.q, w.k, w.v, w.gate, w.up};
         for (auto* x : in_h)
             if (!prefill_gemm_supported(x->type, d.hidden)) return false;
@@ -1213,6 +1212,8 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
         aa.T = T; aa.pos0 = pos0; aa.ld_scores = d.context;
         aa.heads = d.heads; aa.kv_heads = d.kv_heads; aa.head_dim = d.head_dim; aa.rope_half = m->rope_half;
         aa.context = d.context; aa.kv_fp16 = d.kv_fp16;
+        aa.q_norm = w.q_norm_f; aa.k_norm = w.k_norm_f; aa.eps = d.eps;
+        aa.window = d.sliding_window;
         HIPCHK(launch_prefill_rope_kv(aa, s));
         HIPCHK(launch_prefill_attention(aa, s));
         HIPCHK(launch_prefill_planes(m->pf_attn, T, qdim, nullptr, 0.f, pl, s));

@@ -215,6 +215,11 @@ struct PfAttnArgs {
     // q, k and v as sums of q_split (k_split, v_split) K parts, q_part elements apart
     int q_split, k_split, v_split;
     int64_t q_part, k_part, v_part;
+    // per-head Q/K RmsNorm weights [head_dim] applied before RoPE (null: none)
+    // with eps; SlidingWindow (0: every earlier position; fp16 KV path only)
+    const float *q_norm, *k_norm;
+    float eps;
+    int window;
 };
 bool prefill_gemm_supported(uint32_t type, int cols);
 // Optional RmsNorm (norm_w non-null) of each row of x, then its planes.

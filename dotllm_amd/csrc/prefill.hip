@@ -701,6 +701,40 @@ __device__ __forceinline__ float sum_parts(const float* x, int64_t idx, int n, i
     return v;
 }
 
+// With per-head Q/K norms (IE:354-359, IE:367-372) one wavefront takes a
+// head: the sum of squares of its (summed) row, then VectorMath.RmsNorm's
+// vector-lane / tail forms on each element and its rotation partner, then
+// the rotation; the decode step's qk_norm_kernel sums in the same order.
+__device__ __forceinline__ void pf_norm_rope_heads(const float* x, int split, int64_t part, int64_t row0, int nheads,
+                                                   int HD, const float* w, float eps, const float* cs, const float* sn,
+                                                   int half, float* qr_out, void* cache, int64_t slot0,
+                                                   int64_t head_stride, int fp16) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    auto partner = [&](int d) { return d < half ? d + half : (d < 2 * half ? d - half : d); };
+    auto pidx = [&](int d) { return d < half ? d : (d < 2 * half ? d - half : 0); };
+    const int n8 = HD & ~7;
+    for (int h = wave; h < nheads; h += WG / 64) {
+        const int64_t r = row0 + (int64_t)h * HD;
+        float ss = 0.f;
+        for (int d = lane; d < HD; d += 64) {
+            const float v = sum_parts(x, r + d, split, part);
+            ss += v * v;
+        }
+        ss = wave_sum(ss);
+        const float inv = (1.0f / (sqrtf(((ss / (float)HD) + eps))));
+        auto nrm = [&](int d) {
+#pragma clang fp contract(off)
+            const float v = sum_parts(x, r + d, split, part);
+            return d < n8 ? ((w[d] * v) * inv) : (w[d] * (v * inv));
+        };
+        for (int d = lane; d < HD; d += 64) {
+            const float y = rope_pair(nrm(d), nrm(partner(d)), cs[pidx(d)], sn[pidx(d)], d, half);
+            if (qr_out) qr_out[(int64_t)h * HD + d] = y;
+            else store_kv(cache, slot0 + (int64_t)h * head_stride + d, y, fp16);
+        }
+    }
+}
+
 __global__ __launch_bounds__(WG) void pf_rope_kv_kernel(PfAttnArgs a) {
     const int t = blockIdx.x, p = a.pos0 + t;
     const int HD = a.head_dim, half = a.rope_half;
@@ -710,7 +744,13 @@ __global__ __launch_bounds__(WG) void pf_rope_kv_kernel(PfAttnArgs a) {
     // element d's rotation partner and the pair's table index
     auto partner = [&](int d) { return d < half ? d + half : (d < 2 * half ? d - half : d); };
     auto pidx = [&](int d) { return d < half ? d : (d < 2 * half ? d - half : 0); };
-    for (int i = threadIdx.x; i < qdim; i += WG) {
+    if (a.q_norm)
+        pf_norm_rope_heads(a.q, a.q_split, a.q_part, (int64_t)t * qdim, a.heads, HD, a.q_norm, a.eps, cs, sn, half,
+                           a.qr + (int64_t)t * qdim, nullptr, 0, 0, 0);
+    if (a.k_norm)
+        pf_norm_rope_heads(a.k, a.k_split, a.k_part, (int64_t)t * kvdim, a.kv_heads, HD, a.k_norm, a.eps, cs, sn,
+                           half, nullptr, a.kcache, (int64_t)p * HD, (int64_t)a.context * HD, a.kv_fp16);
+    for (int i = threadIdx.x; i < qdim && !a.q_norm; i += WG) {
         const int h = i / HD, d = i - h * HD;
         const int64_t r = (int64_t)t * qdim + h * HD;
         const float x = sum_parts(a.q, r + d, a.q_split, a.q_part);
@@ -721,9 +761,11 @@ __global__ __launch_bounds__(WG) void pf_rope_kv_kernel(PfAttnArgs a) {
         const int h = i / HD, d = i - h * HD;
         const int64_t r = (int64_t)t * kvdim + h * HD;
         const int64_t slot = ((int64_t)h * a.context + p) * HD + d;
-        const float x = sum_parts(a.k, r + d, a.k_split, a.k_part);
-        const float y = sum_parts(a.k, r + partner(d), a.k_split, a.k_part);
-        store_kv(a.kcache, slot, rope_pair(x, y, cs[pidx(d)], sn[pidx(d)], d, half), a.kv_fp16);
+        if (!a.k_norm) {
+            const float x = sum_parts(a.k, r + d, a.k_split, a.k_part);
+            const float y = sum_parts(a.k, r + partner(d), a.k_split, a.k_part);
+            store_kv(a.kcache, slot, rope_pair(x, y, cs[pidx(d)], sn[pidx(d)], d, half), a.kv_fp16);
+        }
         store_kv(a.vcache, slot, sum_parts(a.v, (int64_t)t * kvdim + i, a.v_split, a.v_part), a.kv_fp16);
     }
 }
@@ -1020,14 +1062,18 @@ __global__ __launch_bounds__(WG) void pf_attn_max_mfma(PfAttnArgs a) {
     QFrag<HD> qf;
     qf.load(a, min(tq, a.T - 1), h, lk);
     const int last = tq < a.T ? a.pos0 + tq : -1;      // the query's last key
+    // SlidingWindow (IE:385-387): the query's first key, and the block's
+    // first tile (its first query's window starts earliest)
+    const int first = a.window > 0 ? max(0, last + 1 - a.window) : 0;
+    const int jstart = a.window > 0 ? max(0, a.pos0 + t0 + 1 - a.window) / AK * AK : 0;
     const int nkeys = a.pos0 + min(t0 + AQ, a.T);
     const int64_t kbase = (int64_t)kvh * a.context * HD;
     const _Float16* kc = reinterpret_cast<const _Float16*>(a.kcache);
     float m = -INFINITY;
     KTile<HD> kt_regs;
-    kt_regs.load(kc, kbase, 0, nkeys, tid);
+    kt_regs.load(kc, kbase, jstart, nkeys, tid);
     int it = 0;
-    for (int j0 = 0; j0 < nkeys; j0 += AK, it++) {
+    for (int j0 = jstart; j0 < nkeys; j0 += AK, it++) {
         const int buf = it & 1;
         kt_regs.store(Ks[buf], tid);   // buffer last read two tiles ago
         __syncthreads();
@@ -1036,8 +1082,10 @@ __global__ __launch_bounds__(WG) void pf_attn_max_mfma(PfAttnArgs a) {
         for (int kt = 0; kt < AK / 16; kt++) {
             const f4 c = qf.scores(Ks[buf], kt, lr, lk);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                if (j0 + kt * 16 + 4 * lk + r <= last) m = fmaxf(m, c[r]);
+            for (int r = 0; r < 4; r++) {
+                const int key = j0 + kt * 16 + 4 * lk + r;
+                if (key <= last && key >= first) m = fmaxf(m, c[r]);
+            }
         }
     }
     m = fmaxf(m, fx(lane_xor16, m));
@@ -1064,7 +1112,11 @@ __global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
     QFrag<HD> qf;
     qf.load(a, tqc, h, lk);
     const int last = tq < a.T ? a.pos0 + tq : -1;
-    const int n8 = (a.pos0 + tqc + 1) & ~7;            // keys of the query on the vector lanes
+    // the query's window (all earlier keys without one); its first
+    // 8 floor(len/8) keys are the Softmax's vector lanes
+    const int first = a.window > 0 ? max(0, a.pos0 + tqc + 1 - a.window) : 0;
+    const int jstart = a.window > 0 ? max(0, a.pos0 + t0 + 1 - a.window) / AK * AK : 0;
+    const int n8 = first + ((a.pos0 + tqc + 1 - first) & ~7);
     const float mq = a.rowmax[(int64_t)h * a.T + tqc];
     const int nkeys = a.pos0 + min(t0 + AQ, a.T);
     const int64_t base = (int64_t)kvh * a.context * HD;
@@ -1084,9 +1136,9 @@ __global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
             vr[k] = *reinterpret_cast<const h8*>(vc + base + (int64_t)min(j0 + r, nkeys - 1) * HD + 8 * q);
         }
     };
-    kr.load(kc, base, 0, nkeys, tid);
-    load_v(0);
-    for (int j0 = 0; j0 < nkeys; j0 += AK) {
+    kr.load(kc, base, jstart, nkeys, tid);
+    load_v(jstart);
+    for (int j0 = jstart; j0 < nkeys; j0 += AK) {
         __syncthreads();   // the previous tile's LDS reads are done
         kr.store(Ks, tid);
 #pragma unroll
@@ -1111,7 +1163,7 @@ __global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
                 for (int r = 0; r < 4; r++) {
                     const int key = j0 + kt * 16 + 4 * lk + r;
                     float ev = 0.f;
-                    if (key <= last) {
+                    if (key <= last && key >= first) {
 #pragma clang fp contract(off)
                         const float x = c[r] - mq;
                         ev = key < n8 ? exp_approx(x) : expf(x);

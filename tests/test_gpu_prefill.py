@@ -261,3 +261,33 @@ def test_batched_matmul_short_k(hip, t, k):
     hip.mat_mul(a.reshape(-1), w, y, t, k, n)
     err = row_rel_err(y.reshape(m, n), ref)
     assert err <= FP32_LEVEL, err
+
+
+@pytest.mark.parametrize("window,split", [(40, None), (100, None), (100, 150), (40, 70)])
+def test_prefill_tiny_sliding_window(hip, window, split):
+    """SlidingWindow (IE:385-387) in the batched prompt (fp16 KV, the MFMA
+    attention): each query attends from its window's start, the Softmax's
+    vector lanes counted from there, and a query block starts at the key tile
+    of its first query's window.  300 tokens (5 query tiles whose windows start
+    in different key tiles), also as two calls (the second at pos0 = split,
+    its windows reaching into the cache), against the oracle's loop."""
+    img = synth.build_image("tiny", seed=1234, context=400, sliding_window=window)
+    prompt = synth.prompt(32000, 300, seed=29)
+    _prompt_check(hip, img, prompt, 400, True, [0, 3], split=split)
+
+
+def test_prefill_small5_sliding_window(hip, oracle_threads):
+    """A window of 30 with query groups of 2 (Q5_K_M mix): 80 tokens, fp16 KV."""
+    img = synth.build_image("small5", seed=1234, context=96, sliding_window=30)
+    _prompt_check(hip, img, synth.prompt(32000, 80, seed=7), 96, True, [0, 3])
+
+
+@pytest.mark.parametrize("kv_fp16", [True, False])
+def test_prefill_qk_norm(hip, oracle_threads, kv_fp16):
+    """Per-head Q/K norms (IE:354-373) in the batched prompt: each head's row
+    normed in the RoPE/KV pass before its rotation; tiny (MHA) 200 tokens and
+    small5 (query groups of 2, fused Q/K/V) 80 tokens, against the oracle."""
+    img = synth.build_image("tiny", seed=1234, context=256, qk_norm=True)
+    _prompt_check(hip, img, synth.prompt(32000, 200, seed=31), 256, kv_fp16, [0, 3])
+    img = synth.build_image("small5", seed=1234, context=96, qk_norm=True, fused_qkv=True)
+    _prompt_check(hip, img, synth.prompt(32000, 80, seed=7), 96, kv_fp16, [0, 3])
