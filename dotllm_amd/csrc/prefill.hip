@@ -1050,7 +1050,8 @@ __device__ __forceinline__ void attn_block(const PfAttnArgs& a, int& t0, int& h)
     t0 = (nqb - 1 - L / a.heads) * AQ;
 }
 
-// Pass 1: each query's maximum score over keys 0 .. pos0 + t.
+// Pass 1: each query's maximum score over its keys, 0 (or its window's
+// start) .. pos0 + t.
 template <int HD>
 __global__ __launch_bounds__(WG) void pf_attn_max_mfma(PfAttnArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][AK][HD + KPAD];
@@ -1094,8 +1095,8 @@ __global__ __launch_bounds__(WG) void pf_attn_max_mfma(PfAttnArgs a) {
 }
 
 // Pass 2: the same scores, softmax numerators (ExpApprox on the first
-// 8 floor(n/8) keys, expf on the tail, VM:215-258) and out = sum_j e_j V_j /
-// sum_j e_j.
+// 8 floor(n/8) of the query's n keys, expf on the tail, VM:215-258) and
+// out = sum_j e_j V_j / sum_j e_j.
 template <int HD>
 __global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
     constexpr int DT = HD / 16;              // 16-wide output tiles over the head dimension
