@@ -454,3 +454,42 @@ def test_sliding_window_needs_one_launch_attention():
     img = synth.build_image("tiny", seed=17, context=256, sliding_window=40)
     with pytest.raises(Exception, match="sliding-window"):
         _fresh_engine_env(img, ATTN_PATHS["three launches"], 256, kv_fp16=True)
+
+
+def test_phi3mini_gguf_layout_past_the_window(hip, oracle_threads):
+    """The Phi-3-mini GGUF layout as a whole: fused Q8_0 attn_qkv and
+    attention.sliding_window 2047, with 2100 seeded KV positions on both
+    sides, then 3 steps from position 2100 (so each attends to its last 2047
+    positions only: the window starts inside the cache's chunk 0), fp16 KV,
+    teacher-forced on the oracle's tokens within the floor-based bound."""
+    ctx, cap = 2100, 2112
+    img = synth.build_image("phi3mini", seed=1234, context=cap, fused_qkv=True, sliding_window=2047)
+    pair = OraclePair(img, True, cap)
+    pair.kv_fill_random(ctx, seed=11)
+    eng = _engine(hip, img, True, context=cap)
+    eng.kv_fill_random(ctx, seed=11)
+    tok, errs, rows = 1, [], []
+    for pos in range(ctx, ctx + 3):
+        rl = pair.step(tok, pos)
+        gl = eng.process_token(tok, pos)
+        errs.append(float(np.max(np.abs(gl - rl))))
+        rows.append((gl, rl))
+        tok = int(np.argmax(rl))
+    pair.close()
+    eng.dispose()
+    bound, tie_at = pair.bounds()
+    for (gl, rl), t in zip(rows, tie_at):
+        top2 = np.sort(rl)[-2:]
+        if top2[1] - top2[0] >= t:
+            assert int(np.argmax(gl)) == int(np.argmax(rl))
+    # the window matters here: the same weights attending to every position
+    plain = O.Model(synth.build_image("phi3mini", seed=1234, context=cap, fused_qkv=True), kv_fp16=True,
+                    context=cap)
+    plain.kv_fill_random(ctx, seed=11)
+    moved = float(np.max(np.abs(plain.process_token(1, ctx) - rows[0][1])))
+    plain.close()
+    print(f"phi3mini fused QKV, window 2047, from position {ctx}: max |dlogit| per step "
+          f"{['%.3e' % e for e in errs]}, bounds {['%.3e' % b for b in bound]}; "
+          f"without the window the first step moves by {moved:.3e}")
+    assert np.all(np.asarray(errs) <= bound), (errs, bound)
+    assert moved > 2 * bound[0]
