@@ -291,7 +291,17 @@ public sealed unsafe class HipBackend : IComputeBackend, IDeviceDecodeBackend
     public IDeviceDecoder? TryCreateDecoder(LoadedModel model)
     {
         if (!HipDecoder.Supports(model, out _)) return null;
-        var d = new HipDecoder(model, this);
+        HipDecoder d;
+        try
+        {
+            d = new HipDecoder(model, this);
+        }
+        catch (NotSupportedException)
+        {
+            // a shape the step refuses at creation (e.g. a sliding window with
+            // a context beyond the one-launch attention's 16384 positions)
+            return null;
+        }
         lock (_lock) _decoders.Add(d);
         return d;
     }
