@@ -42,3 +42,24 @@ def test_tiny_greedy_golden():
         np.testing.assert_allclose(row[st["top5"]], st["top5_logits"], rtol=0, atol=0)
         assert abs(float(np.sum(row, dtype=np.float64)) - st["sum"]) <= 1e-9 * max(1.0, abs(st["sum"]))
         assert abs(float(np.sum(row.astype(np.float64) ** 2)) - st["sumsq"]) <= 1e-9 * st["sumsq"]
+
+
+def test_device_floors_within_reordering_range():
+    """The greedy regression floors of the full-size GPU runs (MIN_SAME in
+    tests/test_gpu_long.py: how far the device was measured to keep the
+    reference's tokens) against how far the oracle itself keeps them when
+    only its summation order changes (order_prefix.json, written by
+    tests/golden/order_prefix.py from the same fixtures): every floor is at
+    least the shortest of the reorderings, so the device departs no earlier
+    than some valid reordering of the reference's arithmetic; and each
+    recorded prefix length is what the recorded tokens give against the
+    fixture's."""
+    from test_gpu_long import MIN_SAME
+    d = json.load(open(os.path.join(HERE, "order_prefix.json")))
+    assert set(d) <= set(MIN_SAME)
+    for key, r in d.items():
+        assert MIN_SAME[key] >= min(r["identical"]), (key, MIN_SAME[key], r["identical"])
+        ref = np.load(os.path.join(HERE, f"long_{key}.npz"))["tokens"].tolist()
+        for o, toks in r["tokens"].items():
+            same = next((i for i, (a, b) in enumerate(zip(toks, ref)) if a != b), len(ref))
+            assert same == r["identical"][r["orders"].index(int(o))], (key, o)
