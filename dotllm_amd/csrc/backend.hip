@@ -82,6 +82,10 @@ bool env_flag(const char* name) {
     const char* v = getenv(name);
     return v && *v && strcmp(v, "0") != 0;
 }
+bool env_is_zero(const char* name) {
+    const char* v = getenv(name);
+    return v && strcmp(v, "0") == 0;
+}
 
 }  // namespace
 
@@ -1180,6 +1184,14 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
                                            sp, n);
         return e != hipSuccess ? e : launch_prefill_add_parts(m->pf_h, m->pf_parts_q, sp, n, n, s);
     };
+    // Q and K (same type) as one launch where neither would be split in K:
+    // their row tiles then share the CUs in one grid instead of K's narrow
+    // launch running beside Q's (LLMDOT_HIP_PF_QK_PAIR=0 turns this off)
+    const bool pair_ok = !env_is_zero("LLMDOT_HIP_PF_QK_PAIR") && qdim % 128 == 0;
+    auto qk_pair = [&](const LayerW& w) {
+        return pair_ok && w.q->type == w.k->type && prefill_ksplit(w.q->type, T, qdim, d.hidden) == 1 &&
+               prefill_ksplit(w.k->type, T, kvdim, d.hidden) == 1;
+    };
     HIPCHK(launch_embed_rows(m->embd->dev, m->embd->type, d.hidden, m->pf_tokens, T, m->pf_h, s));
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
@@ -1189,14 +1201,19 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
         llmdot_hip_ctx* c = m->ctx;
         int nq = 1, nk = 1, nv = 1;
         HIPCHK(hipEventRecord(c->fork, s));
-        HIPCHK(hipStreamWaitEvent(c->side[0], c->fork, 0));
         HIPCHK(hipStreamWaitEvent(c->side[1], c->fork, 0));
-        HIPCHK(proj(w.k, kvdim, d.hidden, m->pf_k, m->pf_parts_k, c->side[0], &nk));
         HIPCHK(proj(w.v, kvdim, d.hidden, m->pf_v, m->pf_parts_v, c->side[1], &nv));
-        HIPCHK(hipEventRecord(c->join[0], c->side[0]));
         HIPCHK(hipEventRecord(c->join[1], c->side[1]));
-        HIPCHK(proj(w.q, qdim, d.hidden, m->pf_q, m->pf_parts_q, s, &nq));
-        HIPCHK(hipStreamWaitEvent(s, c->join[0], 0));
+        if (qk_pair(w)) {   // Q and K in one launch, of 128-token tiles
+            HIPCHK(launch_prefill_gemm_pair(w.q->type, pl, w.q->dev, qdim, m->pf_q, qdim, w.k->dev, kvdim, m->pf_k,
+                                            kvdim, T, d.hidden, s));
+        } else {
+            HIPCHK(hipStreamWaitEvent(c->side[0], c->fork, 0));
+            HIPCHK(proj(w.k, kvdim, d.hidden, m->pf_k, m->pf_parts_k, c->side[0], &nk));
+            HIPCHK(hipEventRecord(c->join[0], c->side[0]));
+            HIPCHK(proj(w.q, qdim, d.hidden, m->pf_q, m->pf_parts_q, s, &nq));
+            HIPCHK(hipStreamWaitEvent(s, c->join[0], 0));
+        }
         HIPCHK(hipStreamWaitEvent(s, c->join[1], 0));
         PfAttnArgs aa{};
         aa.q = nq > 1 ? m->pf_parts_q : m->pf_q;

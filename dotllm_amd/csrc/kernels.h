@@ -237,6 +237,11 @@ hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const 
 // moved a deep-layer fp16 KV row one ulp past twice the oracle's reorder
 // floor.)
 int prefill_ksplit(uint32_t type, int M, int N, int K);
+// Two STORE products over the same planes in one launch: out[M][ldo] of the
+// [N][K] blocks w (N a multiple of 128 rows) and outb[M][ldob] of the [nb][K]
+// blocks wb, same type; each output equals launch_prefill_gemm's.
+hipError_t launch_prefill_gemm_pair(uint32_t type, const PfPlanes& p, const uint8_t* w, int N, float* out, int ldo,
+                                    const uint8_t* wb, int nb, float* outb, int ldob, int M, int K, hipStream_t s);
 // h[i] += sum over the nparts parts (stride elements apart) of parts[p][i], i < n.
 hipError_t launch_prefill_add_parts(float* h, const float* parts, int nparts, int64_t stride, int64_t n,
                                     hipStream_t s);

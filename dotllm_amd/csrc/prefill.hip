@@ -182,6 +182,11 @@ struct PfGemmArgs {
     int tiles_n;                         // weight-row tiles (128 rows; SWIGLU: 64 gate + 64 up)
     int ksplit;                          // K parts (STORE only): each a whole number of blocks
     int64_t part_stride;
+    // STORE with a second matrix: row tiles from tn_b on read wb [nb rows]
+    // into outb [M][ldob] (tn_b = tiles_n: none)
+    const uint8_t* wb;
+    float* outb;
+    int tn_b, nb, ldob;
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -432,11 +437,16 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
     const int K = a.K, spp = K / 32 / a.ksplit;   // 32-element steps per part
     const int st0 = part * spp, st1 = st0 + spp;
     const int64_t rbytes = (int64_t)(K / F::EPB) * F::BSZ;
+    // the matrix this row tile reads (uniform per workgroup): the second one
+    // from row tile tn_b on
+    const bool segb = EPI == PF_STORE && tn >= a.tn_b;
+    const int tnl = segb ? tn - a.tn_b : tn, Nl = segb ? a.nb : a.N;
+    const uint8_t* const wseg = segb ? a.wb : a.w;
     auto grow_of = [&](int r) {   // tile row -> weight row (SWIGLU: rows 0..63 gate, 64..127 up)
-        const int g = EPI == PF_SWIGLU ? tn * 64 + (r & 63) : tn * BN + r;
-        return min(g, a.N - 1);
+        const int g = EPI == PF_SWIGLU ? tn * 64 + (r & 63) : tnl * BN + r;
+        return min(g, Nl - 1);
     };
-    auto wsel = [&](int r) -> const uint8_t* { return EPI == PF_SWIGLU && r >= 64 ? a.w2 : a.w; };
+    auto wsel = [&](int r) -> const uint8_t* { return EPI == PF_SWIGLU && r >= 64 ? a.w2 : wseg; };
 
     // DMA sources.  Activations: instruction i of wave wv covers stage slots
     // q = (NX wv + i) 64 + lane: plane q / (4 TM), token (q >> 2) % TM,
@@ -674,10 +684,11 @@ __global__ __launch_bounds__(WG, 2) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int t = m0 + ti * 16 + 4 * lk + e;
-                    const int row = tn * BN + wn * 16 * TJ + tj * 16 + lr;
-                    if (t < a.M && row < a.N) {
+                    const int row = tnl * BN + wn * 16 * TJ + tj * 16 + lr;
+                    if (t < a.M && row < Nl) {
                         const float y = acc[ti][tj][e] * xi[ti][e];
-                        float* o = a.out + part * a.part_stride + (int64_t)t * a.ldo + row;
+                        float* o = segb ? a.outb + (int64_t)t * a.ldob + row
+                                        : a.out + part * a.part_stride + (int64_t)t * a.ldo + row;
                         if (EPI == PF_ADD) {
 #pragma clang fp contract(off)
                             *o = *o + y;
@@ -1204,7 +1215,9 @@ __global__ __launch_bounds__(WG, 3) void pf_attn_pv_mfma(PfAttnArgs a) {
 
 template <uint32_t FMT>
 hipError_t launch_gemm_fmt(int epi, PfGemmArgs a, hipStream_t s) {
-    a.tiles_n = epi == PF_SWIGLU ? (a.N + 63) / 64 : (a.N + BN - 1) / BN;
+    const int tn_a = epi == PF_SWIGLU ? (a.N + 63) / 64 : (a.N + BN - 1) / BN;
+    a.tiles_n = tn_a + (a.wb ? (a.nb + BN - 1) / BN : 0);
+    a.tn_b = tn_a;
     const int tiles = a.tiles_n * ((a.M + BM - 1) / BM) * a.ksplit;
     // 128 to 255 tiles of BM tokens fill only part of the CUs: 64-token tiles
     // (LLMDOT_HIP_PF_TM64=0 turns this off)
@@ -1258,6 +1271,10 @@ hipError_t launch_prefill_planes(const float* x, int M, int K, const float* norm
     return hipGetLastError();
 }
 
+namespace {
+hipError_t launch_gemm_type(uint32_t type, int epi, const PfGemmArgs& a, hipStream_t s);
+}
+
 hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const uint8_t* w, const uint8_t* w2, int M,
                                int N, int K, float* out, int ldo, hipStream_t s, int ksplit, int64_t part_stride) {
     if (M <= 0 || N <= 0 || !prefill_gemm_supported(type, K) || (epi == PF_SWIGLU && !w2) || ldo < N)
@@ -1271,6 +1288,22 @@ hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const 
     if ((int64_t)M * K * 2 >= (int64_t)1 << 31 || (int64_t)N * byte_count(type, K) >= ((int64_t)1 << 31) - 65536)
         return hipErrorInvalidValue;
     PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, w2, out, M, N, K, ldo, 0, ksplit, part_stride};
+    return launch_gemm_type(type, epi, a, s);
+}
+
+hipError_t launch_prefill_gemm_pair(uint32_t type, const PfPlanes& p, const uint8_t* w, int N, float* out, int ldo,
+                                    const uint8_t* wb, int nb, float* outb, int ldob, int M, int K, hipStream_t s) {
+    if (M <= 0 || N <= 0 || nb <= 0 || N % BN || !w || !wb || !prefill_gemm_supported(type, K) || ldo < N ||
+        ldob < nb)
+        return hipErrorInvalidValue;
+    if ((int64_t)M * K * 2 >= (int64_t)1 << 31 || (int64_t)std::max(N, nb) * byte_count(type, K) >= ((int64_t)1 << 31) - 65536)
+        return hipErrorInvalidValue;
+    PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, nullptr, out, M, N, K, ldo, 0, 1, 0, wb, outb, 0, nb, ldob};
+    return launch_gemm_type(type, PF_STORE, a, s);
+}
+
+namespace {
+hipError_t launch_gemm_type(uint32_t type, int epi, const PfGemmArgs& a, hipStream_t s) {
     switch (type) {
     case GGML_Q4_K: return launch_gemm_fmt<GGML_Q4_K>(epi, a, s);
     case GGML_Q5_K: return launch_gemm_fmt<GGML_Q5_K>(epi, a, s);
@@ -1280,6 +1313,7 @@ hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const 
     default: return hipErrorInvalidValue;
     }
 }
+}  // namespace
 
 hipError_t launch_prefill_rope_kv(const PfAttnArgs& a, hipStream_t s) {
     if (a.T <= 0 || a.q_split < 1 || a.k_split < 1 || a.v_split < 1) return hipErrorInvalidValue;

@@ -246,6 +246,34 @@ def test_prefill_64_token_tiles_bit_identical(hip, monkeypatch):
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
 
 
+def test_prefill_qk_pair_bit_identical(hip, monkeypatch):
+    """Phi-3-mini shape (Q and K Q8_0, V Q6_K), 1024-token prompt: Q and K
+    (24 row tiles each) run as one launch of 48 row tiles instead of two side
+    by side.  Each output's sum runs in the same order either way, so the last
+    logits and the KV cache must be bit-identical with the pair turned off."""
+    n, ctx = 1024, 1040
+    img = synth.build_image("phi3mini", seed=1234, context=ctx)
+    prompt = synth.prompt(32064, n, seed=31)
+    runs = []
+    for off in (False, True):
+        if off:
+            monkeypatch.setenv("LLMDOT_HIP_PF_QK_PAIR", "0")
+        else:
+            monkeypatch.delenv("LLMDOT_HIP_PF_QK_PAIR", raising=False)
+        eng = InferenceEngine(LoadedModel.load(img), hip, kv_fp16=True, context=ctx)
+        try:
+            logits, am = eng.prefill(prompt, 0)
+            kv = [eng.kv_read(layer, pos) for layer in (0, 15, 31) for pos in (0, 511, 1023)]
+        finally:
+            eng.dispose()
+        runs.append((np.array(logits, copy=True), am, kv))
+    (l0, a0, kv0), (l1, a1, kv1) = runs
+    assert a0 == a1
+    assert np.array_equal(l0, l1), float(np.max(np.abs(l0 - l1)))
+    for (k0, v0), (k1, v1) in zip(kv0, kv1):
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+
+
 @pytest.mark.parametrize("t", [Q8_0, Q4_0])
 @pytest.mark.parametrize("k", [96, 160])
 def test_batched_matmul_short_k(hip, t, k):
