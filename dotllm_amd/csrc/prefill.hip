@@ -1272,8 +1272,17 @@ hipError_t launch_prefill_planes(const float* x, int M, int K, const float* norm
 }
 
 namespace {
-hipError_t launch_gemm_type(uint32_t type, int epi, const PfGemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_type(uint32_t type, int epi, const PfGemmArgs& a, hipStream_t s) {
+    switch (type) {
+    case GGML_Q4_K: return launch_gemm_fmt<GGML_Q4_K>(epi, a, s);
+    case GGML_Q5_K: return launch_gemm_fmt<GGML_Q5_K>(epi, a, s);
+    case GGML_Q6_K: return launch_gemm_fmt<GGML_Q6_K>(epi, a, s);
+    case GGML_Q8_0: return launch_gemm_fmt<GGML_Q8_0>(epi, a, s);
+    case GGML_Q4_0: return launch_gemm_fmt<GGML_Q4_0>(epi, a, s);
+    default: return hipErrorInvalidValue;
+    }
 }
+}  // namespace
 
 hipError_t launch_prefill_gemm(uint32_t type, int epi, const PfPlanes& p, const uint8_t* w, const uint8_t* w2, int M,
                                int N, int K, float* out, int ldo, hipStream_t s, int ksplit, int64_t part_stride) {
@@ -1296,24 +1305,12 @@ hipError_t launch_prefill_gemm_pair(uint32_t type, const PfPlanes& p, const uint
     if (M <= 0 || N <= 0 || nb <= 0 || N % BN || !w || !wb || !prefill_gemm_supported(type, K) || ldo < N ||
         ldob < nb)
         return hipErrorInvalidValue;
-    if ((int64_t)M * K * 2 >= (int64_t)1 << 31 || (int64_t)std::max(N, nb) * byte_count(type, K) >= ((int64_t)1 << 31) - 65536)
+    if ((int64_t)M * K * 2 >= (int64_t)1 << 31 ||
+        (int64_t)std::max(N, nb) * byte_count(type, K) >= ((int64_t)1 << 31) - 65536)
         return hipErrorInvalidValue;
     PfGemmArgs a{p.xh, p.xl, p.sh, p.sl, p.xinv, w, nullptr, out, M, N, K, ldo, 0, 1, 0, wb, outb, 0, nb, ldob};
     return launch_gemm_type(type, PF_STORE, a, s);
 }
-
-namespace {
-hipError_t launch_gemm_type(uint32_t type, int epi, const PfGemmArgs& a, hipStream_t s) {
-    switch (type) {
-    case GGML_Q4_K: return launch_gemm_fmt<GGML_Q4_K>(epi, a, s);
-    case GGML_Q5_K: return launch_gemm_fmt<GGML_Q5_K>(epi, a, s);
-    case GGML_Q6_K: return launch_gemm_fmt<GGML_Q6_K>(epi, a, s);
-    case GGML_Q8_0: return launch_gemm_fmt<GGML_Q8_0>(epi, a, s);
-    case GGML_Q4_0: return launch_gemm_fmt<GGML_Q4_0>(epi, a, s);
-    default: return hipErrorInvalidValue;
-    }
-}
-}  // namespace
 
 hipError_t launch_prefill_rope_kv(const PfAttnArgs& a, hipStream_t s) {
     if (a.T <= 0 || a.q_split < 1 || a.k_split < 1 || a.v_split < 1) return hipErrorInvalidValue;
