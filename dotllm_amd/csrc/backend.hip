@@ -839,7 +839,7 @@ struct llmdot_hip_model {
     std::deque<Weight> views;          // Q, K and V row ranges of fused attn_qkv tensors
     // activations
     float *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
-    // h packed for its next RmsNorm consumer: xn = w * h, xssq[i] = sum of h^2 over h[8i .. 8i+7]
+    // h packed for its next RmsNorm consumer: xn = w * h, xssq[i] = sum of h^2 over h[4i .. 4i+3]
     float *xn = nullptr, *xssq = nullptr;
     // KV cache [layer][kv_head][context][head_dim]
     uint8_t *kcache = nullptr, *vcache = nullptr;
@@ -1421,7 +1421,7 @@ extern "C" int32_t llmdot_hip_model_create(llmdot_hip_ctx* ctx, const llmdot_hip
     if ((rc = A(sizeof(float) * qdim, &p))) return bail(rc); m->attn = (float*)p;
     if ((rc = A(sizeof(float) * d.ffn, &p))) return bail(rc); m->act = (float*)p;
     if ((rc = A(sizeof(float) * d.hidden, &p))) return bail(rc); m->xn = (float*)p;
-    if ((rc = A(sizeof(float) * (d.hidden / 8), &p))) return bail(rc); m->xssq = (float*)p;
+    if ((rc = A(sizeof(float) * (d.hidden / 4), &p))) return bail(rc); m->xssq = (float*)p;
     if ((rc = A(sizeof(float) * d.vocab, &p))) return bail(rc); m->logits = (float*)p;
     const size_t elt = d.kv_fp16 ? 2 : 4;
     m->kv_layer_bytes = (size_t)d.kv_heads * d.context * d.head_dim * elt;

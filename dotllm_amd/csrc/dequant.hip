@@ -145,20 +145,20 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
     if (w) {   // uniform
         if (i < hidden) packed[i] = w[i] * h;
         float q = h * h;
-        q = sum8(q);
-        if ((i & 7) == 0 && i < hidden) ssq[i >> 3] = q;
+        q = sum4(q);
+        if ((i & 3) == 0 && i < hidden) ssq[i >> 2] = q;
     }
 }
 
-// One thread per element; lanes 8k..8k+7 reduce their squares for ssq[k].
+// One thread per element; lanes 4k..4k+3 reduce their squares for ssq[k].
 __global__ __launch_bounds__(256) void pack_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                         float* __restrict__ packed, float* __restrict__ ssq) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     const float h = i < n ? x[i] : 0.f;
     if (i < n) packed[i] = w[i] * h;   // RmsNorm's vector lanes compute (w * x) * inv
     float q = h * h;
-    q = sum8(q);
-    if ((i & 7) == 0 && i < n) ssq[i >> 3] = q;
+    q = sum4(q);
+    if ((i & 3) == 0 && i < n) ssq[i >> 2] = q;
 }
 
 hipError_t launch_pack_norm(const float* x, const float* w, int n, float* packed, float* ssq, hipStream_t s) {

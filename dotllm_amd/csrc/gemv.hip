@@ -757,7 +757,8 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
     // Output rows in slabs of SLAB: slab j of this workgroup is rows
     // (j * wgs + blk) * SLAB ..., so at any moment the workgroups of a
     // segment stream through one contiguous stretch of each matrix.  The ADD
-    // epilogue packs rows in aligned 8s.
+    // epilogue packs rows in aligned 4s (slabs of 8 where the workgroup's rows
+    // allow, else of its 4).
     constexpr int SLAB = EPI == EPI_ADD ? (ROWS_WG % 8 == 0 ? 8 : ROWS_WG) : OPB;
     auto out_row = [&](int o) { return ((o / SLAB) * seg.wgs + blk) * SLAB + o % SLAB; };
     const int K = a.cols;
@@ -784,13 +785,15 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         return base + (int64_t)(r < seg.rows ? r : 0) * rbytes;
     };
 
-    // RmsNorm: the producer's sums of h^2 over 8-element groups, K/8 <= 4 per
-    // thread (threads >= K/32), issued first and summed after the rows
-    float sq[4];
+    // RmsNorm: the producer's sums of h^2 over 4-element groups, two per
+    // 8-element group (K/8 <= 4 groups per thread, threads >= K/32), issued
+    // first and summed after the rows
+    float2 sq[4];
     if (NORM) {
         const int nq = K >> 3;
 #pragma unroll
-        for (int k = 0; k < 4; k++) sq[k] = a.ssq[min((int)threadIdx.x + k * (int)blockDim.x, nq - 1)];
+        for (int k = 0; k < 4; k++)
+            sq[k] = reinterpret_cast<const float2*>(a.ssq)[min((int)threadIdx.x + k * (int)blockDim.x, nq - 1)];
     }
     // ADD: the residual and norm weight of this lane's output row, loaded
     // before the rows so the epilogue does not wait on them; unconditional
@@ -809,7 +812,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
         const int nq = K >> 3;
         float hsq = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) hsq += (int)threadIdx.x + k * (int)blockDim.x < nq ? sq[k] : 0.f;
+        for (int k = 0; k < 4; k++) hsq += (int)threadIdx.x + k * (int)blockDim.x < nq ? sq[k].x + sq[k].y : 0.f;
         const float w = wave_sum(hsq);
         if (lane == 0) ssq[wave] = w;   // over every wave: each entry of a.ssq is read by one thread
     }
@@ -842,14 +845,14 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(GemvArgs a) {
             hn = res + total(b * RB + k);   // residual: a[i] + b[i]
             seg.out[row] = hn;
         }
-        if (a.pack_out) {   // the updated vector packed for its RmsNorm consumer (rows come in 8s)
+        if (a.pack_out) {   // the updated vector packed for its RmsNorm consumer (rows come in 4s)
             if (valid) {
 #pragma clang fp contract(off)
                 a.pack_out[row] = pw * hn;
             }
             float q = hn * hn;
-            q = sum8(q);
-            if (valid && (t & 7) == 0) a.pack_ssq[row >> 3] = q;
+            q = sum4(q);
+            if (valid && (t & 3) == 0) a.pack_ssq[row >> 2] = q;
         }
     } else if (EPI == EPI_SWIGLU) {
         if (valid) {
@@ -989,8 +992,15 @@ int gemv_plan(uint32_t type, int epi, int rows_total, int cols) {
     if (epi == EPI_SWIGLU && rows_total % (7 * opb) == 0 && (rows_total / (7 * opb)) % 256 == 0) return 7;
     int nb = 8;
     while (nb > 1 && ((rows_total + nb * opb - 1) / (nb * opb)) * nw < target_waves(nw)) nb /= 2;
-    // the ADD epilogue packs rows in groups of 8
-    while (epi == EPI_ADD && nb < 8 && (nb * opb) % 8) nb *= 2;
+    // the ADD epilogue packs rows in groups of 4 and prefers slabs of 8; but
+    // where 8-row slabs leave a fraction of a workgroup per CU (some CUs two,
+    // others one) and 4-row workgroups fill the CUs evenly, it takes 4 rows
+    // (Phi-3-mini's 3072-row O and down projections: 768 workgroups, not 384)
+    if (epi == EPI_ADD) {
+        auto wgs = [&](int n) { return (rows_total + n * opb - 1) / (n * opb); };
+        while (nb < 8 && (nb * opb) % 8) nb *= 2;
+        if (nb > 1 && wgs(nb) % 256 && ((nb / 2) * opb) % 4 == 0 && wgs(nb / 2) % 256 == 0) nb /= 2;
+    }
     return nb;
 }
 
@@ -1050,7 +1060,10 @@ hipError_t launch_gemv(uint32_t type, int epi, GemvArgs& a, hipStream_t s) {
         if (a.seg[i].rows < 0) return hipErrorInvalidValue;
         rows_total += a.seg[i].rows;
     }
-    const int nb = gemv_plan(type, epi, rows_total, a.cols);
+    // Q4_K + Q6_K Q/K/V launches: one batch per workgroup (4 rows; the 7B
+    // shape's 1536 workgroups measured 0.2% faster than 896 of 8 rows, while
+    // the Q8_0 + Q6_K mix lost 3% that way)
+    const int nb = t2 != type && type == GGML_Q4_K ? 1 : gemv_plan(type, epi, rows_total, a.cols);
     const int rwg1 = gemv_rows_per_wg(type, epi, nb);
     const int hv = gemv_halves(type, epi, a.cols, t2 != type, (rows_total + rwg1 - 1) / rwg1);
     const int rwg = hv * rwg1;

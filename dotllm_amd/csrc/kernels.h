@@ -16,8 +16,9 @@ hipError_t launch_dequant(const uint8_t* src, float* dst, uint32_t type, int num
 // w non-null also packs out for its RmsNorm consumer (see launch_pack_norm).
 hipError_t launch_embed(const uint8_t* table, uint32_t type, int hidden, const int32_t* token_dev,
                         float* out, const float* w, float* packed, float* ssq, hipStream_t s);
-// Packs x for an RmsNorm consumer: packed[i] = w[i] * x[i], ssq[i/8] = sum of x^2
-// over 8 consecutive elements (n a multiple of 8).
+// Packs x for an RmsNorm consumer: packed[i] = w[i] * x[i], ssq[i/4] = sum of x^2
+// over 4 consecutive elements (n a multiple of 8).  The consumer adds the two
+// sums of each 8-element group, ssq[2j] + ssq[2j+1].
 hipError_t launch_pack_norm(const float* x, const float* w, int n, float* packed, float* ssq, hipStream_t s);
 
 // ---- gemv.hip ----
@@ -53,11 +54,11 @@ struct GemvArgs {
     int nseg;
     int cols;             // reduction length K
     const float* x;       // fp32 input; with norm != 0 it is already w * h (RmsNorm weights applied)
-    const float* ssq;     // norm != 0: sums of h^2 over consecutive 8-element groups, K/8 of them
+    const float* ssq;     // norm != 0: sums of h^2 over consecutive 4-element groups, K/4 of them
     int norm;             // RmsNorm of the input: row sums are scaled by 1/sqrt(sum(h^2)/K + eps)
     float eps;
     // EPI_ADD: also pack the updated vector for its RmsNorm consumer:
-    // pack_out[i] = pack_w[i] * out[i] and pack_ssq[i/8] = sum of out^2 over 8 rows
+    // pack_out[i] = pack_w[i] * out[i] and pack_ssq[i/4] = sum of out^2 over 4 rows
     const float* pack_w;
     float* pack_out;
     float* pack_ssq;
