@@ -1864,10 +1864,10 @@ extern "C" int32_t llmdot_hip_model_time_decode(llmdot_hip_model* m, int32_t fir
     out->gemv_launches = launches;
     if (per_kernel && !m->L.empty()) {
         const LayerW& w = m->L[0];
-        // weights + the packed RmsNorm input (w*h, one sum of squares per 8
+        // weights + the packed RmsNorm input (w*h, one sum of squares per 4
         // elements) + the SwiGLU output
         out->gemv_bytes = (double)launches * ((double)w.gate->nbytes + (double)w.up->nbytes +
-                                              4.0 * (m->d.hidden + m->d.hidden / 8.0 + (double)m->d.ffn));
+                                              4.0 * (m->d.hidden + m->d.hidden / 4.0 + (double)m->d.ffn));
     }
     return 0;
 }
