@@ -1196,8 +1196,9 @@ int enqueue_prefill_chunk(llmdot_hip_model* m, int T, int pos0) {
     for (int l = 0; l < d.layers; l++) {
         const LayerW& w = m->L[l];
         HIPCHK(launch_prefill_planes(m->pf_h, T, d.hidden, w.attn_norm_f, d.eps, pl, s));
-        // Q, K and V read the same planes and write separate buffers: K and V
-        // run on the side streams beside Q (K and V alone fill half the CUs)
+        // Q, K and V read the same planes and write separate buffers: V runs
+        // on a side stream beside Q and K (one launch where qk_pair allows,
+        // else K on the other side stream; K and V alone fill half the CUs)
         llmdot_hip_ctx* c = m->ctx;
         int nq = 1, nk = 1, nv = 1;
         HIPCHK(hipEventRecord(c->fork, s));
